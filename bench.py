@@ -1,0 +1,197 @@
+"""Benchmark of the MI355X verify-and-sample path.
+
+Default workload (C2): fused greedy verify, B=64, k=2,
+V=49152, bf16 logits, one launch per step. Every step reads a different one of
+NSETS input sets (together larger than the 256 MB Infinity Cache) that are
+already resident in HBM. Steps are submitted through one captured HIP graph of
+NSETS launches replayed K/NSETS times; the timed region is bracketed by HIP
+events on the stream the kernels run on, with device synchronisation on both
+sides. Prints one JSON line.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth, GB/s
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return platform.processor() or "unknown"
+
+
+# ---------------------------------------------------------------------------
+# C2: fused greedy verify
+# ---------------------------------------------------------------------------
+
+def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    from loopspec_amd import verify, workloads
+
+    cfg = workloads.C2
+    _log(f"generating {nsets} input sets for {cfg.name}")
+    sets = [workloads.greedy_inputs(cfg, seed=1000 + i, device=device) for i in range(nsets)]
+    ws = torch.zeros(verify.greedy_verify_workspace_bytes(cfg.batch, cfg.k, cfg.vocab), dtype=torch.uint8, device=device)
+    acc = torch.empty((nsets, cfg.batch), dtype=torch.int32, device=device)
+    tok = torch.empty((nsets, cfg.batch, cfg.k + 1), dtype=torch.int64, device=device)
+
+    def step(i: int) -> None:
+        t, d = sets[i]
+        verify.greedy_verify(t, d, accept_len=acc[i], tokens=tok[i], workspace=ws)
+
+    for i in range(nsets):  # eager warm-up (and lazy library load) before capture
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(nsets):
+            step(i)
+    replays = max(1, -(-steps // nsets))
+    wreplays = max(1, -(-warmup // nsets))
+    for _ in range(wreplays):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    timed_steps = replays * nsets
+    ms_per_step = ms / timed_steps
+    accepted = acc.sum().item() / nsets  # accepted drafts per step
+    tokens_per_step = accepted + cfg.batch  # + one correction/bonus token per row
+    nbytes = workloads.greedy_algorithmic_bytes(cfg)
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": "verify+sample rows/s (C2 greedy, vocab 49152, B=64, k=2)",
+        "value": cfg.batch / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "steps": timed_steps,
+        "warmup": wreplays * nsets,
+        "ms_per_step": ms_per_step,
+        "dtype": "bf16",
+        "config": {
+            "workload": cfg.name,
+            "batch": cfg.batch,
+            "k": cfg.k,
+            "vocab": cfg.vocab,
+            "input_sets": nsets,
+            "input_set_bytes": nbytes,
+            "kernel": "ls::greedy_kernel<BF16,true>",
+            "submission": "hipGraph of one launch per step",
+        },
+        "tokens_per_s": tokens_per_step / (ms_per_step * 1e-3),
+        "acceptance_rate": accepted / (cfg.batch * cfg.k),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+    }
+
+
+def cpu_baseline_greedy(max_seconds: float = 20.0) -> dict:
+    """Reference torch-CPU greedy path (oracle.torch_ref) on a bounded C2 sample.
+
+    Times torch.argmax over each step's B*(2k+1) endpoint rows plus the per-row
+    resolve, exactly as the reference's policy does it, on the host cores.
+    """
+    from loopspec_amd import workloads
+    from oracle import torch_ref
+
+    cfg = workloads.C2
+    target, draft = workloads.greedy_inputs(cfg, seed=7, device="cpu")
+    threads = len(os.sched_getaffinity(0))
+    results = {}
+    for nthreads in (threads, 1):
+        torch.set_num_threads(nthreads)
+        budget = max_seconds / 2
+        done_rows = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            for b in range(cfg.batch):
+                torch_ref.greedy_verify_step(target[b], draft[b])
+            done_rows += cfg.batch
+        results[nthreads] = done_rows / (time.perf_counter() - t0)
+    torch.set_num_threads(threads)
+    return {
+        "value": results[threads],
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"C2 shape (B=64,k=2,V=49152,bf16) batches for ~{max_seconds / 2:.0f}s per thread setting; "
+                  "torch-CPU restatement of decisions.py argmax+resolve",
+        "value_1_thread": results[1],
+        "torch_threads": threads,
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model(),
+        "torch_version": torch.__version__,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--sets", type=int, default=10, help="distinct input sets rotated through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(rows are independent; see DESIGN.md for how the batch would shard).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        return 1
+    device = torch.device("cuda", 0)
+    from loopspec_amd import _lib
+
+    _lib.load()
+    if args.config != "C2":
+        print(f"unknown config {args.config}", file=sys.stderr)
+        return 2
+    result = bench_greedy(args.steps, args.warmup, device, args.sets)
+    result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                   "data": "synthetic (seeded N(0,3^2) logits, draft = target + N(0,1), 1% planted ties)"})
+    if not args.no_cpu_baseline:
+        _log("timing CPU baseline")
+        result["cpu_baseline"] = cpu_baseline_greedy()
+    order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+             "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"]
+    line = {k: result[k] for k in order if k in result}
+    line.update({k: v for k, v in result.items() if k not in line})
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

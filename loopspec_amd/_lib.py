@@ -1,0 +1,136 @@
+"""ctypes binding of libloopspec_hip.so (the C-ABI in include/loopspec_hip.h).
+
+Only raw device pointers, element strides, sizes and the current HIP stream
+cross the boundary. Status codes map to the exception types the reference
+raises for the same conditions: LS_ERR_VALUE -> ValueError (shape/workspace
+mismatch, sglang_recurrent/loopspec/sampling/sampler.py:525-526), everything
+else -> RuntimeError. There is no CPU fallback: if the library is missing the
+import-time loader raises, so a GPU run can never silently use another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libloopspec_hip.so"
+
+LS_OK, LS_ERR_VALUE, LS_ERR_RUNTIME, LS_ERR_HIP = 0, 1, 2, 3
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_U64 = ctypes.c_uint64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+_F64 = ctypes.c_double
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "ls_abi_version": (_I32, []),
+    "ls_last_error": (ctypes.c_char_p, []),
+    "ls_set_option": (_I32, [ctypes.c_char_p, _I64]),
+    "ls_argmax_rows": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _U64, _P]),
+    "ls_argmax_rows_workspace": (_U64, [_I64, _I64]),
+    "ls_greedy_verify": (
+        _I32,
+        [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _P],
+    ),
+    "ls_greedy_verify_workspace": (_U64, [_I64, _I64, _I64]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m loopspec_amd.build` "
+                "(or __graft_entry__.build()) before using loopspec_amd"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raise the exception matching a non-zero C-ABI status."""
+    if status == LS_OK:
+        return
+    msg = load().ls_last_error().decode(errors="replace")
+    if status == LS_ERR_VALUE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> None:
+    """Invoke a status-returning entry point and raise on failure."""
+    check(getattr(load(), name)(*args))
+
+
+def query(name: str, *args) -> int:
+    """Invoke a size/version query that returns a plain integer."""
+    return int(getattr(load(), name)(*args))
+
+
+def set_option(name: str, value: int) -> None:
+    call("ls_set_option", name.encode(), int(value))
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_cuda(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"LoopSpec {what} requires CUDA (HIP) tensors")
+
+
+class Workspace:
+    """Zero-filled device scratch reused across calls on one device.
+
+    The kernels leave their scratch zeroed when they finish, so one buffer can
+    back every later call that is ordered on the same stream. The buffer only
+    grows; growth allocates a fresh zeroed tensor (outside any graph capture).
+    """
+
+    def __init__(self) -> None:
+        self._buffers: dict[tuple[int, str], torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int, tag: str = "default") -> torch.Tensor:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        key = (index, tag)
+        buf = self._buffers.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=torch.device("cuda", index))
+            self._buffers[key] = buf
+        return buf
+
+
+WORKSPACE = Workspace()

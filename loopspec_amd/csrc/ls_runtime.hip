@@ -1,0 +1,82 @@
+// Host runtime of the C-ABI: error reporting, device attributes, options.
+#include "ls_runtime.hpp"
+
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+namespace ls {
+
+namespace {
+thread_local std::string g_last_error;
+
+std::mutex g_mu;
+std::map<std::string, int64_t>& options_map() {
+  static std::map<std::string, int64_t> m = {
+      {"greedy_splits", 0},   // workgroups per row in the greedy kernels
+      {"greedy_block", 0},    // unused placeholder kept for sweeps
+      {"sample_splits", 0},   // chunk workgroups per row in dense sampling
+      {"spec_block", 0},      // threads per row in the fused sampling verify
+  };
+  return m;
+}
+
+int g_cu_count[64] = {0};
+}  // namespace
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int ok() { return LS_OK; }
+
+int hip_fail(hipError_t err, const char* what) {
+  return fail(LS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, what);
+  return LS_OK;
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_cu_count[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_cu_count[dev] = n;
+  }
+  return g_cu_count[dev];
+}
+
+int64_t option(const char* name) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto& m = options_map();
+  auto it = m.find(name);
+  return it == m.end() ? 0 : it->second;
+}
+
+}  // namespace ls
+
+extern "C" {
+
+int ls_abi_version(void) { return 1; }
+
+const char* ls_last_error(void) { return ls::g_last_error.c_str(); }
+
+int ls_set_option(const char* name, int64_t value) {
+  if (name == nullptr) return ls::fail(LS_ERR_VALUE, "option name is NULL");
+  std::lock_guard<std::mutex> lk(ls::g_mu);
+  auto& m = ls::options_map();
+  auto it = m.find(name);
+  if (it == m.end()) return ls::fail(LS_ERR_VALUE, std::string("unknown option: ") + name);
+  if (value < 0) return ls::fail(LS_ERR_VALUE, std::string("option must be >= 0: ") + name);
+  it->second = value;
+  return LS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,42 @@
+// Host-side runtime helpers shared by the C-ABI entry points: status codes,
+// the thread-local error message, device properties and tuning options.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/loopspec_hip.h"
+
+namespace ls {
+
+// Record an error message for ls_last_error() and return `code`.
+int fail(int code, const std::string& msg);
+int ok();
+
+// Map a failed HIP call to LS_ERR_HIP with the runtime's message.
+int hip_fail(hipError_t err, const char* what);
+
+// Launch-error check after a kernel launch.
+int check_launch(const char* what);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// Tuning knobs settable through ls_set_option(); 0 means "use the heuristic".
+int64_t option(const char* name);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int dtype_bytes(int dtype) {
+  return dtype == LS_DTYPE_F32 ? 4 : (dtype == LS_DTYPE_BF16 || dtype == LS_DTYPE_F16) ? 2 : 0;
+}
+
+}  // namespace ls
+
+#define LS_HIP_CHECK(expr)                                   \
+  do {                                                       \
+    hipError_t _e = (expr);                                  \
+    if (_e != hipSuccess) return ::ls::hip_fail(_e, #expr);  \
+  } while (0)

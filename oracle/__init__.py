@@ -1,0 +1,24 @@
+"""CPU oracle for the LoopSpec verify-and-sample path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the algorithm of the reference's hot path
+(sglang_recurrent/loopspec/{decisions,pipeline,graph_ops}.py and
+sglang_recurrent/loopspec/sampling/*.py). It is the checker the HIP kernels are
+compared against and the timed CPU baseline. Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it; the product package ``loopspec_amd`` never does.
+
+Modules:
+- ``greedy``:   argmax and greedy chain verification (exact; numpy).
+- ``numerics``: the declared arithmetic shared by oracle and kernels (fp32 FMA
+                emulation, the EXP function, 2^-46 fixed-point masses).
+- ``sampling``: softmax, top-p cutoff, categorical CDF sampling, speculative
+                verification, residuals (declared arithmetic; numpy).
+- ``graph_ops``: KV slot allocation, request-mapping update, state-row copy
+                and the paged KV commit (integer; numpy).
+- ``torch_ref``: literal torch-CPU restatements of the reference's code
+                (sort/cumsum/searchsorted, torch.softmax, ...), used to pin the
+                declared arithmetic against the reference's own formulation and
+                as the CPU baseline.
+
+Parity status of each function is stated in its docstring ("pinned by: ...").
+"""
