@@ -16,6 +16,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
+
 import torch
 
 
@@ -71,3 +73,80 @@ def greedy_algorithmic_bytes(cfg: GreedyConfig, with_draft_logits: bool = True) 
     rows = cfg.batch * (cfg.k + 1) + (cfg.batch * cfg.k if with_draft_logits else 0)
     out = cfg.batch * 4 + cfg.batch * (cfg.k + 1) * 8
     return rows * cfg.vocab * elem + out
+
+
+@dataclass(frozen=True)
+class SamplingConfig:
+    name: str
+    batch: int
+    k: int
+    vocab: int
+    dtype: torch.dtype
+    temperature: float
+    top_p: float
+    penalty: float = 1.0
+    target_std: float = 3.0
+    noise_std: float = 1.0
+    hist_min: int = 0
+    hist_max: int = 0
+    zipf_s: float = 1.1
+
+
+C3 = SamplingConfig("C3-spec-b64-k2-v49152-fp32-t1.0-p0.7", 64, 2, 49152, torch.float32, 1.0, 0.7)
+C4 = SamplingConfig("C4-spec-b32-k4-v128256-bf16-t0.7-p0.9-rep1.1", 32, 4, 128256, torch.bfloat16, 0.7, 0.9,
+                    penalty=1.1, target_std=4.0, hist_min=256, hist_max=4096)
+C5_SAMPLING = SamplingConfig("C5-spec-b128-k2-v49152-fp32-t1.0-p0.7", 128, 2, 49152, torch.float32, 1.0, 0.7)
+
+
+def zipf_ids(n: int, vocab: int, s: float, rng: np.random.Generator) -> np.ndarray:
+    """Token ids with P(id = i) proportional to (i + 1)^-s over the whole vocabulary."""
+    weights = np.arange(1, vocab + 1, dtype=np.float64) ** -s
+    cdf = np.cumsum(weights)
+    cdf /= cdf[-1]
+    return np.minimum(np.searchsorted(cdf, rng.random(n), side="right"), vocab - 1).astype(np.int32)
+
+
+def sampling_inputs(cfg: SamplingConfig, seed: int, device: torch.device | str = "cpu") -> dict:
+    """Seeded logits, Philox uniforms and token histories for a sampling config.
+
+    Returns a dict with
+      target  [B, k+1, V] cfg.dtype,  final logits ~ N(0, target_std^2)
+      draft   [B, k, V]   cfg.dtype,  target[:, :k] + N(0, noise_std^2)
+      uniforms       float32 [B, 2k+1]  verify draws (acceptance, residual, bonus)
+      draft_uniforms float32 [B, k]     draws used to sample the draft tokens from q
+      history int32 [B, hist_max] (padded with 0) and history_len int32 [B]
+    The draft tokens themselves are sampled from q by the caller.
+    """
+    from . import philox
+
+    device = torch.device(device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    b, k, v = cfg.batch, cfg.k, cfg.vocab
+    target = torch.randn((b, k + 1, v), generator=g, device=device) * cfg.target_std
+    draft = target[:, :k] + torch.randn((b, k, v), generator=g, device=device) * cfg.noise_std
+    out = {
+        "target": target.to(cfg.dtype).contiguous(),
+        "draft": draft.to(cfg.dtype).contiguous(),
+        "uniforms": torch.from_numpy(philox.uniforms((b, 2 * k + 1), seed=2 * seed + 1)).to(device),
+        "draft_uniforms": torch.from_numpy(philox.uniforms((b, k), seed=2 * seed + 2)).to(device),
+    }
+    hist_max = cfg.hist_max
+    hist = np.zeros((b, max(hist_max, 1)), dtype=np.int32)
+    lens = np.zeros(b, dtype=np.int32)
+    if hist_max > 0:
+        rng = np.random.default_rng(seed)
+        for r in range(b):
+            n = int(rng.integers(cfg.hist_min, cfg.hist_max + 1))
+            lens[r] = n
+            hist[r, :n] = zipf_ids(n, v, cfg.zipf_s, rng)
+    out["history"] = torch.from_numpy(hist).to(device)
+    out["history_len"] = torch.from_numpy(lens).to(device)
+    return out
+
+
+def sampling_algorithmic_bytes(cfg: SamplingConfig, history_bytes: int = 0) -> int:
+    """Every logit read once, plus the uniforms, draft ids, histories and outputs."""
+    elem = torch.tensor([], dtype=cfg.dtype).element_size()
+    rows = cfg.batch * (2 * cfg.k + 1)
+    small = cfg.batch * (2 * cfg.k + 1) * 4 + cfg.batch * cfg.k * 8 + cfg.batch * 4 + cfg.batch * (cfg.k + 1) * 8
+    return rows * cfg.vocab * elem + small + history_bytes
