@@ -117,6 +117,93 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
     }
 
 
+# ---------------------------------------------------------------------------
+# C3 / C4: fused lossless speculative verify
+# ---------------------------------------------------------------------------
+
+def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    """One launch per step of ls_spec_verify on rotating resident input sets.
+
+    Draft tokens are sampled on the GPU from the filtered draft distributions
+    (ls_sample_logits with each set's draft uniforms) before timing.
+    """
+    from loopspec_amd import verify, workloads
+
+    _log(f"generating {nsets} input sets for {cfg.name}")
+    sets = []
+    for i in range(nsets):
+        inp = workloads.sampling_inputs(cfg, seed=2000 + i, device=device)
+        flat = inp["draft"].reshape(cfg.batch * cfg.k, cfg.vocab)
+        hist = inp["history"] if cfg.penalty != 1.0 else None
+        hl = inp["history_len"] if cfg.penalty != 1.0 else None
+        if hist is not None:
+            hist = hist.repeat_interleave(cfg.k, dim=0).contiguous()
+            hl = hl.repeat_interleave(cfg.k).contiguous()
+        drafts = verify.sample_logits(flat, inp["draft_uniforms"].reshape(-1).contiguous(), cfg.temperature,
+                                      cfg.top_p, penalty=cfg.penalty, history=hist, history_len=hl)
+        inp["draft_tokens"] = drafts.reshape(cfg.batch, cfg.k)
+        sets.append(inp)
+    ws = torch.zeros(verify.spec_verify_workspace_bytes(cfg.batch, cfg.k, cfg.vocab), dtype=torch.uint8,
+                     device=device)
+    acc = torch.empty((nsets, cfg.batch), dtype=torch.int32, device=device)
+    tok = torch.empty((nsets, cfg.batch, cfg.k + 1), dtype=torch.int64, device=device)
+
+    def step(i: int) -> None:
+        s = sets[i]
+        verify.speculative_verify(
+            s["target"], s["draft"], s["draft_tokens"], s["uniforms"], cfg.temperature, cfg.top_p,
+            penalty=cfg.penalty, history=s["history"] if cfg.penalty != 1.0 else None,
+            history_len=s["history_len"] if cfg.penalty != 1.0 else None,
+            accept_len=acc[i], tokens=tok[i], workspace=ws)
+
+    ms_per_step, timed, wsteps = _time_graph(step, nsets, steps, warmup)
+    hist_bytes = int(sets[0]["history_len"].sum().item()) * 4 if cfg.penalty != 1.0 else 0
+    nbytes = workloads.sampling_algorithmic_bytes(cfg, hist_bytes)
+    accepted = acc.sum().item() / nsets
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": f"verify+sample rows/s ({cfg.name})",
+        "value": cfg.batch / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "steps": timed,
+        "warmup": wsteps,
+        "ms_per_step": ms_per_step,
+        "dtype": {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[cfg.dtype],
+        "config": {"workload": cfg.name, "batch": cfg.batch, "k": cfg.k, "vocab": cfg.vocab,
+                   "temperature": cfg.temperature, "top_p": cfg.top_p, "penalty": cfg.penalty,
+                   "input_sets": nsets, "input_set_bytes": nbytes,
+                   "kernel": "ls::sample_rows_kernel<spec>", "submission": "hipGraph of one launch per step"},
+        "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
+        "acceptance_rate": accepted / (cfg.batch * cfg.k),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
+def _time_graph(step, nsets: int, steps: int, warmup: int):
+    """Capture one graph of nsets steps, replay it; return (ms/step, steps, warmup steps)."""
+    for i in range(nsets):
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(nsets):
+            step(i)
+    replays = max(1, -(-steps // nsets))
+    wreplays = max(1, -(-warmup // nsets))
+    for _ in range(wreplays):
+        graph.replay()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * nsets), replays * nsets, wreplays * nsets
+
+
 def cpu_baseline_greedy(max_seconds: float = 20.0) -> dict:
     """Reference torch-CPU greedy path (oracle.torch_ref) on a bounded C2 sample.
 
@@ -176,10 +263,17 @@ def main() -> int:
     from loopspec_amd import _lib
 
     _lib.load()
-    if args.config != "C2":
+    from loopspec_amd import workloads
+
+    if args.config == "C2":
+        result = bench_greedy(args.steps, args.warmup, device, args.sets)
+    elif args.config in ("C3", "C4"):
+        cfg = workloads.C3 if args.config == "C3" else workloads.C4
+        result = bench_spec(cfg, args.steps, args.warmup, device, args.sets)
+        args.no_cpu_baseline = True
+    else:
         print(f"unknown config {args.config}", file=sys.stderr)
         return 2
-    result = bench_greedy(args.steps, args.warmup, device, args.sets)
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                    "data": "synthetic (seeded N(0,3^2) logits, draft = target + N(0,1), 1% planted ties)"})
     if not args.no_cpu_baseline:

@@ -10,9 +10,12 @@
  *   - `stream` is a hipStream_t passed as an opaque pointer (NULL = default stream).
  *     Work is only enqueued; no entry point synchronises the device or allocates
  *     device memory. Scratch memory comes from the caller's `workspace`, which must
- *     be zero-filled once when it is allocated; kernels leave it zeroed again, so
- *     a workspace can be reused by later calls on the same stream (and inside a
- *     captured graph). Calls that share a workspace must be stream-ordered.
+ *     be zero-filled once when it is allocated. Every kernel leaves the words that
+ *     must start at zero (arrival counters, combine slots) zeroed again, so a
+ *     workspace can be reused by later calls of the SAME entry point on the same
+ *     stream (and inside a captured graph), whatever their shapes. Do not share one
+ *     workspace between different entry points. Calls that share a workspace must
+ *     be stream-ordered; concurrent calls on one workspace race.
  *   - Token ids, row ids and slot ids are int64 unless stated; KV mapping tables
  *     are int32, matching the reference's layout contracts
  *     (sglang_recurrent/loopspec/sampling/sampler.py:3-12,
@@ -86,6 +89,74 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride,
                      int64_t* row_argmax, void* workspace, uint64_t workspace_bytes,
                      ls_stream_t stream);
 uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
+
+/* ------------------------------------------------------------------------------
+ * (a) logit processing + (c) lossless speculative sampling
+ *
+ * Shared processing of a logits row (any of f32/bf16/f16, contiguous vocab,
+ * 16-byte aligned rows, vocab*elem_bytes a multiple of 16):
+ *   x = logits; for ids in the row's history (if penalty != 1):
+ *       x <- x < 0 ? x*penalty : x*RN(1/penalty);  then x <- x*RN(1/T) (T != 1);
+ *   p = softmax(x) in the library's declared arithmetic (see DESIGN.md of the
+ *   repository: ls_exp, 2^-46 fixed-point masses);
+ *   top_p < 1: keep p >= c with c = max{v : sum_{p>=v} fx46(p) >= fx46(top_p)}
+ *   (ties kept; the whole row if no v qualifies), renormalise by the retained
+ *   mass -- the value semantics of sort + cumsum + searchsorted(right=False)
+ *   + gather + where + sum of filtered_probabilities
+ *   (sglang_recurrent/loopspec/sampling/distributions.py:14-86).
+ *   top_k must be 0 or >= vocab (top-k filtering is not offered here).
+ * ------------------------------------------------------------------------------ */
+
+/* Fused chain verify, one launch for B batch elements of k draft positions:
+ * filters every target row [B, k+1, V] (P_i) and draft row [B, k, V] (Q_i);
+ * position i accepts draft_tokens[b, i] iff u[b,i] < min(1, P_i[x]/Q_i[x])
+ * (sglang_recurrent/loopspec/sampling/sampler.py:428-460); the first rejection
+ * at i emits a draw from normalize(max(P_i - Q_i, 0)) (falling back to P_i at
+ * zero mass, sglang_recurrent/loopspec/sampling/rejection.py:60-69) with
+ * u[b, k+i]; if all k accept, a bonus draw from P_k with u[b, 2k]
+ * (direct final sample, sglang_recurrent/loopspec/sampling/policy.py:156-165).
+ * Draws are inverse-CDF over token index (sampler.py:22-102).
+ *   uniforms: float32 [B, 2k+1] contiguous; draft_tokens: int64 [B, k].
+ *   history: int32 rows of token ids (row stride history_stride), lengths
+ *            history_len[B]; used only when penalty != 1.
+ *   accept_len: int32 [B]; tokens: int64 [B, k+1] (emitted tokens, -1 padded).
+ * Replaces SamplingDecisionPolicy.queue/read for q1 verification
+ * (sglang_recurrent/loopspec/sampling/policy.py:220-283) along the pipeline's
+ * accept prefix (sglang_recurrent/loopspec/pipeline.py:365-412). */
+int ls_spec_verify(const void* target_logits, int64_t target_batch_stride,
+                   int64_t target_pos_stride, const void* draft_logits,
+                   int64_t draft_batch_stride, int64_t draft_pos_stride,
+                   const int64_t* draft_tokens, const float* uniforms, int dtype,
+                   int64_t batch, int64_t k, int64_t vocab, float temperature, float top_p,
+                   int64_t top_k, float penalty, const int32_t* history,
+                   int64_t history_stride, const int32_t* history_len,
+                   int32_t* accept_len, int64_t* tokens, void* workspace,
+                   uint64_t workspace_bytes, ls_stream_t stream);
+uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
+
+/* Filter each logits row and draw one token per row with uniforms[row]
+ * (float32 [rows]) into out_tokens (int64 [rows]); history rows as above,
+ * one per logits row. Replaces prepare_sampling_probabilities followed by
+ * sample_probabilities / CategoricalSampler.sample
+ * (sglang_recurrent/loopspec/sampling/distributions.py:89-171). */
+int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows,
+                     int64_t vocab, float temperature, float top_p, int64_t top_k,
+                     float penalty, const int32_t* history, int64_t history_stride,
+                     const int32_t* history_len, const float* uniforms, int64_t* out_tokens,
+                     ls_stream_t stream);
+
+/* Dense filtering: probs_out (optional, [rows, V] float32, row stride
+ * probs_stride) receives p; filtered_out (optional) the filtered, renormalised
+ * distribution (p itself when top_p == 1); cutoff_out / mass_out (optional,
+ * float32 [rows]) the cutoff value and binary32 retained mass. top_p_rows
+ * (optional, float32 [rows]) overrides top_p per row when top_p < 1.
+ * Replaces filtered_probabilities and the probability/cutoff part of
+ * prepare_sampling_probabilities (distributions.py:14-149). */
+int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows,
+                     int64_t vocab, float temperature, float top_p, const float* top_p_rows,
+                     int64_t top_k, float* probs_out, int64_t probs_stride,
+                     float* filtered_out, int64_t filtered_stride, float* cutoff_out,
+                     float* mass_out, ls_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,130 @@
+// Declared arithmetic of the sampling path, device side.
+//
+// Every operation here is exactly reproducible: binary32 mul/add/div with
+// round-to-nearest-even, single-rounding fma (v_fma_f32), v_rndne_f32, exact
+// power-of-two scaling (v_ldexp_f32) and integer arithmetic. The library is
+// compiled with -ffp-contract=off, so no other fusion happens. The same
+// sequence of operations is restated on the CPU (oracle/numerics.py) and the
+// two agree bit for bit.
+//
+//  ls_exp(t)    Cody-Waite reduction k = rint(RN(t*log2e)), r = t - k*ln2 in two
+//               fmas, e^r by a degree-6 polynomial (Horner, fma), result
+//               P(r)*2^k; t < -87 (or NaN) gives 0. Within 2 ulp of exp.
+//  fx46(w)      floor(w * 2^46): masses of weights in [0, 1] as exact integers.
+//               Any summation order gives the same total.
+//  u64_to_f32   round-to-nearest-even of an exact mass; mass_to_f32 scales by
+//               2^-46 (exact).
+//  floor_u_times(u, T) = floor(u * T) exactly, for the inverse-CDF target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ls {
+
+constexpr float kLog2e = 1.44269504f;          // 0x3FB8AA3B
+constexpr float kLn2Hi = 0.693145752f;         // 0x3F317200, 16 significant bits
+constexpr float kLn2Lo = 1.42860677e-06f;      // ln 2 - kLn2Hi, rounded
+constexpr float kExpMin = -87.0f;
+constexpr float kExpC0 = 1.0f;
+constexpr float kExpC1 = 1.0f;
+constexpr float kExpC2 = 0x1.fffffcp-2f;
+constexpr float kExpC3 = 0x1.55540cp-3f;
+constexpr float kExpC4 = 0x1.55584p-5f;
+constexpr float kExpC5 = 0x1.126e3ap-7f;
+constexpr float kExpC6 = 0x1.6ae0eep-10f;
+// Upper bound of e^r over the reduced range |r| <= ln2/2 + 87 * 2^-24 * ln2.
+constexpr float kExpPolyMax = 1.4143f;
+constexpr int kFxBits = 46;
+constexpr double kFxOne = 70368744177664.0;  // 2^46
+
+// e = ls_exp(t); *k receives the binary exponent used for the scaling, or
+// kExpNoBucket when t < kExpMin (e == 0).
+constexpr int kExpNoBucket = -1000;
+__device__ __forceinline__ float ls_exp_k(float t, int* k) {
+  if (!(t >= kExpMin)) {
+    *k = kExpNoBucket;
+    return 0.0f;
+  }
+  const float kf = __builtin_rintf(t * kLog2e);
+  float r = __builtin_fmaf(kf, -kLn2Hi, t);
+  r = __builtin_fmaf(kf, -kLn2Lo, r);
+  float p = kExpC6;
+  p = __builtin_fmaf(p, r, kExpC5);
+  p = __builtin_fmaf(p, r, kExpC4);
+  p = __builtin_fmaf(p, r, kExpC3);
+  p = __builtin_fmaf(p, r, kExpC2);
+  p = __builtin_fmaf(p, r, kExpC1);
+  p = __builtin_fmaf(p, r, kExpC0);
+  const int ki = static_cast<int>(kf);
+  *k = ki;
+  return __builtin_ldexpf(p, ki);
+}
+
+__device__ __forceinline__ float ls_exp(float t) {
+  int k;
+  return ls_exp_k(t, &k);
+}
+
+// floor(w * 2^46) for w in [0, 1], as a double holding an exact integer.
+// Sums of fewer than 128 such terms stay exact in binary64.
+__device__ __forceinline__ double fx46_d(float w) {
+  return __builtin_trunc(static_cast<double>(w) * kFxOne);
+}
+__device__ __forceinline__ uint64_t fx46(float w) {
+  return static_cast<uint64_t>(fx46_d(w));
+}
+
+__device__ __forceinline__ float u64_to_f32(uint64_t x) {
+  if (x == 0) return 0.0f;
+  const int nb = 64 - __builtin_clzll(x);
+  if (nb <= 24) return static_cast<float>(static_cast<uint32_t>(x));
+  int shift = nb - 24;
+  uint64_t mant = x >> shift;
+  const uint64_t rem = x & ((1ull << shift) - 1ull);
+  const uint64_t half = 1ull << (shift - 1);
+  if (rem > half || (rem == half && (mant & 1ull))) {
+    ++mant;
+    if (mant == (1ull << 24)) {
+      mant >>= 1;
+      ++shift;
+    }
+  }
+  return __builtin_ldexpf(static_cast<float>(static_cast<uint32_t>(mant)), shift);
+}
+
+__device__ __forceinline__ float mass_to_f32(uint64_t mass_fx) {
+  return __builtin_ldexpf(u64_to_f32(mass_fx), -kFxBits);
+}
+
+// floor(u * total) exactly, for binary32 u in [0, 1).
+__device__ __forceinline__ uint64_t floor_u_times(float u, uint64_t total) {
+  if (!(u > 0.0f)) return 0;
+  const uint32_t b = __float_as_uint(u);
+  const int eb = static_cast<int>((b >> 23) & 0xffu);
+  uint64_t m = b & 0x7fffffu;
+  int shift;
+  if (eb == 0) {
+    shift = 149;
+  } else {
+    m |= 0x800000u;
+    shift = 150 - eb;  // >= 24 because u < 1
+  }
+  // 88-bit product m * total as (hi:lo).
+  const uint64_t lo_part = (total & 0xffffffffull) * m;  // < 2^56
+  const uint64_t hi_part = (total >> 32) * m;             // < 2^56
+  const uint64_t lo = lo_part + (hi_part << 32);
+  const uint64_t hi = (hi_part >> 32) + (lo < lo_part ? 1ull : 0ull);
+  if (shift >= 128) return 0;
+  if (shift >= 64) return hi >> (shift - 64);
+  return (lo >> shift) | (hi << (64 - shift));
+}
+
+// u < min(1, p / q) with a NaN ratio rejecting (the reference's strict test).
+__device__ __forceinline__ bool accept_draw(float u, float p, float q) {
+  const float ratio = p / q;
+  if (ratio != ratio) return false;
+  return u < (ratio < 1.0f ? ratio : 1.0f);
+}
+
+}  // namespace ls

@@ -108,3 +108,151 @@ def greedy_verify(
 
 def greedy_verify_workspace_bytes(batch: int, k: int, vocab: int) -> int:
     return _lib.query("ls_greedy_verify_workspace", batch, k, vocab)
+
+
+def _history_args(history: torch.Tensor | None, history_len: torch.Tensor | None, groups: int, dev):
+    if history is None:
+        return None, 0, None
+    _lib.require_cuda(history, "repetition penalty history")
+    if history.dtype != torch.int32 or history.dim() != 2 or history.stride(-1) != 1 or history.shape[0] < groups:
+        raise ValueError("history must be int32 [rows, L] with contiguous ids")
+    if history_len is None:
+        history_len = torch.full((history.shape[0],), history.shape[1], dtype=torch.int32, device=dev)
+    if history_len.dtype != torch.int32 or not history_len.is_contiguous() or history_len.shape[0] < groups:
+        raise ValueError("history_len must be contiguous int32 [rows]")
+    return history.data_ptr(), history.stride(0), history_len.data_ptr()
+
+
+def speculative_verify(
+    target_logits: torch.Tensor,
+    draft_logits: torch.Tensor,
+    draft_tokens: torch.Tensor,
+    uniforms: torch.Tensor,
+    temperature: float = 1.0,
+    top_p: float = 1.0,
+    *,
+    penalty: float = 1.0,
+    history: torch.Tensor | None = None,
+    history_len: torch.Tensor | None = None,
+    top_k: int = 0,
+    accept_len: torch.Tensor | None = None,
+    tokens: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Lossless speculative verification of a chain of k draft positions.
+
+    target_logits [B, k+1, V] and draft_logits [B, k, V] (same dtype), draft
+    tokens int64 [B, k] (sampled from the filtered draft distributions),
+    uniforms float32 [B, 2k+1]: u[:, i] accept position i, u[:, k+i] the residual
+    draw after a rejection at i, u[:, 2k] the bonus draw. Returns
+    (accept_len int32 [B], tokens int64 [B, k+1]); see ls_spec_verify.
+    """
+    _check_rows(target_logits, "speculative_verify")
+    _check_rows(draft_logits, "speculative_verify")
+    if target_logits.dim() != 3:
+        raise ValueError("target_logits must be [B, k+1, V]")
+    batch, kp1, vocab = target_logits.shape
+    k = kp1 - 1
+    dev = target_logits.device
+    if draft_logits.shape != (batch, k, vocab) or draft_logits.dtype != target_logits.dtype:
+        raise ValueError("draft_logits must be [B, k, V] with the target's dtype")
+    if draft_tokens.shape != (batch, k) or draft_tokens.dtype != torch.int64:
+        raise ValueError("draft_tokens must be int64 [B, k]")
+    if uniforms.shape != (batch, 2 * k + 1) or uniforms.dtype != torch.float32:
+        raise ValueError("uniforms must be float32 [B, 2k+1]")
+    draft_tokens = draft_tokens.contiguous()
+    uniforms = uniforms.contiguous()
+    if accept_len is None:
+        accept_len = torch.empty(batch, dtype=torch.int32, device=dev)
+    if tokens is None:
+        tokens = torch.empty((batch, kp1), dtype=torch.int64, device=dev)
+    h_ptr, h_stride, hl_ptr = _history_args(history, history_len, batch, dev) if penalty != 1.0 else (None, 0, None)
+    nbytes = _lib.query("ls_spec_verify_workspace", batch, k, vocab)
+    ws = workspace if workspace is not None else _lib.WORKSPACE.get(dev, nbytes, "spec")
+    _lib.call(
+        "ls_spec_verify",
+        target_logits.data_ptr(), target_logits.stride(0), target_logits.stride(1),
+        draft_logits.data_ptr(), draft_logits.stride(0), draft_logits.stride(1),
+        draft_tokens.data_ptr(), uniforms.data_ptr(), _lib.dtype_code(target_logits),
+        batch, k, vocab, float(temperature), float(top_p), int(top_k), float(penalty),
+        h_ptr, h_stride, hl_ptr, accept_len.data_ptr(), tokens.data_ptr(),
+        ws.data_ptr(), ws.numel(), _lib.stream(dev),
+    )
+    return accept_len, tokens
+
+
+def spec_verify_workspace_bytes(batch: int, k: int, vocab: int) -> int:
+    return _lib.query("ls_spec_verify_workspace", batch, k, vocab)
+
+
+def sample_logits(
+    logits: torch.Tensor,
+    uniforms: torch.Tensor,
+    temperature: float = 1.0,
+    top_p: float = 1.0,
+    *,
+    penalty: float = 1.0,
+    history: torch.Tensor | None = None,
+    history_len: torch.Tensor | None = None,
+    top_k: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Filter each row of logits [R, V] and draw one token per row (int64 [R])."""
+    _check_rows(logits, "sample_logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be [rows, vocab]")
+    rows, vocab = logits.shape
+    dev = logits.device
+    if uniforms.shape != (rows,) or uniforms.dtype != torch.float32:
+        raise ValueError("uniforms must be float32 [rows]")
+    uniforms = uniforms.contiguous()
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=dev)
+    h_ptr, h_stride, hl_ptr = _history_args(history, history_len, rows, dev) if penalty != 1.0 else (None, 0, None)
+    _lib.call(
+        "ls_sample_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
+        float(temperature), float(top_p), int(top_k), float(penalty), h_ptr, h_stride, hl_ptr,
+        uniforms.data_ptr(), out.data_ptr(), _lib.stream(dev),
+    )
+    return out
+
+
+def filter_logits(
+    logits: torch.Tensor,
+    temperature: float = 1.0,
+    top_p: float = 1.0,
+    *,
+    top_p_rows: torch.Tensor | None = None,
+    top_k: int = 0,
+    want_probs: bool = False,
+    want_filtered: bool = True,
+) -> dict[str, torch.Tensor]:
+    """Dense filtering of logits [R, V]; returns a dict with 'filtered' (new
+    float32 [R, V]), optionally 'probs' (unfiltered softmax), 'cutoff' and
+    'mass' (float32 [R])."""
+    _check_rows(logits, "filter_logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be [rows, vocab]")
+    rows, vocab = logits.shape
+    dev = logits.device
+    res: dict[str, torch.Tensor] = {
+        "cutoff": torch.empty(rows, dtype=torch.float32, device=dev),
+        "mass": torch.empty(rows, dtype=torch.float32, device=dev),
+    }
+    if want_probs:
+        res["probs"] = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+    if want_filtered:
+        res["filtered"] = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+    if top_p_rows is not None:
+        if top_p_rows.dtype != torch.float32 or top_p_rows.numel() < rows:
+            raise ValueError("top_p_rows must be float32 with at least one entry per row")
+        top_p_rows = top_p_rows.reshape(-1).contiguous()
+    probs, filt = res.get("probs"), res.get("filtered")
+    _lib.call(
+        "ls_filter_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
+        float(temperature), float(top_p), _lib.ptr(top_p_rows), int(top_k),
+        _lib.ptr(probs), probs.stride(0) if probs is not None else 0,
+        _lib.ptr(filt), filt.stride(0) if filt is not None else 0,
+        res["cutoff"].data_ptr(), res["mass"].data_ptr(), _lib.stream(dev),
+    )
+    return res

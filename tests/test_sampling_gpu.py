@@ -1,0 +1,231 @@
+"""GPU parity of the sampling kernels against the declared-arithmetic oracle.
+
+Tokens, accept lengths, cutoffs and masses must match bit-exactly; the
+probabilities themselves are also produced in the same declared arithmetic,
+so they are compared exactly as well (the 1e-5 contract tolerance against the
+reference's torch formulation is checked on the CPU in test_oracle_sampling.py).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nm
+from oracle import sampling as osmp
+from loopspec_amd import philox, verify, workloads
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_filter(logits, temperature, top_p, penalty=1.0, history=None):
+    x = osmp.process_logits(np.asarray(logits, dtype=np.float32), temperature, penalty, history)
+    return osmp.filter_row(x, top_p)
+
+
+def draft_tokens_from(inp, cfg):
+    """Sample each draft position from its filtered draft distribution (oracle)."""
+    d = inp["draft"].float().numpy()
+    du = inp["draft_uniforms"].numpy()
+    out = np.zeros((cfg.batch, cfg.k), dtype=np.int64)
+    for b in range(cfg.batch):
+        hist = None
+        if cfg.penalty != 1.0:
+            hist = inp["history"][b, : int(inp["history_len"][b])].numpy()
+        for i in range(cfg.k):
+            q = oracle_filter(d[b, i], cfg.temperature, cfg.top_p, cfg.penalty, hist).P
+            out[b, i] = osmp.categorical_pick(q, du[b, i])
+    return torch.from_numpy(out)
+
+
+def run_spec(cfg, inp, drafts, gpu):
+    hist = inp["history"].to(gpu) if cfg.penalty != 1.0 else None
+    hl = inp["history_len"].to(gpu) if cfg.penalty != 1.0 else None
+    acc, tok = verify.speculative_verify(
+        inp["target"].to(gpu), inp["draft"].to(gpu), drafts.to(gpu), inp["uniforms"].to(gpu),
+        cfg.temperature, cfg.top_p, penalty=cfg.penalty, history=hist, history_len=hl)
+    torch.cuda.synchronize()
+    return acc.cpu().numpy(), tok.cpu().numpy()
+
+
+def oracle_spec(cfg, inp, drafts):
+    hists = None
+    if cfg.penalty != 1.0:
+        hists = [inp["history"][b, : int(inp["history_len"][b])].numpy() for b in range(cfg.batch)]
+    return osmp.speculative_verify(inp["target"].float().numpy(), inp["draft"].float().numpy(), drafts.numpy(),
+                                   inp["uniforms"].numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hists)
+
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 49152), (torch.float16, 4096),
+                                         (torch.bfloat16, 128256), (torch.float32, 1000)])
+@pytest.mark.parametrize("temperature,top_p", [(1.0, 0.7), (0.7, 0.9), (1.0, 1.0), (1.3, 0.05)])
+def test_filter_logits_bitexact(gpu, dtype, vocab, temperature, top_p):
+    g = torch.Generator().manual_seed(vocab + int(top_p * 100))
+    logits = (torch.randn(6, vocab, generator=g) * 3).to(dtype)
+    announce(f"filter dtype={dtype} V={vocab} T={temperature} top_p={top_p}")
+    res = verify.filter_logits(logits.to(gpu), temperature, top_p, want_probs=True)
+    torch.cuda.synchronize()
+    for r in range(6):
+        want = oracle_filter(logits[r].float().numpy(), temperature, top_p)
+        assert np.array_equal(res["probs"][r].cpu().numpy(), want.soft.p), r
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
+        if top_p < 1:
+            assert res["cutoff"][r].item() == want.cutoff
+            assert res["mass"][r].item() == nm.mass_to_f32(want.mass_fx)
+
+
+@pytest.mark.parametrize("case", ["all_equal", "one_hot", "tiny_top_p", "two_level", "neg_inf"])
+def test_filter_logits_edge_rows(gpu, case):
+    v = 49152
+    x = torch.randn(4, v) * 2
+    if case == "all_equal":
+        x[:] = 0.5  # every element in one octave: slow path, dense support
+    elif case == "one_hot":
+        x[:, 123] = 60.0
+    elif case == "tiny_top_p":
+        pass
+    elif case == "two_level":
+        x[:] = -5.0
+        x[:, ::3] = 0.0  # a third of the row ties at the top
+    elif case == "neg_inf":
+        x[:, 1000:] = -float("inf")
+    top_p = 1e-6 if case == "tiny_top_p" else 0.7
+    announce(f"filter edge case {case}")
+    res = verify.filter_logits(x.to(gpu), 1.0, top_p, want_probs=True)
+    torch.cuda.synchronize()
+    for r in range(4):
+        want = oracle_filter(x[r].numpy(), 1.0, top_p)
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), (case, r)
+        assert res["cutoff"][r].item() == want.cutoff
+
+
+def test_filter_per_row_thresholds(gpu):
+    x = torch.randn(5, 8192) * 3
+    tp = torch.tensor([0.1, 0.5, 0.7, 0.95, 0.999], dtype=torch.float32)
+    res = verify.filter_logits(x.to(gpu), 1.0, 0.7, top_p_rows=tp.to(gpu))
+    torch.cuda.synchronize()
+    for r in range(5):
+        want = oracle_filter(x[r].numpy(), 1.0, float(tp[r]))
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P)
+
+
+@pytest.mark.parametrize("dtype,vocab,temperature,top_p", [
+    (torch.float32, 49152, 1.0, 0.7), (torch.bfloat16, 128256, 0.7, 0.9), (torch.float32, 4096, 1.0, 1.0),
+    (torch.float16, 32000, 0.8, 0.5)])
+def test_sample_logits_bitexact(gpu, dtype, vocab, temperature, top_p):
+    rows = 16
+    g = torch.Generator().manual_seed(7)
+    logits = (torch.randn(rows, vocab, generator=g) * 3).to(dtype)
+    u = torch.from_numpy(philox.uniforms((rows,), seed=9))
+    announce(f"sample dtype={dtype} V={vocab}")
+    got = verify.sample_logits(logits.to(gpu), u.to(gpu), temperature, top_p)
+    torch.cuda.synchronize()
+    want = [osmp.categorical_pick(oracle_filter(logits[r].float().numpy(), temperature, top_p).P, u[r].item())
+            for r in range(rows)]
+    assert got.cpu().tolist() == want
+
+
+def test_sample_logits_with_penalty(gpu):
+    cfg = workloads.SamplingConfig("t", 6, 1, 32000, torch.bfloat16, 0.7, 0.9, penalty=1.1, target_std=4.0,
+                                   hist_min=50, hist_max=400)
+    inp = workloads.sampling_inputs(cfg, 3)
+    logits = inp["target"][:, 0]
+    u = inp["uniforms"][:, 0].contiguous()
+    announce("sample with repetition penalty")
+    got = verify.sample_logits(logits.to(gpu), u.to(gpu), cfg.temperature, cfg.top_p, penalty=cfg.penalty,
+                               history=inp["history"].to(gpu), history_len=inp["history_len"].to(gpu))
+    torch.cuda.synchronize()
+    want = []
+    for r in range(cfg.batch):
+        hist = inp["history"][r, : int(inp["history_len"][r])].numpy()
+        q = oracle_filter(logits[r].float().numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hist).P
+        want.append(osmp.categorical_pick(q, u[r].item()))
+    assert got.cpu().tolist() == want
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_spec_verify_c3_full_shape(gpu, seed):
+    cfg = workloads.C3
+    inp = workloads.sampling_inputs(cfg, seed)
+    drafts = draft_tokens_from(inp, cfg)
+    announce(f"spec C3 full seed={seed}")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
+
+
+def test_spec_verify_c4_like_with_penalty(gpu):
+    cfg = workloads.SamplingConfig("c4s", 4, 4, 128256, torch.bfloat16, 0.7, 0.9, penalty=1.1, target_std=4.0,
+                                   hist_min=256, hist_max=4096)
+    inp = workloads.sampling_inputs(cfg, 5)
+    drafts = draft_tokens_from(inp, cfg)
+    announce("spec C4-like")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
+
+
+@pytest.mark.parametrize("variant", ["unfiltered", "flat", "forced_reject", "k1", "k3_fp16"])
+def test_spec_verify_variants(gpu, variant):
+    base = dict(name=variant, batch=6, k=2, vocab=16384, dtype=torch.float32, temperature=1.0, top_p=0.7)
+    if variant == "unfiltered":
+        base["top_p"] = 1.0
+    if variant == "flat":
+        base["target_std"] = 0.05  # near-uniform rows: huge supports
+        base["top_p"] = 0.5
+    if variant == "k1":
+        base["k"] = 1
+    if variant == "k3_fp16":
+        base.update(k=3, dtype=torch.float16, temperature=1.2)
+    cfg = workloads.SamplingConfig(**base)
+    inp = workloads.sampling_inputs(cfg, 11)
+    drafts = draft_tokens_from(inp, cfg)
+    if variant == "forced_reject":
+        inp["uniforms"][:, 0] = 0.9999999  # almost always reject position 0
+    announce(f"spec variant {variant}")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len), variant
+    assert np.array_equal(tok, want.tokens), variant
+
+
+def test_spec_verify_graph_replays(gpu):
+    cfg = workloads.SamplingConfig("g", 8, 2, 49152, torch.float32, 1.0, 0.7)
+    inp = workloads.sampling_inputs(cfg, 2)
+    drafts = draft_tokens_from(inp, cfg)
+    want = oracle_spec(cfg, inp, drafts)
+    t, d, dr, u = (inp["target"].to(gpu), inp["draft"].to(gpu), drafts.to(gpu), inp["uniforms"].to(gpu))
+    acc = torch.empty(8, dtype=torch.int32, device=gpu)
+    tok = torch.empty((8, 3), dtype=torch.int64, device=gpu)
+    verify.speculative_verify(t, d, dr, u, 1.0, 0.7, accept_len=acc, tokens=tok)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("spec graph capture")
+    with torch.cuda.graph(g):
+        verify.speculative_verify(t, d, dr, u, 1.0, 0.7, accept_len=acc, tokens=tok)
+    for rep in range(3):
+        acc.fill_(-7)
+        tok.fill_(-7)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(acc.cpu().numpy(), want.accept_len), rep
+        assert np.array_equal(tok.cpu().numpy(), want.tokens), rep
+
+
+def test_spec_verify_alternating_shapes_share_workspace(gpu):
+    """Calls of different (B, k) on one workspace: each must see zeroed counters."""
+    ws = torch.zeros(verify.spec_verify_workspace_bytes(64, 3, 8192), dtype=torch.uint8, device=gpu)
+    shapes = [(64, 2), (8, 2), (64, 3), (3, 1), (64, 2)]
+    for i, (b, k) in enumerate(shapes):
+        cfg = workloads.SamplingConfig("alt", b, k, 8192, torch.float32, 1.0, 0.8)
+        inp = workloads.sampling_inputs(cfg, 40 + i)
+        drafts = draft_tokens_from(inp, cfg)
+        announce(f"spec alternating shapes B={b} k={k}")
+        acc, tok = verify.speculative_verify(inp["target"].to(gpu), inp["draft"].to(gpu), drafts.to(gpu),
+                                             inp["uniforms"].to(gpu), 1.0, 0.8, workspace=ws)
+        torch.cuda.synchronize()
+        want = oracle_spec(cfg, inp, drafts)
+        assert np.array_equal(acc.cpu().numpy(), want.accept_len), (b, k)
+        assert np.array_equal(tok.cpu().numpy(), want.tokens), (b, k)
