@@ -254,7 +254,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(rows are independent; see DESIGN.md for how the batch would shard).", file=sys.stderr)
+              "(verify rows are independent, so a batch shards by batch element with no "
+              "cross-GPU traffic; run one process per GPU).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)

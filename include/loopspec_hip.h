@@ -97,8 +97,8 @@ uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
  * 16-byte aligned rows, vocab*elem_bytes a multiple of 16):
  *   x = logits; for ids in the row's history (if penalty != 1):
  *       x <- x < 0 ? x*penalty : x*RN(1/penalty);  then x <- x*RN(1/T) (T != 1);
- *   p = softmax(x) in the library's declared arithmetic (see DESIGN.md of the
- *   repository: ls_exp, 2^-46 fixed-point masses);
+ *   p = softmax(x) in the library's declared arithmetic (a fixed polynomial
+ *   exp, exact 2^-46 fixed-point masses, p = RN(e / RN32(mass)));
  *   top_p < 1: keep p >= c with c = max{v : sum_{p>=v} fx46(p) >= fx46(top_p)}
  *   (ties kept; the whole row if no v qualifies), renormalise by the retained
  *   mass -- the value semantics of sort + cumsum + searchsorted(right=False)
@@ -110,7 +110,7 @@ uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 /* Fused chain verify, one launch for B batch elements of k draft positions:
  * filters every target row [B, k+1, V] (P_i) and draft row [B, k, V] (Q_i);
  * position i accepts draft_tokens[b, i] iff u[b,i] < min(1, P_i[x]/Q_i[x])
- * (sglang_recurrent/loopspec/sampling/sampler.py:428-460); the first rejection
+ * (sglang_recurrent/loopspec/sampling/sampler.py:429-460); the first rejection
  * at i emits a draw from normalize(max(P_i - Q_i, 0)) (falling back to P_i at
  * zero mass, sglang_recurrent/loopspec/sampling/rejection.py:60-69) with
  * u[b, k+i]; if all k accept, a bonus draw from P_k with u[b, 2k]
@@ -157,6 +157,133 @@ int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
                      int64_t top_k, float* probs_out, int64_t probs_stride,
                      float* filtered_out, int64_t filtered_stride, float* cutoff_out,
                      float* mass_out, ls_stream_t stream);
+
+/* Top-k filtering of probability rows (float32, row stride row_stride): c_k =
+ * the k-th largest value of the row (duplicates counted, 1 <= k <= vocab),
+ * c = max(c_k, cutoff_in[row]) when cutoff_in (float32 [rows]) is given, and
+ * filtered[row] = p >= c ? p / retained mass : 0 (ties at c kept); cutoff_out
+ * (optional, float32 [rows]) receives c. With cutoff_in = the top-p cutoff of
+ * ls_filter_logits this is the joint top-k/top-p rule of filtered_probabilities
+ * (sglang_recurrent/loopspec/sampling/distributions.py:72-86); alone it stands
+ * in for the top-k-only sgl_kernel.top_k_renorm_prob call (distributions.py:51-57). */
+int ls_top_k_filter(const float* probs, int64_t row_stride, int64_t rows, int64_t vocab, int64_t k,
+                    const float* cutoff_in, float* filtered, int64_t out_stride, float* cutoff_out,
+                    ls_stream_t stream);
+
+/* Dense-row primitives of CategoricalSampler / RejectionSampler. Probability rows
+ * are float32 with unit vocabulary stride and the given row stride (elements);
+ * token ids and flags are int64. Draws are the index-ordered inverse CDF over
+ * exact 2^-46 fixed-point masses: the first j with cum(j) > floor(u * total);
+ * index 0 when the total is zero. One 1024-lane workgroup per row. */
+
+/* out[s] = draw from row r = sample_rows ? sample_rows[s] : s with uniforms[s].
+ * Replaces CategoricalSampler.sample / _sample_with_uniforms
+ * (sglang_recurrent/loopspec/sampling/sampler.py:22-102, 508-588). */
+int ls_sample_probs(const float* probs, int64_t row_stride, int64_t rows, int64_t vocab,
+                    const float* uniforms, const int64_t* sample_rows, int64_t nsamples,
+                    int64_t* out, ls_stream_t stream);
+
+/* Draw from the retained, unnormalised weights probs >= cutoff, cutoff =
+ * sorted_probs[r, cutoff_indices[r * cutoff_stride]] (ties kept); optional
+ * indirect rows as above. Replaces CategoricalSampler.sample_top_p
+ * (sampler.py:106-175, 786-837). */
+int ls_sample_top_p(const float* probs, int64_t row_stride, const float* sorted_probs,
+                    int64_t sorted_stride, const int64_t* cutoff_indices, int64_t cutoff_stride,
+                    int64_t rows, int64_t vocab, const float* uniforms, const int64_t* sample_rows,
+                    int64_t nsamples, int64_t* out, ls_stream_t stream);
+
+/* normalized[r] = probs >= cutoff ? probs / retained mass : 0. Replaces
+ * CategoricalSampler.normalize_top_p_for_sampling (sampler.py:348-425, 737-785). */
+int ls_normalize_top_p(const float* probs, int64_t row_stride, const float* sorted_probs,
+                       int64_t sorted_stride, const int64_t* cutoff_indices, int64_t cutoff_stride,
+                       int64_t rows, int64_t vocab, float* normalized, int64_t out_stride,
+                       ls_stream_t stream);
+
+/* q2 conditional residual r = max(second - first, 0) with r[selected] = 0:
+ * samples[b] drawn from r with uniforms[b]; normalized[b] = r / mass (zero row at
+ * zero mass); actions[b] = mass > 0 && second[x] < first[x] at x = selected[b].
+ * Replaces CategoricalSampler.sample_conditional_residual (sampler.py:179-344,
+ * 629-703). */
+int ls_conditional_residual(const float* first, int64_t first_stride, const float* second,
+                            int64_t second_stride, const int64_t* selected_tokens, int64_t rows,
+                            int64_t vocab, const float* uniforms, float* normalized,
+                            int64_t out_stride, int64_t* actions, int64_t* samples,
+                            ls_stream_t stream);
+
+/* decisions int64 [rows, 5] = (accepted ? token : -1, 0, accepted, !accepted, 0)
+ * with accepted = u < min(1, target/proposal) in binary32 (a NaN ratio rejects).
+ * Replaces CategoricalSampler.verify (sampler.py:429-460, 705-735). */
+int ls_verify_decisions(const float* target_masses, const float* proposal_masses,
+                        const float* uniforms, const int64_t* tokens, int64_t rows,
+                        int64_t* decisions, ls_stream_t stream);
+
+/* Rejection fallback for `rows` rejected q1 proposals: F = normalize(max(P - Q1,
+ * 0)) (normalize(P) at zero mass); with q2 (metadata[r] = (y, has_q2)) accept y
+ * iff uniforms[2r] < min(1, F[y] / R[y]); the fallback draw always consumes
+ * uniforms[2r+1] from normalize(max(F - R, 0)) (F without q2 or at zero mass).
+ * out int64 [rows, 3] = (token, second_accepted, second_rejected). A q2 token
+ * outside [0, vocab) is never accepted. Replaces RejectionSampler._run
+ * (sglang_recurrent/loopspec/sampling/rejection.py:42-97), one row per replay
+ * there, any number of rows per launch here. */
+int ls_rejection(const float* first, int64_t first_stride, const float* target,
+                 int64_t target_stride, const float* second, int64_t second_stride,
+                 const int64_t* metadata, const float* uniforms, int64_t rows, int64_t vocab,
+                 int64_t* out, ls_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * (d) KV slots, request mapping and the branch -> main KV-timeline commit
+ * ------------------------------------------------------------------------------ */
+
+/* Rows with valid_markers[b] >= 0 take free_slots[(cursor + rank) % capacity]
+ * in batch order (rank = number of valid rows before b); skipped rows keep
+ * their output; *allocation_cursor advances by the number of valid rows.
+ * All arrays int64, contiguous; allocation_cursor is a device scalar.
+ * Replaces allocate_decode_slots (sglang_recurrent/loopspec/graph_ops.py:137-172). */
+int ls_allocate_decode_slots(const int64_t* free_slots, int64_t capacity,
+                             int64_t* allocation_cursor, const int64_t* valid_markers,
+                             int64_t batch, int64_t* out_cache_locs, ls_stream_t stream);
+
+/* mapping: int32 [request_capacity, mapping_stride] (first max_context_len
+ * columns used). For each row b: copy_lens[b] > 0 copies
+ * mapping[source_rows[b], :copy_len] to mapping[request_rows[b], :copy_len];
+ * copy_lens[b] >= 0 then sets mapping[request_rows[b], positions[b]] =
+ * (int32) out_cache_locs[b]; copy_lens[b] < 0 skips the row. [B] arrays int64.
+ * Replaces update_request_mapping (sglang_recurrent/loopspec/graph_ops.py:221-271). */
+int ls_update_request_mapping(int32_t* mapping, int64_t mapping_stride,
+                              int64_t max_context_len, const int64_t* request_rows,
+                              const int64_t* source_rows, const int64_t* copy_lens,
+                              const int64_t* positions, const int64_t* out_cache_locs,
+                              int64_t batch, ls_stream_t stream);
+
+/* Row copies of width_bytes bytes: gather (gather != 0) destination[b] =
+ * source[row_indices[b]]; scatter destination[row_indices[b]] = source[b].
+ * Indices < 0 or >= bank_rows skip the row. row_indices int64 [B].
+ * Replaces copy_state_rows (sglang_recurrent/loopspec/graph_ops.py:53-94). */
+int ls_copy_state_rows(const void* source, void* destination, const int64_t* row_indices,
+                       int64_t batch, int64_t bank_rows, int64_t width_bytes, int gather,
+                       ls_stream_t stream);
+
+/* Paged commit of accepted draft tokens (two kernels, stream-ordered).
+ * KV pool: `planes` planes (layers x loops x {K, V}), plane p's token row of slot s
+ * at kv + p*plane_stride_bytes + s*token_bytes; slot = page*page_size + offset,
+ * num_pages physical pages. Row b appends its first accept_len[b] (int32, clamped
+ * to [0, k]) branch tokens (branch_slots int64 [B, k]) at positions ctx_len[b]..
+ * of its page table (int32 [B, max_pages]); a position in a page the row does
+ * not own yet (page index >= ceil(ctx_len/page_size)) takes the next page of the
+ * free-page ring free_pages[(*page_cursor + i) % ring_size] in batch order. Writes
+ * dst_slots int64 [B, k] (-1 for non-accepted tokens), updates page_table,
+ * ctx_len and *page_cursor, then copies every plane's token row from the branch
+ * slot to the destination slot. Out-of-range pages/slots are skipped and set
+ * *status |= 1 (status may be NULL). planes == 0 runs only the slot plan.
+ * The reference's own commit is an ownership transfer of page-size-1 slots
+ * (sglang_recurrent/loopspec/branching/manager.py:410-482); this is the paged
+ * counterpart with the same ring-allocation rule (graph_ops.py:117-134). */
+int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t token_bytes,
+                 int64_t num_pages, int64_t page_size, const int32_t* accept_len,
+                 const int64_t* branch_slots, int64_t batch, int64_t k, int32_t* page_table,
+                 int64_t max_pages, int64_t* ctx_len, const int64_t* free_pages,
+                 int64_t ring_size, int64_t* page_cursor, int64_t* dst_slots, int32_t* status,
+                 ls_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,400 @@
+// Dense-row sampling primitives behind the reference's CategoricalSampler and
+// RejectionSampler interfaces (gfx950). One 1024-lane workgroup per row; the
+// row is streamed through L2 in two or three exact passes:
+//
+//  dense_sample     inverse-CDF draw over weights w(i) produced per mode:
+//                   plain p (sampler.py:22-102), retained top-p p >= cutoff
+//                   (sampler.py:106-175), q2 conditional residual
+//                   max(q2 - q1, 0) with the q1 token excluded (sampler.py:179-281)
+//  dense_normalize  w(i) / mass for the top-p (sampler.py:348-425) and residual
+//                   (sampler.py:284-344, incl. the proposal action flag) modes
+//  verify_decisions u < min(1, p/q) 5-tuples (sampler.py:429-460)
+//  rejection        RejectionSampler._run for a batch of rejected rows
+//                   (rejection.py:42-97)
+// Masses are exact 2^-46 fixed-point sums and draws follow the declared
+// arithmetic of ls_numerics.hpp.
+#include "ls_block.hpp"
+#include "ls_runtime.hpp"
+
+namespace ls {
+namespace {
+
+constexpr int kDB = 1024;
+enum WMode : int { kPlain = 0, kTopP = 1, kResid = 2 };
+
+struct DenseParams {
+  const float* probs;  // [B, V]: p (plain/top-p) or q2 (residual)
+  int64_t stride;
+  const float* sorted;  // top-p: sorted probabilities and cutoff ranks
+  int64_t sstride;
+  const int64_t* cutoff_idx;
+  int64_t cutoff_idx_stride;
+  const float* first;  // residual: q1 rows and the selected q1 ids
+  int64_t fstride;
+  const int64_t* selected;
+  int64_t vocab;
+  const float* uniforms;
+  const int64_t* sample_rows;  // optional indirect rows
+  int64_t* samples;
+  float* normalized;
+  int64_t nstride;
+  int64_t* actions;
+};
+
+template <int MODE>
+struct Weight {
+  const float* row;
+  const float* frow;
+  float cutoff;
+  int64_t sel;
+  __device__ __forceinline__ float operator()(int64_t i) const {
+    const float v = row[i];
+    if constexpr (MODE == kPlain) {
+      return v;
+    } else if constexpr (MODE == kTopP) {
+      return v >= cutoff ? v : 0.0f;
+    } else {
+      const float d = v - frow[i];
+      return (i == sel || !(d > 0.0f)) ? 0.0f : d;
+    }
+  }
+};
+
+template <int MODE>
+__device__ __forceinline__ Weight<MODE> weight_for(const DenseParams& p, int64_t row) {
+  Weight<MODE> w;
+  w.row = p.probs + row * p.stride;
+  w.frow = nullptr;
+  w.cutoff = 0.0f;
+  w.sel = -1;
+  if constexpr (MODE == kTopP) {
+    w.cutoff = p.sorted[row * p.sstride + p.cutoff_idx[row * p.cutoff_idx_stride]];
+  }
+  if constexpr (MODE == kResid) {
+    w.frow = p.first + row * p.fstride;
+    w.sel = p.selected[row];
+  }
+  return w;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kDB) void dense_sample_kernel(const DenseParams p) {
+  __shared__ uint64_t red[kDB / kWave];
+  __shared__ int64_t result;
+  const int64_t s = blockIdx.x;
+  const int64_t row = p.sample_rows ? p.sample_rows[s] : s;
+  const Weight<MODE> w = weight_for<MODE>(p, row);
+  const int64_t tok = row_pick<kDB>(p.vocab, p.uniforms[s], w, red, &result);
+  if (threadIdx.x == 0) p.samples[s] = tok;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kDB) void dense_normalize_kernel(const DenseParams p) {
+  __shared__ uint64_t red[kDB / kWave];
+  const int64_t row = blockIdx.x;
+  const Weight<MODE> w = weight_for<MODE>(p, row);
+  const uint64_t mfx = row_mass<kDB>(p.vocab, w, red);
+  const float mass = mass_to_f32(mfx);
+  float* out = p.normalized + row * p.nstride;
+  for (int64_t i = threadIdx.x; i < p.vocab; i += kDB) {
+    const float v = w(i);
+    if constexpr (MODE == kResid) {
+      out[i] = mfx > 0 ? v / mass : 0.0f;
+    } else {
+      out[i] = p.probs[row * p.stride + i] >= w.cutoff ? p.probs[row * p.stride + i] / mass : 0.0f;
+    }
+  }
+  if constexpr (MODE == kResid) {
+    if (threadIdx.x == 0 && p.actions) {
+      const int64_t x = w.sel;
+      const bool gated = w.row[x] < w.frow[x];
+      p.actions[row] = (mfx > 0 && gated) ? 1 : 0;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void verify_kernel(const float* __restrict__ target, const float* __restrict__ proposal,
+                                                     const float* __restrict__ uniforms,
+                                                     const int64_t* __restrict__ tokens, int64_t rows,
+                                                     int64_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows) return;
+  const bool acc = accept_draw(uniforms[i], target[i], proposal[i]);
+  int64_t* o = out + i * 5;
+  o[0] = acc ? tokens[i] : -1;
+  o[1] = 0;
+  o[2] = acc ? 1 : 0;
+  o[3] = acc ? 0 : 1;
+  o[4] = 0;
+}
+
+struct RejParams {
+  const float* first;   // Q1 rows [R, V]
+  int64_t fstride;
+  const float* target;  // P rows
+  int64_t tstride;
+  const float* second;  // R rows (read only where metadata says q2 exists)
+  int64_t sstride;
+  const int64_t* metadata;  // [R, 2]: q2 token (dummy when absent), has_q2
+  const float* uniforms;    // [R, 2]: q2 acceptance, fallback draw
+  int64_t vocab;
+  int64_t* out;             // [R, 3]: token, second_accepted, second_rejected
+};
+
+__global__ __launch_bounds__(kDB) void rejection_kernel(const RejParams p) {
+  __shared__ uint64_t red[kDB / kWave];
+  __shared__ int64_t result;
+  const int64_t r = blockIdx.x;
+  const float* Q = p.first + r * p.fstride;
+  const float* P = p.target + r * p.tstride;
+  const float* R = p.second + r * p.sstride;
+  const bool has_second = p.metadata[2 * r + 1] != 0;
+  const int64_t n = p.vocab;
+  // F = normalize(max(P - Q1, 0)), falling back to normalize(P) at zero mass.
+  auto delta = [&](int64_t i) {
+    const float d = P[i] - Q[i];
+    return d > 0.0f ? d : 0.0f;
+  };
+  const uint64_t d_fx = row_mass<kDB>(n, delta, red);
+  const uint64_t p_fx = row_mass<kDB>(n, [&](int64_t i) { return P[i]; }, red);
+  const bool use_d = d_fx > 0;
+  const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
+  auto F = [&](int64_t i) { return (use_d ? delta(i) : P[i]) / den; };
+  const int64_t y = p.metadata[2 * r];
+  bool accepted = false;
+  if (has_second && y >= 0 && y < n) accepted = accept_draw(p.uniforms[2 * r], F(y), R[y]);
+  // Fallback: normalize(max(F - R, 0)) with q2, or F itself.
+  uint64_t s_fx = 0;
+  if (has_second) {
+    s_fx = row_mass<kDB>(n, [&](int64_t i) {
+      const float d = F(i) - R[i];
+      return d > 0.0f ? d : 0.0f;
+    }, red);
+  }
+  const bool use_s = has_second && s_fx > 0;
+  const float sden = use_s ? mass_to_f32(s_fx) : 1.0f;
+  const int64_t sampled = row_pick<kDB>(n, p.uniforms[2 * r + 1], [&](int64_t i) {
+    if (use_s) {
+      const float d = F(i) - R[i];
+      return (d > 0.0f ? d : 0.0f) / sden;
+    }
+    return F(i);
+  }, red, &result);
+  if (threadIdx.x == 0) {
+    p.out[3 * r + 0] = accepted ? y : sampled;
+    p.out[3 * r + 1] = accepted ? 1 : 0;
+    p.out[3 * r + 2] = (has_second && !accepted) ? 1 : 0;
+  }
+}
+
+// k-th largest value of a non-negative float32 row (duplicates counted) by a
+// 4-pass most-significant-digit radix select on the IEEE bits (monotone for
+// non-negative floats), then c = max(c_k, cutoff_in[row]) and the retained,
+// renormalised row. Per-wave sub-histograms keep LDS atomics uncontended.
+constexpr int kTkWaves = kDB / kWave;
+
+__global__ __launch_bounds__(kDB) void top_k_filter_kernel(const float* __restrict__ probs, int64_t stride,
+                                                           int64_t vocab, int64_t k,
+                                                           const float* __restrict__ cutoff_in,
+                                                           float* __restrict__ out, int64_t out_stride,
+                                                           float* __restrict__ cutoff_out) {
+  __shared__ uint32_t hist[kTkWaves][256];
+  __shared__ uint32_t total[256];
+  __shared__ uint32_t sel[2];  // chosen digit, remaining rank within it
+  __shared__ uint64_t red[kDB / kWave];
+  const int64_t row = blockIdx.x;
+  const float* pr = probs + row * stride;
+  const int wid = threadIdx.x / kWave;
+  uint32_t prefix = 0, prefix_mask = 0;
+  uint32_t rank = static_cast<uint32_t>(k);  // 1-based rank among keys matching the prefix
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = threadIdx.x; i < kTkWaves * 256; i += kDB) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < vocab; i += kDB) {
+      const float v = pr[i];
+      const uint32_t key = v > 0.0f ? __float_as_uint(v) : 0u;
+      if ((key & prefix_mask) == prefix) atomicAdd(&hist[wid][(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int w = 0; w < kTkWaves; ++w) c += hist[w][threadIdx.x];
+      total[threadIdx.x] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t r = rank;
+      int d = 255;
+      for (; d > 0; --d) {
+        if (total[d] >= r) break;
+        r -= total[d];
+      }
+      sel[0] = static_cast<uint32_t>(d);
+      sel[1] = r;
+    }
+    __syncthreads();
+    prefix |= sel[0] << shift;
+    prefix_mask |= 255u << shift;
+    rank = sel[1];
+    __syncthreads();
+  }
+  float c = __uint_as_float(prefix);
+  if (cutoff_in) c = fmaxf(c, cutoff_in[row]);
+  auto w = [&](int64_t i) {
+    const float v = pr[i];
+    return v >= c ? v : 0.0f;
+  };
+  const uint64_t mfx = row_mass<kDB>(vocab, w, red);
+  const float mass = mass_to_f32(mfx);
+  float* o = out + row * out_stride;
+  for (int64_t i = threadIdx.x; i < vocab; i += kDB) {
+    const float v = pr[i];
+    o[i] = v >= c ? v / mass : 0.0f;
+  }
+  if (threadIdx.x == 0 && cutoff_out) cutoff_out[row] = c;
+}
+
+int launch_sample(const DenseParams& p, int mode, int64_t n, hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(n)), b(kDB);
+  switch (mode) {
+    case kPlain: hipLaunchKernelGGL(dense_sample_kernel<kPlain>, g, b, 0, st, p); break;
+    case kTopP: hipLaunchKernelGGL(dense_sample_kernel<kTopP>, g, b, 0, st, p); break;
+    case kResid: hipLaunchKernelGGL(dense_sample_kernel<kResid>, g, b, 0, st, p); break;
+    default: return fail(LS_ERR_VALUE, "unknown weight mode");
+  }
+  return check_launch("dense sample launch");
+}
+
+}  // namespace
+}  // namespace ls
+
+using namespace ls;
+
+extern "C" {
+
+int ls_sample_probs(const float* probs, int64_t row_stride, int64_t rows, int64_t vocab, const float* uniforms,
+                    const int64_t* sample_rows, int64_t nsamples, int64_t* out, ls_stream_t stream) {
+  if (rows < 0 || nsamples < 0 || vocab <= 0) return fail(LS_ERR_VALUE, "sample_probs: invalid shape");
+  if (nsamples == 0) return LS_OK;
+  if (!probs || !uniforms || !out) return fail(LS_ERR_VALUE, "sample_probs: NULL pointer");
+  DenseParams p{};
+  p.probs = probs;
+  p.stride = row_stride;
+  p.vocab = vocab;
+  p.uniforms = uniforms;
+  p.sample_rows = sample_rows;
+  p.samples = out;
+  return launch_sample(p, kPlain, nsamples, static_cast<hipStream_t>(stream));
+}
+
+int ls_sample_top_p(const float* probs, int64_t row_stride, const float* sorted_probs, int64_t sorted_stride,
+                    const int64_t* cutoff_indices, int64_t cutoff_stride, int64_t rows, int64_t vocab,
+                    const float* uniforms, const int64_t* sample_rows, int64_t nsamples, int64_t* out,
+                    ls_stream_t stream) {
+  if (rows < 0 || nsamples < 0 || vocab <= 0) return fail(LS_ERR_VALUE, "sample_top_p: invalid shape");
+  if (nsamples == 0) return LS_OK;
+  if (!probs || !sorted_probs || !cutoff_indices || !uniforms || !out)
+    return fail(LS_ERR_VALUE, "sample_top_p: NULL pointer");
+  DenseParams p{};
+  p.probs = probs;
+  p.stride = row_stride;
+  p.sorted = sorted_probs;
+  p.sstride = sorted_stride;
+  p.cutoff_idx = cutoff_indices;
+  p.cutoff_idx_stride = cutoff_stride;
+  p.vocab = vocab;
+  p.uniforms = uniforms;
+  p.sample_rows = sample_rows;
+  p.samples = out;
+  return launch_sample(p, kTopP, nsamples, static_cast<hipStream_t>(stream));
+}
+
+int ls_normalize_top_p(const float* probs, int64_t row_stride, const float* sorted_probs, int64_t sorted_stride,
+                       const int64_t* cutoff_indices, int64_t cutoff_stride, int64_t rows, int64_t vocab,
+                       float* normalized, int64_t out_stride, ls_stream_t stream) {
+  if (rows < 0 || vocab <= 0) return fail(LS_ERR_VALUE, "normalize_top_p: invalid shape");
+  if (rows == 0) return LS_OK;
+  if (!probs || !sorted_probs || !cutoff_indices || !normalized)
+    return fail(LS_ERR_VALUE, "normalize_top_p: NULL pointer");
+  DenseParams p{};
+  p.probs = probs;
+  p.stride = row_stride;
+  p.sorted = sorted_probs;
+  p.sstride = sorted_stride;
+  p.cutoff_idx = cutoff_indices;
+  p.cutoff_idx_stride = cutoff_stride;
+  p.vocab = vocab;
+  p.normalized = normalized;
+  p.nstride = out_stride;
+  hipLaunchKernelGGL(dense_normalize_kernel<kTopP>, dim3(static_cast<unsigned>(rows)), dim3(kDB), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return check_launch("normalize_top_p launch");
+}
+
+int ls_conditional_residual(const float* first, int64_t first_stride, const float* second, int64_t second_stride,
+                            const int64_t* selected_tokens, int64_t rows, int64_t vocab, const float* uniforms,
+                            float* normalized, int64_t out_stride, int64_t* actions, int64_t* samples,
+                            ls_stream_t stream) {
+  if (rows < 0 || vocab <= 0) return fail(LS_ERR_VALUE, "conditional_residual: invalid shape");
+  if (rows == 0) return LS_OK;
+  if (!first || !second || !selected_tokens || !uniforms || !normalized || !actions || !samples)
+    return fail(LS_ERR_VALUE, "conditional_residual: NULL pointer");
+  DenseParams p{};
+  p.probs = second;
+  p.stride = second_stride;
+  p.first = first;
+  p.fstride = first_stride;
+  p.selected = selected_tokens;
+  p.vocab = vocab;
+  p.uniforms = uniforms;
+  p.samples = samples;
+  p.normalized = normalized;
+  p.nstride = out_stride;
+  p.actions = actions;
+  const auto st = static_cast<hipStream_t>(stream);
+  int rc = launch_sample(p, kResid, rows, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(dense_normalize_kernel<kResid>, dim3(static_cast<unsigned>(rows)), dim3(kDB), 0, st, p);
+  return check_launch("conditional_residual normalize launch");
+}
+
+int ls_verify_decisions(const float* target_masses, const float* proposal_masses, const float* uniforms,
+                        const int64_t* tokens, int64_t rows, int64_t* decisions, ls_stream_t stream) {
+  if (rows < 0) return fail(LS_ERR_VALUE, "verify_decisions: invalid rows");
+  if (rows == 0) return LS_OK;
+  if (!target_masses || !proposal_masses || !uniforms || !tokens || !decisions)
+    return fail(LS_ERR_VALUE, "verify_decisions: NULL pointer");
+  hipLaunchKernelGGL(verify_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), target_masses, proposal_masses, uniforms, tokens, rows,
+                     decisions);
+  return check_launch("verify_decisions launch");
+}
+
+int ls_rejection(const float* first, int64_t first_stride, const float* target, int64_t target_stride,
+                 const float* second, int64_t second_stride, const int64_t* metadata, const float* uniforms,
+                 int64_t rows, int64_t vocab, int64_t* out, ls_stream_t stream) {
+  if (rows < 0 || vocab <= 0) return fail(LS_ERR_VALUE, "rejection: invalid shape");
+  if (rows == 0) return LS_OK;
+  if (!first || !target || !second || !metadata || !uniforms || !out)
+    return fail(LS_ERR_VALUE, "rejection: NULL pointer");
+  RejParams p{first, first_stride, target, target_stride, second, second_stride, metadata, uniforms, vocab, out};
+  hipLaunchKernelGGL(rejection_kernel, dim3(static_cast<unsigned>(rows)), dim3(kDB), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return check_launch("rejection launch");
+}
+
+int ls_top_k_filter(const float* probs, int64_t row_stride, int64_t rows, int64_t vocab, int64_t k,
+                    const float* cutoff_in, float* filtered, int64_t out_stride, float* cutoff_out,
+                    ls_stream_t stream) {
+  if (rows < 0 || vocab <= 0 || k < 1 || k > vocab) return fail(LS_ERR_VALUE, "top_k_filter: invalid shape or k");
+  if (rows == 0) return LS_OK;
+  if (!probs || !filtered) return fail(LS_ERR_VALUE, "top_k_filter: NULL pointer");
+  hipLaunchKernelGGL(top_k_filter_kernel, dim3(static_cast<unsigned>(rows)), dim3(kDB), 0,
+                     static_cast<hipStream_t>(stream), probs, row_stride, vocab, k, cutoff_in, filtered, out_stride,
+                     cutoff_out);
+  return check_launch("top_k_filter launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,293 @@
+// (d) KV-slot bookkeeping and the branch -> main KV-timeline commit, gfx950.
+//
+//  allocate_decode_slots   one workgroup: exclusive rank of valid rows in batch
+//                          order, ring lookup, cursor advance
+//                          (sglang_recurrent/loopspec/graph_ops.py:97-172)
+//  update_request_mapping  prefix copy of a parent's mapping row and the append
+//                          of the new slot (graph_ops.py:175-271)
+//  copy_state_rows         gather/scatter of state-bank rows (graph_ops.py:20-94)
+//  kv_commit_plan          page allocation for accepted tokens (batch-ordered
+//                          exclusive scan over the rows' new-page counts into a
+//                          free-page ring) and destination slots
+//  kv_commit_copy          16-byte copies of every plane's token row, branch
+//                          slot -> main-timeline slot
+// All integer work is exact; every kernel bounds-checks slot and page ids and
+// skips (and reports) entries that fall outside the tables it was given.
+#include "ls_common.hpp"
+#include "ls_runtime.hpp"
+
+namespace ls {
+namespace {
+
+constexpr int kScanBlock = 1024;
+constexpr int kCopyBlock = 256;
+
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Exclusive scan over a 1024-lane block; *total receives the sum.
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* smem, uint32_t* total) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const uint32_t inc = wave_incl_scan_u32(v, lane);
+  __syncthreads();
+  if (lane == kWave - 1) smem[wid] = inc;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kScanBlock / kWave; ++i) {
+    const uint32_t s = smem[i];
+    base += i < wid ? s : 0u;
+    tot += s;
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+__global__ __launch_bounds__(kScanBlock) void allocate_slots_kernel(const int64_t* __restrict__ free_slots,
+                                                                     int64_t capacity, int64_t* cursor,
+                                                                     const int64_t* __restrict__ markers,
+                                                                     int64_t batch, int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t base = *cursor;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
+    const int64_t b = b0 + threadIdx.x;
+    const bool valid = b < batch && markers[b] >= 0;
+    uint32_t total;
+    const uint32_t rank = block_excl_scan_u32(valid ? 1u : 0u, red, &total);
+    if (valid) {
+      int64_t off = (base + carry + rank) % capacity;
+      off += off < 0 ? capacity : 0;
+      out[b] = free_slots[off];
+    }
+    carry += total;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *cursor = base + carry;
+}
+
+__global__ __launch_bounds__(kCopyBlock) void update_mapping_kernel(int32_t* __restrict__ mapping, int64_t stride,
+                                                                    int64_t max_ctx,
+                                                                    const int64_t* __restrict__ rows,
+                                                                    const int64_t* __restrict__ sources,
+                                                                    const int64_t* __restrict__ copy_lens,
+                                                                    const int64_t* __restrict__ positions,
+                                                                    const int64_t* __restrict__ slots,
+                                                                    int64_t span) {
+  const int64_t b = blockIdx.y;
+  const int64_t c = copy_lens[b];
+  if (c < 0) return;
+  const int64_t dst = rows[b], src = sources[b];
+  const int64_t lim = c < max_ctx ? c : max_ctx;
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * span;
+  const int64_t stop = start + span < lim ? start + span : lim;
+  int32_t* d = mapping + dst * stride;
+  const int32_t* s = mapping + src * stride;
+  for (int64_t i = start + threadIdx.x; i < stop; i += kCopyBlock) d[i] = s[i];
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int64_t pos = positions[b];
+    if (pos >= 0 && pos < max_ctx) d[pos] = static_cast<int32_t>(slots[b]);
+  }
+}
+
+template <int UNIT>
+__global__ __launch_bounds__(kCopyBlock) void copy_rows_kernel(const char* __restrict__ src, char* __restrict__ dst,
+                                                               const int64_t* __restrict__ idx, int64_t width_bytes,
+                                                               int64_t nrows_bank, int gather) {
+  const int64_t b = blockIdx.y;
+  const int64_t r = idx[b];
+  if (r < 0 || r >= nrows_bank) return;
+  const int64_t from = gather ? r : b, to = gather ? b : r;
+  const char* s = src + from * width_bytes;
+  char* d = dst + to * width_bytes;
+  const int64_t units = width_bytes / UNIT;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * kCopyBlock + threadIdx.x; u < units;
+       u += static_cast<int64_t>(gridDim.x) * kCopyBlock) {
+    if constexpr (UNIT == 16) {
+      reinterpret_cast<u32x4*>(d)[u] = reinterpret_cast<const u32x4*>(s)[u];
+    } else if constexpr (UNIT == 4) {
+      reinterpret_cast<uint32_t*>(d)[u] = reinterpret_cast<const uint32_t*>(s)[u];
+    } else {
+      d[u] = s[u];
+    }
+  }
+}
+
+// Page allocation and destination slots for the commit (one workgroup).
+__global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
+    const int32_t* __restrict__ accept_len, int64_t batch, int k, int page_size, int64_t max_pages,
+    int64_t num_pages, int32_t* __restrict__ page_table, int64_t* __restrict__ ctx_len,
+    const int64_t* __restrict__ free_pages, int64_t ring, int64_t* page_cursor, int64_t* __restrict__ dst_slots,
+    int32_t* status) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t base = *page_cursor;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
+    const int64_t b = b0 + threadIdx.x;
+    int64_t a = 0, ctx = 0, owned = 0, need = 0;
+    if (b < batch) {
+      a = accept_len[b];
+      a = a < 0 ? 0 : (a > k ? k : a);
+      ctx = ctx_len[b];
+      owned = (ctx + page_size - 1) / page_size;
+      const int64_t pages_after = (ctx + a + page_size - 1) / page_size;
+      need = pages_after > owned ? pages_after - owned : 0;
+    }
+    uint32_t total;
+    const uint32_t excl = block_excl_scan_u32(static_cast<uint32_t>(need), red, &total);
+    if (b < batch) {
+      bool bad = false;
+      int32_t* pt = page_table + b * max_pages;
+      for (int64_t i = 0; i < need; ++i) {
+        const int64_t pidx = owned + i;
+        int64_t ro = (base + carry + excl + i) % ring;
+        ro += ro < 0 ? ring : 0;
+        const int64_t page = free_pages[ro];
+        if (pidx < max_pages) {
+          pt[pidx] = static_cast<int32_t>(page);
+        } else {
+          bad = true;
+        }
+      }
+      for (int j = 0; j < k; ++j) {
+        int64_t slot = -1;
+        if (j < a) {
+          const int64_t pos = ctx + j;
+          const int64_t pidx = pos / page_size;
+          const int64_t page = pidx < max_pages ? pt[pidx] : -1;
+          if (page >= 0 && page < num_pages) {
+            slot = page * page_size + pos % page_size;
+          } else {
+            bad = true;
+          }
+        }
+        dst_slots[b * k + j] = slot;
+      }
+      ctx_len[b] = ctx + a;
+      if (bad && status) atomicOr(status, 1);
+    }
+    carry += total;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *page_cursor = base + carry;
+}
+
+// One workgroup per (token, group of planes): copy the token's row of every
+// plane in the group from its branch slot to its destination slot.
+__global__ __launch_bounds__(kCopyBlock) void kv_copy_kernel(char* __restrict__ kv, int64_t planes,
+                                                             int64_t plane_stride, int64_t token_bytes,
+                                                             int64_t num_slots, const int64_t* __restrict__ src_slots,
+                                                             const int64_t* __restrict__ dst_slots, int planes_per_wg) {
+  const int64_t tok = blockIdx.y;
+  const int64_t d = dst_slots[tok];
+  const int64_t s = src_slots[tok];
+  if (d < 0 || d >= num_slots || s < 0 || s >= num_slots) return;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * planes_per_wg;
+  const int64_t p1 = p0 + planes_per_wg < planes ? p0 + planes_per_wg : planes;
+  const int64_t vecs = token_bytes / 16;
+  for (int64_t p = p0; p < p1; ++p) {
+    const u32x4* from = reinterpret_cast<const u32x4*>(kv + p * plane_stride + s * token_bytes);
+    u32x4* to = reinterpret_cast<u32x4*>(kv + p * plane_stride + d * token_bytes);
+    for (int64_t v = threadIdx.x; v < vecs; v += kCopyBlock) __builtin_nontemporal_store(__builtin_nontemporal_load(from + v), to + v);
+  }
+}
+
+}  // namespace
+}  // namespace ls
+
+using namespace ls;
+
+extern "C" {
+
+int ls_allocate_decode_slots(const int64_t* free_slots, int64_t capacity, int64_t* allocation_cursor,
+                             const int64_t* valid_markers, int64_t batch, int64_t* out_cache_locs,
+                             ls_stream_t stream) {
+  if (batch < 0 || capacity <= 0) return fail(LS_ERR_VALUE, "allocate_decode_slots: B and C must be positive");
+  if (batch == 0) return LS_OK;
+  if (!free_slots || !allocation_cursor || !valid_markers || !out_cache_locs)
+    return fail(LS_ERR_VALUE, "allocate_decode_slots: NULL pointer");
+  hipLaunchKernelGGL(allocate_slots_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream),
+                     free_slots, capacity, allocation_cursor, valid_markers, batch, out_cache_locs);
+  return check_launch("allocate_decode_slots launch");
+}
+
+int ls_update_request_mapping(int32_t* mapping, int64_t mapping_stride, int64_t max_context_len,
+                              const int64_t* request_rows, const int64_t* source_rows, const int64_t* copy_lens,
+                              const int64_t* positions, const int64_t* out_cache_locs, int64_t batch,
+                              ls_stream_t stream) {
+  if (batch < 0 || max_context_len <= 0 || mapping_stride < max_context_len)
+    return fail(LS_ERR_VALUE, "update_request_mapping: invalid shape");
+  if (batch == 0) return LS_OK;
+  if (!mapping || !request_rows || !source_rows || !copy_lens || !positions || !out_cache_locs)
+    return fail(LS_ERR_VALUE, "update_request_mapping: NULL pointer");
+  if (batch > 65535) return fail(LS_ERR_VALUE, "update_request_mapping: batch too large");
+  const int64_t span = 4096;  // entries per workgroup
+  const int64_t gx = (max_context_len + span - 1) / span;
+  hipLaunchKernelGGL(update_mapping_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(batch)),
+                     dim3(kCopyBlock), 0, static_cast<hipStream_t>(stream), mapping, mapping_stride,
+                     max_context_len, request_rows, source_rows, copy_lens, positions, out_cache_locs, span);
+  return check_launch("update_request_mapping launch");
+}
+
+int ls_copy_state_rows(const void* source, void* destination, const int64_t* row_indices, int64_t batch,
+                       int64_t bank_rows, int64_t width_bytes, int gather, ls_stream_t stream) {
+  if (batch < 0 || width_bytes <= 0 || bank_rows < 0) return fail(LS_ERR_VALUE, "copy_state_rows: invalid shape");
+  if (batch == 0) return LS_OK;
+  if (!source || !destination || !row_indices) return fail(LS_ERR_VALUE, "copy_state_rows: NULL pointer");
+  if (batch > 65535) return fail(LS_ERR_VALUE, "copy_state_rows: batch too large");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(source) | reinterpret_cast<uintptr_t>(destination) |
+                       static_cast<uintptr_t>(width_bytes);
+  const int unit = (al % 16 == 0) ? 16 : ((al % 4 == 0) ? 4 : 1);
+  const int64_t units = width_bytes / unit;
+  int64_t gx = (units + kCopyBlock - 1) / kCopyBlock;
+  if (gx > 64) gx = 64;
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(batch));
+  const auto st = static_cast<hipStream_t>(stream);
+  const char* s = static_cast<const char*>(source);
+  char* d = static_cast<char*>(destination);
+  if (unit == 16) {
+    hipLaunchKernelGGL(copy_rows_kernel<16>, grid, dim3(kCopyBlock), 0, st, s, d, row_indices, width_bytes, bank_rows, gather);
+  } else if (unit == 4) {
+    hipLaunchKernelGGL(copy_rows_kernel<4>, grid, dim3(kCopyBlock), 0, st, s, d, row_indices, width_bytes, bank_rows, gather);
+  } else {
+    hipLaunchKernelGGL(copy_rows_kernel<1>, grid, dim3(kCopyBlock), 0, st, s, d, row_indices, width_bytes, bank_rows, gather);
+  }
+  return check_launch("copy_state_rows launch");
+}
+
+int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t token_bytes, int64_t num_pages,
+                 int64_t page_size, const int32_t* accept_len, const int64_t* branch_slots, int64_t batch, int64_t k,
+                 int32_t* page_table, int64_t max_pages, int64_t* ctx_len, const int64_t* free_pages,
+                 int64_t ring_size, int64_t* page_cursor, int64_t* dst_slots, int32_t* status, ls_stream_t stream) {
+  if (batch < 0 || k < 1 || k > 64 || page_size <= 0 || page_size > (1 << 20) || max_pages <= 0 || num_pages <= 0 ||
+      ring_size <= 0 ||
+      planes < 0 || token_bytes <= 0)
+    return fail(LS_ERR_VALUE, "kv_commit: invalid shape");
+  if (batch == 0) return LS_OK;
+  if (!accept_len || !branch_slots || !page_table || !ctx_len || !free_pages || !page_cursor || !dst_slots)
+    return fail(LS_ERR_VALUE, "kv_commit: NULL pointer");
+  if (planes > 0 && (!kv || token_bytes % 16 != 0 || plane_stride_bytes % 16 != 0 || !aligned16(kv)))
+    return fail(LS_ERR_VALUE, "kv_commit: KV rows must be 16-byte aligned multiples of 16 bytes");
+  if (num_pages > 0x7fffffffLL) return fail(LS_ERR_VALUE, "kv_commit: page ids must fit int32");
+  if (batch * k > 65535) return fail(LS_ERR_VALUE, "kv_commit: too many tokens");
+  const auto st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(kv_plan_kernel, dim3(1), dim3(kScanBlock), 0, st, accept_len, batch, static_cast<int>(k),
+                     static_cast<int>(page_size), max_pages, num_pages, page_table, ctx_len, free_pages, ring_size,
+                     page_cursor, dst_slots, status);
+  int rc = check_launch("kv_commit plan launch");
+  if (rc || planes == 0) return rc;
+  const int ppw = 8;
+  const int64_t gx = (planes + ppw - 1) / ppw;
+  hipLaunchKernelGGL(kv_copy_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(batch * k)),
+                     dim3(kCopyBlock), 0, st, static_cast<char*>(kv), planes, plane_stride_bytes, token_bytes,
+                     num_pages * page_size, branch_slots, dst_slots, ppw);
+  return check_launch("kv_commit copy launch");
+}
+
+}  // extern "C"

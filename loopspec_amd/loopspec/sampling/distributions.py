@@ -1,0 +1,117 @@
+"""Filter endpoint logits and sample token ids without host readback (drop-in).
+
+Same functions, arguments and results as the reference
+(sglang_recurrent/loopspec/sampling/distributions.py:14-171). Softmax,
+temperature and the top-p cutoff run in one fused gfx950 pass per row (no sort:
+the cutoff is found by a mass-ordered radix select in LDS); joint top-k/top-p
+adds one row pass for the k-th largest value. The arithmetic is the library's
+declared one (a fixed polynomial exp, exact 2^-46 fixed-point masses), so
+values agree with the reference's float32 torch path to rounding while the
+cutoff rule, ties included, is the same.
+
+The top-p context returned by prepare_sampling_probabilities keeps arity 3 but
+carries (unfiltered probs [B, V], cutoff values [B, 1], zero ranks [B, 1]) in
+place of a sorted copy of the probabilities: sorted[r, rank[r]] still locates
+each row's cutoff, for this module's CategoricalSampler.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from ... import _lib
+
+
+def _thresholds(top_p_thresholds: torch.Tensor | None, rows: int, top_p: float) -> torch.Tensor | None:
+    if top_p_thresholds is None or top_p >= 1:
+        return None
+    t = top_p_thresholds[:rows]
+    if t.dtype != torch.float32:
+        raise ValueError("top_p_thresholds must be float32 [N, 1]")
+    t = t.reshape(-1)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _filter(logits: torch.Tensor, temperature: float, top_p: float, thresholds: torch.Tensor | None, *,
+            probs: torch.Tensor | None, filtered: torch.Tensor | None, cutoff: torch.Tensor | None) -> None:
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with a contiguous vocabulary axis")
+    rows, vocab = logits.shape
+    if rows == 0:
+        return
+    mass = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    if cutoff is None:
+        cutoff = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _lib.call(
+        "ls_filter_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
+        float(temperature), float(top_p), _lib.ptr(thresholds), 0,
+        _lib.ptr(probs), probs.stride(0) if probs is not None else 0,
+        _lib.ptr(filtered), filtered.stride(0) if filtered is not None else 0,
+        cutoff.data_ptr(), mass.data_ptr(), _lib.stream(logits.device),
+    )
+
+
+def filtered_probabilities(logits: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                           top_p_thresholds: torch.Tensor | None = None) -> torch.Tensor:
+    """Filtered, normalised CUDA float32 probabilities [B, V] (distributions.py:14-86).
+
+    top_k = 0 or >= V disables top-k; top_p = 1 disables top-p; per-row
+    thresholds [N, 1] (N >= B) replace top_p when top_p < 1.
+    """
+    if not logits.is_cuda:
+        raise RuntimeError("LoopSpec sampling requires CUDA logits")
+    rows, vocab = logits.shape
+    effective_top_k = 0 if top_k >= vocab else top_k
+    thresholds = _thresholds(top_p_thresholds, rows, top_p)
+    out = torch.empty((rows, vocab), dtype=torch.float32, device=logits.device)
+    if effective_top_k == 0:
+        _filter(logits, temperature, top_p, thresholds, probs=None, filtered=out, cutoff=None)
+        return out
+    # Top-k (alone or with top-p): the k-th largest probability, combined with
+    # the top-p cutoff of the same unfiltered softmax, renormalised once.
+    probs = torch.empty_like(out)
+    cutoff = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _filter(logits, temperature, top_p, thresholds, probs=probs, filtered=None, cutoff=cutoff)
+    if rows:
+        _lib.call(
+            "ls_top_k_filter", probs.data_ptr(), probs.stride(0), rows, vocab, int(effective_top_k),
+            cutoff.data_ptr() if top_p < 1 else None, out.data_ptr(), out.stride(0), None,
+            _lib.stream(logits.device),
+        )
+    return out
+
+
+def prepare_sampling_probabilities(logits: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                                   sampler: Any, *, top_p_thresholds: torch.Tensor | None = None):
+    """(filtered probabilities [B, V], top-p context or None) (distributions.py:89-149).
+
+    The context exists on the top-p-only path and feeds sampler.sample_top_p;
+    no RNG is used and no token is drawn here.
+    """
+    vocab = logits.shape[-1]
+    effective_top_k = 0 if top_k >= vocab else top_k
+    if not logits.is_cuda:
+        raise RuntimeError("LoopSpec sampling requires CUDA logits")
+    if effective_top_k == 0 and top_p < 1:
+        rows = logits.shape[0]
+        if rows > sampler.max_rows or vocab != sampler.vocabulary_size:
+            raise ValueError("categorical sampler workspace shape mismatch")
+        thresholds = _thresholds(top_p_thresholds, rows, top_p)
+        probs = torch.empty((rows, vocab), dtype=torch.float32, device=logits.device)
+        normalized = torch.empty_like(probs)
+        cutoffs = torch.empty((rows, 1), dtype=torch.float32, device=logits.device)
+        _filter(logits, temperature, top_p, thresholds, probs=probs, filtered=normalized, cutoff=cutoffs)
+        ranks = torch.zeros((rows, 1), dtype=torch.int64, device=logits.device)
+        return normalized, (probs, cutoffs, ranks)
+    return filtered_probabilities(logits, temperature, effective_top_k, top_p,
+                                  top_p_thresholds=top_p_thresholds), None
+
+
+def sample_probabilities(probs: torch.Tensor, generator: torch.Generator | None, sampler: Any, *,
+                         result_slot: int = 0) -> torch.Tensor:
+    """One token id per row as a CUDA int64 [B] workspace view (distributions.py:152-171)."""
+    if not probs.is_cuda:
+        raise RuntimeError("LoopSpec sampling requires CUDA probabilities")
+    return sampler.sample(probs, generator, result_slot=result_slot)

@@ -1,0 +1,120 @@
+"""RejectionSampler drop-in: residual fallback after a rejected q1 proposal.
+
+Same buffers, capture protocol and queue() contract as the reference
+(sglang_recurrent/loopspec/sampling/rejection.py:18-182). The whole fallback
+(_run: F = normalize(max(P - Q1, 0)), the q2 test against R, the second
+residual and the fallback draw) is one gfx950 kernel, so the captured graph is
+a single node. ``queue_many`` handles several rejected rows with one launch
+while drawing the uniforms exactly as repeated ``queue`` calls would
+(two per row, in row order).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable, Sequence
+
+import torch
+
+from ... import _lib
+
+
+class RejectionSampler:
+    """Own fixed buffers and the HIP graph for q1 rejection handling."""
+
+    def __init__(self, vocabulary_size: int, device: torch.device | str | int,
+                 sample_with_uniforms: Callable[[torch.Tensor, torch.Tensor, torch.Tensor], torch.Tensor]) -> None:
+        self.vocabulary_size = vocabulary_size
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("LoopSpec rejection sampling requires CUDA")
+        # Kept for interface parity; the fused kernel performs the draw itself.
+        self.sample_with_uniforms = sample_with_uniforms
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def _launch(self, first: torch.Tensor, target: torch.Tensor, second: torch.Tensor, metadata: torch.Tensor,
+                uniforms: torch.Tensor, result: torch.Tensor, rows: int) -> None:
+        _lib.call(
+            "ls_rejection", first.data_ptr(), first.stride(0), target.data_ptr(), target.stride(0),
+            second.data_ptr(), second.stride(0), metadata.data_ptr(), uniforms.data_ptr(), rows,
+            self.vocabulary_size, result.data_ptr(), _lib.stream(self.device),
+        )
+
+    def _run(self) -> None:
+        """Fallback for the staged row into self.result [1, 3] (rejection.py:42-97)."""
+        self._launch(self.first, self.target, self.second, self.metadata, self.uniforms, self.result, 1)
+
+    def capture(self) -> None:
+        """Allocate stable buffers, warm the kernel and capture it once (rejection.py:99-139)."""
+        if self.graph is not None:
+            return
+        v = self.vocabulary_size
+        self.first = torch.zeros((1, v), dtype=torch.float32, device=self.device)
+        self.target = torch.zeros_like(self.first)
+        self.target[:, 0] = 1
+        self.second = torch.zeros_like(self.first)
+        self.metadata = torch.zeros(2, dtype=torch.int64, device=self.device)
+        self.metadata_host = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+        self.uniforms = torch.zeros(2, dtype=torch.float32, device=self.device)
+        self.result = torch.zeros((1, 3), dtype=torch.int64, device=self.device)
+        capture_stream = torch.cuda.Stream(device=self.device)
+        capture_stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(capture_stream):
+            for _ in range(3):
+                self._run()
+        capture_stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=capture_stream):
+            self._run()
+        torch.cuda.current_stream(self.device).wait_stream(capture_stream)
+        self.graph = graph
+
+    def queue(self, first_proposal: torch.Tensor, target: torch.Tensor, second_token: int | None,
+              second_proposal: torch.Tensor | None, generator: torch.Generator | None,
+              output_host: torch.Tensor) -> None:
+        """Stage one rejection, replay the graph, enqueue the host copy (rejection.py:141-182)."""
+        if self.graph is None:
+            raise RuntimeError("sampling rejection CUDA graph was not captured")
+        self.first[0].copy_(first_proposal)
+        self.target[0].copy_(target)
+        has_second = second_proposal is not None
+        if has_second:
+            self.second[0].copy_(second_proposal)
+        self.metadata_host[0] = 0 if second_token is None else second_token
+        self.metadata_host[1] = int(has_second)
+        self.metadata.copy_(self.metadata_host, non_blocking=True)
+        torch.rand(2, out=self.uniforms, generator=generator)
+        self.graph.replay()
+        output_host.copy_(self.result[0], non_blocking=True)
+
+    def queue_many(self, first_proposals: Sequence[torch.Tensor], targets: Sequence[torch.Tensor],
+                   second_tokens: Sequence[int | None], second_proposals: Sequence[torch.Tensor | None],
+                   generator: torch.Generator | None, output_host: torch.Tensor) -> None:
+        """Handle R rejected rows in one launch; output_host is pinned int64 [>=R, 3].
+
+        Consumes 2 uniforms per row in row order, like R calls of queue().
+        """
+        rows = len(first_proposals)
+        if rows == 0:
+            return
+        if not (len(targets) == len(second_tokens) == len(second_proposals) == rows):
+            raise ValueError("queue_many: per-row sequences must have equal length")
+        first = torch.stack(list(first_proposals)).float()
+        target = torch.stack(list(targets)).float()
+        zero = None
+        seconds = []
+        for s in second_proposals:
+            if s is None:
+                if zero is None:
+                    zero = torch.zeros(self.vocabulary_size, dtype=torch.float32, device=self.device)
+                s = zero
+            seconds.append(s)
+        second = torch.stack(seconds).float()
+        meta_host = torch.tensor([[0 if t is None else int(t), int(s is not None)]
+                                  for t, s in zip(second_tokens, second_proposals)], dtype=torch.int64)
+        metadata = meta_host.to(self.device)
+        uniforms = torch.empty((rows, 2), dtype=torch.float32, device=self.device)
+        for i in range(rows):
+            torch.rand(2, out=uniforms[i], generator=generator)
+        result = torch.empty((rows, 3), dtype=torch.int64, device=self.device)
+        self._launch(first, target, second, metadata, uniforms, result, rows)
+        output_host[:rows].copy_(result, non_blocking=True)

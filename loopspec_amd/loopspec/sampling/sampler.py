@@ -1,0 +1,217 @@
+"""CategoricalSampler drop-in: reusable workspace + gfx950 sampling kernels.
+
+Keeps the reference's constructor, methods, result-slot semantics, RNG
+consumption (one ``torch.rand`` per call, of the same length, into the same
+uniforms buffer) and error behaviour
+(sglang_recurrent/loopspec/sampling/sampler.py:463-905). The Triton chunk-sum
+and pick kernels are replaced by one 1024-lane workgroup per row that computes
+exact 2^-46 fixed-point masses, so a draw is the first index j with
+cum(j) > floor(u * total): the reference's inverse-CDF rule without its float32
+summation-order dependence.
+
+Token ids, actions and decisions returned here are views into the sampler's
+workspace, valid until the same slot is written again; normalised
+distributions are new tensors. Calls must be serialised on one stream.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import _lib
+from .rejection import RejectionSampler
+
+
+def _prob_rows(t: torch.Tensor, what: str) -> None:
+    _lib.require_cuda(t, what)
+    if t.dtype != torch.float32 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{what}: expected CUDA float32 [B, V] with contiguous columns")
+
+
+def _cutoff_args(sorted_probabilities: torch.Tensor, cutoff_indices: torch.Tensor, rows: int):
+    """Pointer/stride pairs that locate each row's cutoff value
+    sorted_probabilities[r, cutoff_indices[r]] (cutoff_indices [B] or [B, 1])."""
+    _lib.require_cuda(sorted_probabilities, "sorted probabilities")
+    _lib.require_cuda(cutoff_indices, "cutoff indices")
+    if sorted_probabilities.dtype != torch.float32 or sorted_probabilities.stride(-1) != 1:
+        raise ValueError("sorted probabilities must be float32 with contiguous columns")
+    if cutoff_indices.dtype != torch.int64:
+        raise ValueError("cutoff indices must be int64")
+    if cutoff_indices.shape[0] < rows or sorted_probabilities.shape[0] < rows:
+        raise ValueError("top-p context has fewer rows than the probabilities")
+    cstride = cutoff_indices.stride(0)
+    return (sorted_probabilities.data_ptr(), sorted_probabilities.stride(0), cutoff_indices.data_ptr(), cstride)
+
+
+class CategoricalSampler:
+    """Own CUDA scratch/output buffers shared by one serialized sampler
+    (sglang_recurrent/loopspec/sampling/sampler.py:463-506)."""
+
+    def __init__(self, max_rows: int, vocabulary_size: int, device: torch.device | str | int, *,
+                 result_slots: int = 3) -> None:
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("LoopSpec categorical sampling requires CUDA")
+        if max_rows <= 0 or vocabulary_size <= 0 or result_slots <= 0:
+            raise ValueError("categorical sampler dimensions must be positive")
+        _lib.load()
+        self.max_rows = max_rows
+        self.vocabulary_size = vocabulary_size
+        self.device = device
+        self.uniforms = torch.empty(max_rows, dtype=torch.float32, device=device)
+        self.samples = torch.empty((result_slots, max_rows), dtype=torch.int64, device=device)
+        self.verification_decisions = torch.empty((max_rows, 5), dtype=torch.int64, device=device)
+        self.proposal_actions = torch.empty(max_rows, dtype=torch.int64, device=device)
+        self.rejections = RejectionSampler(vocabulary_size, device, self._sample_with_uniforms)
+
+    def _check(self, rows: int, vocabulary_size: int) -> None:
+        if rows > self.max_rows or vocabulary_size != self.vocabulary_size:
+            raise ValueError("categorical sampler workspace shape mismatch")
+
+    def sample(self, probabilities: torch.Tensor, generator: torch.Generator | None = None, *,
+               result_slot: int = 0) -> torch.Tensor:
+        """One token per [B, V] row into samples[result_slot, :B] (sampler.py:508-550)."""
+        _prob_rows(probabilities, "sample")
+        rows, vocabulary_size = probabilities.shape
+        self._check(rows, vocabulary_size)
+        torch.rand(rows, out=self.uniforms[:rows], generator=generator)
+        samples = self.samples[result_slot, :rows]
+        return self._sample_with_uniforms(probabilities, self.uniforms[:rows], samples)
+
+    def _sample_with_uniforms(self, probabilities: torch.Tensor, uniforms: torch.Tensor,
+                              samples: torch.Tensor) -> torch.Tensor:
+        """Fill caller-owned ids from supplied uniforms; no RNG (sampler.py:552-588)."""
+        rows, vocabulary_size = probabilities.shape
+        if rows:
+            _lib.call(
+                "ls_sample_probs", probabilities.data_ptr(), probabilities.stride(0), rows, vocabulary_size,
+                uniforms.data_ptr(), None, rows, samples.data_ptr(), _lib.stream(probabilities.device),
+            )
+        return samples
+
+    def capture_rejection_graph(self) -> None:
+        """Allocate, warm and capture the rejection fallback (sampler.py:590-598)."""
+        self.rejections.capture()
+
+    def queue_rejection(self, first_proposal: torch.Tensor, target: torch.Tensor, second_token: int | None,
+                        second_proposal: torch.Tensor | None, generator: torch.Generator | None,
+                        output_host: torch.Tensor) -> None:
+        """Queue one rejected q1's fallback and its host copy (sampler.py:600-627)."""
+        self.rejections.queue(first_proposal, target, second_token, second_proposal, generator, output_host)
+
+    def sample_conditional_residual(self, first_probabilities: torch.Tensor, second_probabilities: torch.Tensor,
+                                    selected_tokens: torch.Tensor, generator: torch.Generator | None = None, *,
+                                    result_slot: int = 0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(normalised residual [B, V], actions view, candidate ids view) for q2
+        (sampler.py:629-703): r = max(q2 - q1, 0) with r[x] = 0."""
+        _prob_rows(second_probabilities, "sample_conditional_residual")
+        _prob_rows(first_probabilities, "sample_conditional_residual")
+        rows, vocabulary_size = second_probabilities.shape
+        if first_probabilities.shape != second_probabilities.shape:
+            raise ValueError("directional probability shapes must match")
+        self._check(rows, vocabulary_size)
+        torch.rand(rows, out=self.uniforms[:rows], generator=generator)
+        samples = self.samples[result_slot, :rows]
+        normalized = torch.empty_like(second_probabilities)
+        actions = self.proposal_actions[:rows]
+        if rows:
+            sel = selected_tokens if selected_tokens.dtype == torch.int64 else selected_tokens.to(torch.int64)
+            _lib.call(
+                "ls_conditional_residual", first_probabilities.data_ptr(), first_probabilities.stride(0),
+                second_probabilities.data_ptr(), second_probabilities.stride(0), sel.contiguous().data_ptr(),
+                rows, vocabulary_size, self.uniforms.data_ptr(), normalized.data_ptr(), normalized.stride(0),
+                actions.data_ptr(), samples.data_ptr(), _lib.stream(second_probabilities.device),
+            )
+        return normalized, actions, samples
+
+    def verify(self, target_masses: torch.Tensor, proposal_masses: torch.Tensor, tokens: torch.Tensor,
+               generator: torch.Generator | None = None) -> torch.Tensor:
+        """int64 [B, 5] decisions view: u < min(1, p[x]/q[x]) (sampler.py:705-735)."""
+        rows = target_masses.shape[0]
+        if rows > self.max_rows:
+            raise ValueError("categorical sampler workspace shape mismatch")
+        torch.rand(rows, out=self.uniforms[:rows], generator=generator)
+        decisions = self.verification_decisions[:rows]
+        if rows:
+            t = target_masses.float().contiguous()
+            q = proposal_masses.float().contiguous()
+            x = tokens.to(torch.int64).contiguous()
+            _lib.call(
+                "ls_verify_decisions", t.data_ptr(), q.data_ptr(), self.uniforms.data_ptr(), x.data_ptr(), rows,
+                decisions.data_ptr(), _lib.stream(self.device),
+            )
+        return decisions
+
+    def normalize_top_p_for_sampling(self, probabilities: torch.Tensor, sorted_probabilities: torch.Tensor,
+                                     cutoff_indices: torch.Tensor) -> torch.Tensor:
+        """New [B, V]: p >= cutoff ? p / retained mass : 0 (sampler.py:737-784).
+
+        The context may be the reference's (probs, sorted probs [B, V], ranks
+        [B, 1]) or the compact (probs, cutoff values [B, 1], zeros [B, 1]) that
+        prepare_sampling_probabilities returns; both locate the same cutoff.
+        """
+        _prob_rows(probabilities, "normalize_top_p_for_sampling")
+        rows, vocabulary_size = probabilities.shape
+        self._check(rows, vocabulary_size)
+        normalized = torch.empty_like(probabilities)
+        if rows:
+            sp, ss, ci, cs = _cutoff_args(sorted_probabilities, cutoff_indices, rows)
+            _lib.call(
+                "ls_normalize_top_p", probabilities.data_ptr(), probabilities.stride(0), sp, ss, ci, cs, rows,
+                vocabulary_size, normalized.data_ptr(), normalized.stride(0), _lib.stream(probabilities.device),
+            )
+        return normalized
+
+    def sample_top_p(self, probabilities: torch.Tensor, sorted_probabilities: torch.Tensor,
+                     cutoff_indices: torch.Tensor, generator: torch.Generator | None = None, *,
+                     result_slot: int = 0, sample_rows: torch.Tensor | None = None) -> torch.Tensor:
+        """int64 [S] ids drawn from the retained, unnormalised weights p >= cutoff
+        of the selected rows (sampler.py:786-837)."""
+        _prob_rows(probabilities, "sample_top_p")
+        rows, vocabulary_size = probabilities.shape
+        self._check(rows, vocabulary_size)
+        count = rows if sample_rows is None else sample_rows.shape[0]
+        if count > self.max_rows:
+            raise ValueError("categorical sampler workspace shape mismatch")
+        torch.rand(count, out=self.uniforms[:count], generator=generator)
+        samples = self.samples[result_slot, :count]
+        if count:
+            sp, ss, ci, cs = _cutoff_args(sorted_probabilities, cutoff_indices, rows)
+            sr = None
+            if sample_rows is not None:
+                _lib.require_cuda(sample_rows, "sample_rows")
+                if sample_rows.dtype != torch.int64 or not sample_rows.is_contiguous():
+                    raise ValueError("sample_rows must be contiguous int64")
+                sr = sample_rows.data_ptr()
+            _lib.call(
+                "ls_sample_top_p", probabilities.data_ptr(), probabilities.stride(0), sp, ss, ci, cs, rows,
+                vocabulary_size, self.uniforms.data_ptr(), sr, count, samples.data_ptr(),
+                _lib.stream(probabilities.device),
+            )
+        return samples
+
+    def warmup(self) -> None:
+        """Exercise sample / q2 residual / verify once, then synchronize (sampler.py:839-867)."""
+        probabilities = torch.zeros((1, self.vocabulary_size), dtype=torch.float32, device=self.device)
+        probabilities[:, 0] = 1
+        selected = torch.zeros(1, dtype=torch.int64, device=self.device)
+        generator = torch.Generator(device=self.device).manual_seed(0)
+        self.sample(probabilities, generator, result_slot=0)
+        self.sample_conditional_residual(probabilities, probabilities, selected, generator, result_slot=1)
+        mass = torch.ones(1, dtype=torch.float32, device=self.device)
+        token = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.verify(mass, mass, token, generator)
+        torch.cuda.synchronize(self.device)
+
+    def warmup_filtered(self, logits_dtype: torch.dtype = torch.bfloat16) -> None:
+        """Exercise top-p preparation and an indirect q1 draw (sampler.py:869-905)."""
+        from .distributions import prepare_sampling_probabilities
+
+        logits = torch.zeros((1, self.vocabulary_size), dtype=logits_dtype, device=self.device)
+        thresholds = torch.full((1, 1), 0.7, dtype=torch.float32, device=self.device)
+        _, context = prepare_sampling_probabilities(logits, temperature=1.0, top_k=1 << 30, top_p=0.7,
+                                                    top_p_thresholds=thresholds, sampler=self)
+        assert context is not None
+        self.sample_top_p(*context, torch.Generator(device=self.device).manual_seed(0), result_slot=2,
+                          sample_rows=torch.zeros(1, dtype=torch.int64, device=self.device))
+        torch.cuda.synchronize(self.device)

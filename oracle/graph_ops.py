@@ -1,0 +1,108 @@
+"""KV-slot and mapping oracle (integer semantics; numpy; test infrastructure).
+
+Pinned by: exhaustive small cases and closed forms in tests/test_oracle_graph_ops.py
+(every valid/skip pattern up to B=10, ring wrap-around, copy-length signs,
+gather/scatter with skips, paged commit against a page-walk restatement).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def allocate_decode_slots(free_slots: np.ndarray, cursor: int, valid_markers: np.ndarray):
+    """_allocate_decode_slots_kernel (sglang_recurrent/loopspec/graph_ops.py:97-134).
+
+    Rows with marker >= 0 take ring entries (cursor + exclusive_rank) % capacity
+    in batch order; skipped rows consume nothing and keep their output. The
+    cursor advances by the number of valid rows (it is monotonic; only the
+    table index wraps). Returns (slots for valid rows as {row: slot}, new cursor).
+    """
+    cap = len(free_slots)
+    out = {}
+    rank = 0
+    for b, m in enumerate(valid_markers):
+        if int(m) >= 0:
+            out[b] = int(free_slots[(cursor + rank) % cap])
+            rank += 1
+    return out, cursor + rank
+
+
+def update_request_mapping(mapping: np.ndarray, request_rows, source_rows, copy_lens, positions, out_cache_locs):
+    """_update_request_mapping_kernel (graph_ops.py:175-218), in place on an int32 table.
+
+    copy_len > 0 copies mapping[src, :copy_len] to mapping[dst, :copy_len];
+    copy_len >= 0 then appends mapping[dst, pos] = int32(slot); copy_len < 0
+    writes nothing for the row.
+    """
+    m = mapping
+    for b in range(len(request_rows)):
+        c = int(copy_lens[b])
+        if c < 0:
+            continue
+        dst, src = int(request_rows[b]), int(source_rows[b])
+        if c > 0:
+            m[dst, :c] = m[src, :c].copy()
+        m[dst, int(positions[b])] = np.int32(np.int64(out_cache_locs[b]).astype(np.int32))
+    return m
+
+
+def copy_state_rows(source: np.ndarray, destination: np.ndarray, row_indices, gather: bool):
+    """_copy_state_rows_kernel (graph_ops.py:20-94): gather dst[b] = src[idx[b]] or
+    scatter dst[idx[b]] = src[b]; negative indices skip the row."""
+    for b, r in enumerate(row_indices):
+        r = int(r)
+        if r < 0:
+            continue
+        if gather:
+            destination[b] = source[r]
+        else:
+            destination[r] = source[b]
+    return destination
+
+
+def kv_commit_plan(accept_len, branch_slots, page_table, ctx_len, free_pages, page_cursor: int, page_size: int):
+    """Paged commit of accepted draft tokens from the branch into the main timeline.
+
+    Row b appends its first accept_len[b] branch tokens at positions
+    ctx_len[b], ctx_len[b]+1, ... of its page table. A position in a page that
+    the row does not own yet (page index >= ceil(ctx_len / page_size)) takes the
+    next page of the free-page ring, in batch order and then page order, exactly
+    like allocate_decode_slots assigns ring entries (graph_ops.py:117-134). The
+    destination slot of position p is page_table[b, p // page_size] * page_size
+    + p % page_size. Returns (dst_slots [B, k] int64 with -1 for non-accepted
+    tokens, page_table', ctx_len', page_cursor') and leaves the inputs unchanged.
+    """
+    pt = np.array(page_table, copy=True)
+    cl = np.array(ctx_len, dtype=np.int64, copy=True)
+    B, k = np.asarray(branch_slots).shape
+    dst = np.full((B, k), -1, dtype=np.int64)
+    cap = len(free_pages)
+    cur = int(page_cursor)
+    for b in range(B):
+        a = int(accept_len[b])
+        owned = -(-int(cl[b]) // page_size)
+        for j in range(a):
+            pos = int(cl[b]) + j
+            pidx = pos // page_size
+            if pidx >= owned:
+                pt[b, pidx] = np.int32(free_pages[cur % cap])
+                cur += 1
+                owned += 1
+            dst[b, j] = int(pt[b, pidx]) * page_size + pos % page_size
+        cl[b] += a
+    return dst, pt, cl, cur
+
+
+def kv_commit_copy(kv: np.ndarray, branch_slots, dst_slots):
+    """Copy every plane's token row from each branch slot to its destination slot.
+
+    kv is [planes, slots, token_elems]; dst_slots -1 entries are skipped.
+    """
+    bs = np.asarray(branch_slots)
+    ds = np.asarray(dst_slots)
+    for b in range(bs.shape[0]):
+        for j in range(bs.shape[1]):
+            if ds[b, j] >= 0:
+                kv[:, ds[b, j]] = kv[:, bs[b, j]]
+    return kv

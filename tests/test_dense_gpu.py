@@ -1,0 +1,248 @@
+"""GPU parity of the CategoricalSampler / RejectionSampler / distributions
+drop-ins (loopspec_amd.loopspec.sampling) against the declared-arithmetic oracle.
+
+Uniforms are drawn by torch.rand from the caller's generator exactly as the
+reference does; the tests replay the same generator on the host side to know
+them. Token ids, actions and decisions must match bit-exactly; normalised
+distributions are produced in the same declared arithmetic and compared exactly.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nm
+from oracle import sampling as osmp
+from loopspec_amd.loopspec.sampling import distributions as dist
+from loopspec_amd.loopspec.sampling.sampler import CategoricalSampler
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def gen(gpu, seed):
+    return torch.Generator(device=gpu).manual_seed(seed)
+
+
+def uniforms_of(gpu, seed, n):
+    """The uniforms a fresh generator with `seed` yields for torch.rand(n)."""
+    u = torch.empty(n, dtype=torch.float32, device=gpu)
+    torch.rand(n, out=u, generator=gen(gpu, seed))
+    return u.cpu().numpy()
+
+
+def uniforms_seq(gpu, seed, sizes):
+    """Uniforms of successive torch.rand(n) calls on one generator (each call
+    advances the Philox offset on its own, so this differs from one larger call)."""
+    g = gen(gpu, seed)
+    out = []
+    for n in sizes:
+        u = torch.empty(n, dtype=torch.float32, device=gpu)
+        torch.rand(n, out=u, generator=g)
+        out.append(u.cpu().numpy())
+    return out
+
+
+def softmax_rows(rows, vocab, seed, scale=3.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.softmax(torch.randn(rows, vocab, generator=g) * scale, dim=-1)
+
+
+@pytest.mark.parametrize("vocab", [49152, 128256, 1000, 2049, 7])
+def test_sample_matches_oracle(gpu, vocab):
+    rows = 12
+    p = softmax_rows(rows, vocab, vocab)
+    p[3] = 0
+    p[3, vocab - 1] = 1.0  # one-hot at the last index
+    p[4] = 0  # zero mass -> index 0
+    s = CategoricalSampler(16, vocab, gpu)
+    announce(f"sampler.sample V={vocab}")
+    got = s.sample(p.to(gpu), gen(gpu, 5), result_slot=1).cpu().numpy()
+    u = uniforms_of(gpu, 5, rows)
+    want = osmp.sample_rows(p.numpy(), u)
+    assert np.array_equal(got, want)
+    assert got[3] == vocab - 1 and got[4] == 0
+    # The returned ids are a view of result slot 1.
+    assert s.samples[1, :rows].cpu().numpy().tolist() == got.tolist()
+
+
+def test_sample_strided_rows(gpu):
+    vocab = 4096
+    base = softmax_rows(8, 2 * vocab, 1)
+    p = base[:, :vocab]  # row stride 2V, unit column stride
+    s = CategoricalSampler(8, vocab, gpu)
+    got = s.sample(base.to(gpu)[:, :vocab], gen(gpu, 9)).cpu().numpy()
+    want = osmp.sample_rows(p.numpy(), uniforms_of(gpu, 9, 8))
+    assert np.array_equal(got, want)
+
+
+def test_sample_workspace_mismatch_raises(gpu):
+    s = CategoricalSampler(4, 100, gpu)
+    with pytest.raises(ValueError):
+        s.sample(torch.ones(5, 100, device=gpu) / 100)
+    with pytest.raises(ValueError):
+        s.sample(torch.ones(2, 101, device=gpu) / 101)
+    with pytest.raises(RuntimeError):
+        CategoricalSampler(4, 100, "cpu")
+
+
+@pytest.mark.parametrize("indirect", [False, True])
+def test_prepare_and_sample_top_p(gpu, indirect):
+    vocab, rows = 49152, 10
+    g = torch.Generator().manual_seed(3)
+    logits = (torch.randn(rows, vocab, generator=g) * 3).to(torch.bfloat16)
+    thr = torch.full((16, 1), 0.7, dtype=torch.float32)
+    thr[2, 0] = 0.05
+    thr[5, 0] = 0.999
+    s = CategoricalSampler(16, vocab, gpu)
+    announce(f"prepare+sample_top_p indirect={indirect}")
+    normalized, ctx = dist.prepare_sampling_probabilities(logits.to(gpu), 1.0, 1 << 30, 0.7, s,
+                                                          top_p_thresholds=thr.to(gpu))
+    assert ctx is not None and len(ctx) == 3
+    rows_sel = torch.tensor([7, 2, 2, 0, 9], dtype=torch.int64)
+    ids = s.sample_top_p(*ctx, gen(gpu, 11), result_slot=2,
+                         sample_rows=rows_sel.to(gpu) if indirect else None).cpu().numpy()
+    n = len(rows_sel) if indirect else rows
+    u = uniforms_of(gpu, 11, n)
+    probs = ctx[0].cpu().numpy()
+    cut = ctx[1].cpu().numpy()[:, 0]
+    for r in range(rows):
+        want = osmp.filter_row(logits[r].float().numpy(), float(thr[r, 0]))
+        assert np.array_equal(probs[r], want.soft.p)
+        assert cut[r] == want.cutoff
+        assert np.array_equal(normalized[r].cpu().numpy(), want.P)
+    want_ids = osmp.sample_top_p_rows(probs, cut, u, rows_sel.numpy() if indirect else None)
+    assert np.array_equal(ids, want_ids)
+    # normalize_top_p_for_sampling on the same context reproduces `normalized`.
+    again = s.normalize_top_p_for_sampling(*ctx)
+    assert torch.equal(again, normalized)
+
+
+def test_top_p_with_reference_sorted_context(gpu):
+    """The reference's own context (sorted probs, searchsorted ranks) works too."""
+    vocab, rows = 8192, 6
+    p = softmax_rows(rows, vocab, 4).to(gpu)
+    sorted_p = p.sort(dim=-1, descending=True).values
+    ranks = torch.tensor([[0], [5], [100], [vocab - 1], [17], [3]], dtype=torch.int64, device=gpu)
+    s = CategoricalSampler(rows, vocab, gpu)
+    normalized = s.normalize_top_p_for_sampling(p, sorted_p, ranks)
+    ids = s.sample_top_p(p, sorted_p, ranks, gen(gpu, 2)).cpu().numpy()
+    pc, sc, rc = p.cpu().numpy(), sorted_p.cpu().numpy(), ranks.cpu().numpy()[:, 0]
+    cut = np.array([sc[r, rc[r]] for r in range(rows)], dtype=np.float32)
+    for r in range(rows):
+        mass = osmp.retained_mass(pc[r], cut[r])
+        assert np.array_equal(normalized[r].cpu().numpy(), osmp.normalize_retained(pc[r], cut[r], mass))
+    assert np.array_equal(ids, osmp.sample_top_p_rows(pc, cut, uniforms_of(gpu, 2, rows)))
+
+
+def test_conditional_residual(gpu):
+    vocab, rows = 32000, 9
+    q1 = softmax_rows(rows, vocab, 5, 2.0)
+    q2 = softmax_rows(rows, vocab, 6, 2.0)
+    q2[4] = q1[4]  # zero residual mass -> zero row, action 0
+    x1 = torch.randint(0, vocab, (rows,), generator=torch.Generator().manual_seed(1))
+    s = CategoricalSampler(rows, vocab, gpu)
+    announce("conditional_residual")
+    R, act, ids = s.sample_conditional_residual(q1.to(gpu), q2.to(gpu), x1.to(gpu), gen(gpu, 4), result_slot=0)
+    wR, wact, wids = osmp.conditional_residual(q1.numpy(), q2.numpy(), x1.numpy(), uniforms_of(gpu, 4, rows))
+    assert np.array_equal(R.cpu().numpy(), wR)
+    assert np.array_equal(act.cpu().numpy(), wact)
+    assert np.array_equal(ids.cpu().numpy(), wids)
+    assert act[4].item() == 0 and not R[4].any()
+
+
+def test_verify_decisions(gpu):
+    rows = 300
+    g = torch.Generator().manual_seed(8)
+    p = torch.rand(rows, generator=g)
+    q = torch.rand(rows, generator=g) + 1e-3
+    p[:5] = torch.tensor([0.0, 1.0, float("nan"), 0.5, 0.2])
+    q[:5] = torch.tensor([0.5, 0.0, 0.3, 0.5, 0.2])
+    x = torch.randint(0, 1000, (rows,), generator=g)
+    s = CategoricalSampler(512, 1000, gpu)
+    dec = s.verify(p.to(gpu), q.to(gpu), x.to(gpu), gen(gpu, 12)).cpu().numpy()
+    want = osmp.verify_decisions(p.numpy(), q.numpy(), x.numpy(), uniforms_of(gpu, 12, rows))
+    assert np.array_equal(dec, want)
+
+
+@pytest.mark.parametrize("has_second", [False, True])
+def test_rejection_graph_and_batch(gpu, has_second):
+    vocab = 49152
+    s = CategoricalSampler(8, vocab, gpu)
+    s.capture_rejection_graph()
+    rows = 5
+    Q1 = softmax_rows(rows, vocab, 20, 2.0)
+    P = softmax_rows(rows, vocab, 21, 2.0)
+    R = softmax_rows(rows, vocab, 22, 2.0) if has_second else None
+    P[3] = Q1[3]  # zero first residual -> normalize(P) fallback
+    ys = [int(torch.argmax(R[r])) if has_second else None for r in range(rows)]
+    announce(f"rejection has_second={has_second}")
+    host = torch.zeros((rows, 3), dtype=torch.int64, pin_memory=True)
+    g = gen(gpu, 30)
+    for r in range(rows):
+        s.queue_rejection(Q1[r].to(gpu), P[r].to(gpu), ys[r], R[r].to(gpu) if has_second else None, g, host[r])
+    torch.cuda.synchronize()
+    u = np.stack(uniforms_seq(gpu, 30, [2] * rows))
+    for r in range(rows):
+        second = R[r].numpy() if has_second else np.zeros(vocab, np.float32)
+        want = osmp.rejection_run(Q1[r].numpy(), P[r].numpy(), second, ys[r] or 0, has_second, u[r, 0], u[r, 1])
+        assert tuple(host[r].tolist()) == want, r
+    # queue_many: one launch, same uniforms as the per-row replays.
+    host2 = torch.zeros((rows, 3), dtype=torch.int64, pin_memory=True)
+    s.rejections.queue_many([Q1[r].to(gpu) for r in range(rows)], [P[r].to(gpu) for r in range(rows)], ys,
+                            [R[r].to(gpu) if has_second else None for r in range(rows)], gen(gpu, 30), host2)
+    torch.cuda.synchronize()
+    assert torch.equal(host, host2)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(1, 1.0), (50, 1.0), (50, 0.9), (2000, 0.3), (7, 0.999)])
+def test_filtered_probabilities_top_k(gpu, top_k, top_p):
+    vocab, rows = 49152, 5
+    g = torch.Generator().manual_seed(top_k)
+    logits = torch.randn(rows, vocab, generator=g) * 3
+    logits[1, :100] = 9.0  # a run of equal top values straddling k
+    announce(f"filtered_probabilities top_k={top_k} top_p={top_p}")
+    out = dist.filtered_probabilities(logits.to(gpu), 0.8, top_k, top_p).cpu().numpy()
+    for r in range(rows):
+        x = osmp.process_logits(logits[r].numpy(), 0.8)
+        want = osmp.filter_row(x, top_p, top_k)
+        assert np.array_equal(out[r], want.P), r
+
+
+@pytest.mark.parametrize("temperature,top_p", [(1.0, 1.0), (0.7, 0.9)])
+def test_filtered_probabilities_plain(gpu, temperature, top_p):
+    vocab, rows = 128256, 3
+    logits = (torch.randn(rows, vocab, generator=torch.Generator().manual_seed(2)) * 4).to(torch.bfloat16)
+    out = dist.filtered_probabilities(logits.to(gpu), temperature, 0, top_p).cpu().numpy()
+    for r in range(rows):
+        want = osmp.filter_row(osmp.process_logits(logits[r].float().numpy(), temperature), top_p)
+        assert np.array_equal(out[r], want.P)
+
+
+def test_warmups_run(gpu):
+    s = CategoricalSampler(4, 49152, gpu)
+    s.warmup()
+    s.warmup_filtered(torch.bfloat16)
+    s.capture_rejection_graph()
+    s.capture_rejection_graph()  # second call is a no-op
+
+
+def test_rejection_queue_requires_capture(gpu):
+    s = CategoricalSampler(2, 100, gpu)
+    with pytest.raises(RuntimeError):
+        s.queue_rejection(torch.ones(100, device=gpu) / 100, torch.ones(100, device=gpu) / 100, None, None, None,
+                          torch.zeros(3, dtype=torch.int64, pin_memory=True))
+
+
+def test_mass_rounding_matches_declared(gpu):
+    """Masses of the normalised rows are the exact fixed-point sums."""
+    vocab = 4096
+    p = softmax_rows(2, vocab, 77)
+    ranks = torch.zeros((2, 1), dtype=torch.int64)
+    cut = torch.tensor([[1e-4], [0.0]], dtype=torch.float32)
+    s = CategoricalSampler(2, vocab, gpu)
+    out = s.normalize_top_p_for_sampling(p.to(gpu), cut.to(gpu), ranks.to(gpu)).cpu().numpy()
+    for r in range(2):
+        w = np.where(p[r].numpy() >= cut[r, 0].numpy(), p[r].numpy(), np.float32(0))
+        m = nm.mass_to_f32(int(nm.fx46(w).sum(dtype=np.uint64)))
+        assert np.array_equal(out[r], np.where(w > 0, (p[r].numpy() / m).astype(np.float32), np.float32(0)))

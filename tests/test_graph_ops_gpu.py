@@ -1,0 +1,167 @@
+"""GPU parity of the KV-slot / mapping / state-row / KV-commit kernels against
+oracle.graph_ops (integer work: bit-exact), including HIP-graph replays."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import graph_ops as og
+from loopspec_amd.loopspec import graph_ops as go
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("batch", [1, 7, 64, 1023, 1024, 1025, 5000])
+def test_allocate_decode_slots(gpu, batch):
+    rng = np.random.default_rng(batch)
+    cap = 97
+    free = rng.permutation(10_000)[:cap].astype(np.int64)
+    markers = rng.choice([-1, 0, 5], size=batch).astype(np.int64)
+    cursor = 190
+    out = np.full(batch, -7, dtype=np.int64)
+    announce(f"allocate_decode_slots B={batch}")
+    t_out = torch.from_numpy(out).to(gpu)
+    t_cur = torch.tensor(cursor, dtype=torch.int64, device=gpu)
+    go.allocate_decode_slots(torch.from_numpy(free).to(gpu), t_cur, torch.from_numpy(markers).to(gpu), t_out)
+    want, wcur = og.allocate_decode_slots(free, cursor, markers)
+    got = t_out.cpu().numpy()
+    for b in range(batch):
+        assert got[b] == want.get(b, -7)
+    assert t_cur.item() == wcur
+
+
+def test_allocate_in_graph_replays(gpu):
+    cap, batch = 16, 6
+    free = torch.arange(100, 100 + cap, dtype=torch.int64, device=gpu)
+    cursor = torch.zeros((), dtype=torch.int64, device=gpu)
+    markers = torch.tensor([0, -1, 0, 0, -1, 0], dtype=torch.int64, device=gpu)
+    out = torch.full((batch,), -1, dtype=torch.int64, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        go.allocate_decode_slots(free, cursor, markers, out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        go.allocate_decode_slots(free, cursor, markers, out)
+    cur = 4  # eager warm-up call + capture does not execute
+    torch.cuda.synchronize()
+    assert cursor.item() == cur
+    for _ in range(5):
+        g.replay()
+        torch.cuda.synchronize()
+        want, cur = og.allocate_decode_slots(free.cpu().numpy(), cur, markers.cpu().numpy())
+        got = out.cpu().numpy()
+        for b, v in want.items():
+            assert got[b] == v
+        assert cursor.item() == cur
+
+
+@pytest.mark.parametrize("max_ctx", [300, 4096, 9000])
+def test_update_request_mapping(gpu, max_ctx):
+    rng = np.random.default_rng(max_ctx)
+    rows_cap, batch = 40, 24
+    mapping = rng.integers(0, 1 << 30, size=(rows_cap, max_ctx)).astype(np.int32)
+    dst = rng.permutation(20)[:batch % 20 + 4][:batch]
+    batch = len(dst)
+    src = rng.integers(20, rows_cap, size=batch)
+    copy = rng.integers(-2, max_ctx // 2, size=batch)
+    copy[0], copy[1] = 0, -1
+    pos = np.array([max(int(c), 0) + int(rng.integers(0, max_ctx // 2)) for c in copy])
+    slots = rng.integers(0, 1 << 40, size=batch)
+    announce(f"update_request_mapping ctx={max_ctx}")
+    t_map = torch.from_numpy(mapping.copy()).to(gpu)
+    args = [torch.from_numpy(np.asarray(a, dtype=np.int64)).to(gpu) for a in (dst, src, copy, pos, slots)]
+    go.update_request_mapping(t_map, *args)
+    want = og.update_request_mapping(mapping.copy(), dst, src, copy, pos, slots)
+    assert np.array_equal(t_map.cpu().numpy(), want)
+
+
+def test_update_request_mapping_strided_table(gpu):
+    """A mapping view with row stride larger than its context length."""
+    full = torch.zeros((8, 512), dtype=torch.int32)
+    full[:, :] = torch.arange(512, dtype=torch.int32)
+    t_full = full.to(gpu)
+    view = t_full[:, :300]
+    args = [torch.tensor(a, dtype=torch.int64, device=gpu) for a in ([1], [2], [10], [299], [77])]
+    go.update_request_mapping(view, *args)
+    want = full.numpy().copy()
+    og.update_request_mapping(want[:, :300], [1], [2], [10], [299], [77])
+    assert np.array_equal(t_full.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype,width", [(torch.bfloat16, 4096), (torch.float32, 7), (torch.int64, 1),
+                                         (torch.uint8, 33)])
+@pytest.mark.parametrize("gather", [True, False])
+def test_copy_state_rows(gpu, dtype, width, gather):
+    rng = np.random.default_rng(width)
+    nbank, batch = 50, 12
+    idx = rng.permutation(nbank)[:batch].astype(np.int64)
+    idx[3] = -1
+    bank = torch.randint(0, 100, (nbank, width)).to(dtype) if width > 1 else torch.randint(0, 100, (nbank,)).to(dtype)
+    rows = torch.randint(0, 100, (batch, width)).to(dtype) if width > 1 else torch.randint(0, 100, (batch,)).to(dtype)
+    src, dst = (bank, rows) if gather else (rows, bank)
+    announce(f"copy_state_rows {dtype} W={width} gather={gather}")
+    t_src, t_dst = src.to(gpu), dst.to(gpu)
+    go.copy_state_rows(t_src, t_dst, torch.from_numpy(idx).to(gpu), gather=gather)
+    want = og.copy_state_rows(src.numpy() if dtype != torch.bfloat16 else src.view(torch.int16).numpy(),
+                              (dst.numpy() if dtype != torch.bfloat16 else dst.view(torch.int16).numpy()).copy(),
+                              idx, gather)
+    got = t_dst.cpu()
+    got = got.view(torch.int16).numpy() if dtype == torch.bfloat16 else got.numpy()
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("page_size", [1, 16])
+def test_kv_commit(gpu, page_size):
+    rng = np.random.default_rng(page_size)
+    B, k, max_pages = 9, 4, 32
+    num_pages = 400
+    planes, heads, hd = 6, 4, 32
+    slots = num_pages * page_size
+    ctx = rng.integers(0, 100 if page_size == 16 else 20, size=B).astype(np.int64)
+    acc = rng.integers(0, k + 1, size=B).astype(np.int32)
+    acc[0], acc[1] = 0, k
+    owned = [-(-int(c) // page_size) for c in ctx]
+    nres = -(-B * k // page_size)  # the last nres pages hold the branch slots
+    perm = rng.permutation(num_pages - nres)
+    pt = np.full((B, max_pages), -1, dtype=np.int32)
+    used = 0
+    for b in range(B):
+        pt[b, :owned[b]] = perm[used:used + owned[b]]
+        used += owned[b]
+    ring = perm[used:].astype(np.int64)
+    cursor = 3
+    branch = ((num_pages - nres) * page_size + np.arange(B * k)).reshape(B, k).astype(np.int64)
+    kv = torch.randn(planes, slots, heads, hd).to(torch.bfloat16)
+    announce(f"kv_commit page_size={page_size}")
+    t = {n: torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for n, a in
+         (("acc", acc), ("branch", branch), ("pt", pt), ("ctx", ctx), ("ring", ring))}
+    t_cur = torch.tensor(cursor, dtype=torch.int64, device=gpu)
+    t_kv = kv.to(gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    dst = go.commit_kv(t_kv, t["acc"], t["branch"], t["pt"], t["ctx"], t["ring"], t_cur, page_size, status=status)
+    wdst, wpt, wcl, wcur = og.kv_commit_plan(acc, branch, pt, ctx, ring, cursor, page_size)
+    assert np.array_equal(dst.cpu().numpy(), wdst)
+    assert np.array_equal(t["pt"].cpu().numpy(), wpt)
+    assert np.array_equal(t["ctx"].cpu().numpy(), wcl)
+    assert t_cur.item() == wcur
+    assert status.item() == 0
+    want_kv = og.kv_commit_copy(kv.view(torch.int16).numpy().copy(), branch, wdst)
+    assert np.array_equal(t_kv.cpu().view(torch.int16).numpy(), want_kv)
+
+
+def test_kv_commit_reports_overflow(gpu):
+    """A row whose pages would exceed its page-table width is skipped and flagged."""
+    pt = torch.tensor([[0, 1]], dtype=torch.int32, device=gpu)
+    ctx = torch.tensor([4], dtype=torch.int64, device=gpu)  # page_size 2: both entries owned
+    acc = torch.tensor([2], dtype=torch.int32, device=gpu)
+    branch = torch.tensor([[8, 9]], dtype=torch.int64, device=gpu)
+    ring = torch.tensor([3], dtype=torch.int64, device=gpu)
+    cur = torch.zeros((), dtype=torch.int64, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    dst = go.commit_kv(None, acc, branch, pt, ctx, ring, cur, 2, status=status)
+    assert status.item() == 1
+    assert dst.cpu().tolist() == [[-1, -1]]

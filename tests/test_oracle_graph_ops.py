@@ -1,0 +1,130 @@
+"""Pins oracle.graph_ops against invariants and closed forms (CPU only).
+
+The reference holds no tests or fixtures for graph_ops.py, so every check here
+comes from what the operation's contract fixes: ring entries are consumed in
+batch order without gaps, untouched rows stay untouched, the committed
+timeline reads back the branch tokens, pages are never shared.
+"""
+
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import graph_ops as og
+
+
+@pytest.mark.parametrize("batch", range(1, 9))
+def test_allocate_every_marker_pattern(batch):
+    free = np.arange(100, 107, dtype=np.int64)  # capacity 7 forces wrap-around
+    for pattern in itertools.product([-1, 0, 3], repeat=batch):
+        for cursor in (0, 5, 13):
+            got, cur = og.allocate_decode_slots(free, cursor, np.array(pattern))
+            valid = [b for b, m in enumerate(pattern) if m >= 0]
+            # Closed form: the i-th valid row takes ring entry cursor + i.
+            assert list(got) == valid
+            assert [got[b] for b in valid] == [int(free[(cursor + i) % 7]) for i in range(len(valid))]
+            assert cur == cursor + len(valid)
+
+
+def test_allocate_marker_values_are_not_sizes():
+    free = np.arange(10, dtype=np.int64)
+    a, _ = og.allocate_decode_slots(free, 0, np.array([0, 5, 100]))
+    b, _ = og.allocate_decode_slots(free, 0, np.array([1, 1, 1]))
+    assert a == b == {0: 0, 1: 1, 2: 2}
+
+
+def _mapping(rows=6, ctx=12, seed=0):
+    return np.random.default_rng(seed).integers(0, 1000, size=(rows, ctx)).astype(np.int32)
+
+
+def test_update_mapping_copy_append_skip():
+    m0 = _mapping()
+    m = og.update_request_mapping(m0.copy(), [1, 2, 3], [4, 5, 0], [3, 0, -1], [5, 7, 2], [901, 902, 903])
+    # row 1: prefix of row 4 then the new slot at position 5
+    assert (m[1, :3] == m0[4, :3]).all() and m[1, 5] == 901
+    assert (m[1, 3:5] == m0[1, 3:5]).all() and (m[1, 6:] == m0[1, 6:]).all()
+    # row 2: zero copy length only appends
+    assert (np.delete(m[2], 7) == np.delete(m0[2], 7)).all() and m[2, 7] == 902
+    # row 3: negative copy length writes nothing; other rows untouched
+    for r in (0, 3, 4, 5):
+        assert (m[r] == m0[r]).all()
+
+
+def test_update_mapping_slot_truncates_to_int32():
+    m = og.update_request_mapping(_mapping(), [0], [0], [0], [0], [2**32 + 7])
+    assert m[0, 0] == 7
+
+
+def test_copy_state_rows_gather_scatter_roundtrip():
+    rng = np.random.default_rng(1)
+    bank = rng.standard_normal((9, 5)).astype(np.float32)
+    idx = np.array([3, -1, 7, 0])
+    batch = np.full((4, 5), -2.0, dtype=np.float32)
+    og.copy_state_rows(bank, batch, idx, gather=True)
+    assert (batch[0] == bank[3]).all() and (batch[1] == -2).all() and (batch[2] == bank[7]).all()
+    bank2 = np.zeros_like(bank)
+    og.copy_state_rows(batch, bank2, idx, gather=False)
+    for b, r in enumerate(idx):
+        if r >= 0:
+            assert (bank2[r] == bank[r]).all()
+    untouched = [r for r in range(9) if r not in set(idx.tolist())]
+    assert (bank2[untouched] == 0).all()
+
+
+def _walk(page_table_row, ctx, page_size):
+    return [int(page_table_row[p // page_size]) * page_size + p % page_size for p in range(ctx)]
+
+
+@pytest.mark.parametrize("page_size", [1, 2, 3, 16])
+def test_kv_commit_plan_invariants(page_size):
+    rng = np.random.default_rng(page_size)
+    B, k, max_pages = 7, 4, 64
+    num_pages = 1000
+    for trial in range(30):
+        ctx = rng.integers(0, 40, size=B).astype(np.int64)
+        acc = rng.integers(0, k + 1, size=B).astype(np.int32)
+        perm = rng.permutation(num_pages)
+        owned = [-(-int(c) // page_size) for c in ctx]
+        pt = np.full((B, max_pages), -1, dtype=np.int32)
+        used = 0
+        for b in range(B):
+            pt[b, :owned[b]] = perm[used:used + owned[b]]
+            used += owned[b]
+        ring = perm[used:].astype(np.int64)
+        cursor = int(rng.integers(0, 3 * len(ring)))
+        branch = (np.arange(B * k, dtype=np.int64).reshape(B, k) + 10_000)
+        dst, pt2, cl2, cur2 = og.kv_commit_plan(acc, branch, pt, ctx, ring, cursor, page_size)
+        assert (cl2 == ctx + acc).all()
+        new_pages = []
+        for b in range(B):
+            need = -(-int(ctx[b] + acc[b]) // page_size) - owned[b]
+            new_pages += [int(p) for p in pt2[b, owned[b]:owned[b] + need]]
+            # Previously owned pages keep their ids; later entries stay unset.
+            assert (pt2[b, :owned[b]] == pt[b, :owned[b]]).all()
+            assert (pt2[b, owned[b] + need:] == -1).all()
+            # The committed timeline reads back through the page table.
+            walk = _walk(pt2[b], int(cl2[b]), page_size)
+            assert walk[:ctx[b]] == _walk(pt[b], int(ctx[b]), page_size)
+            assert walk[ctx[b]:] == dst[b, :acc[b]].tolist()
+            assert (dst[b, acc[b]:] == -1).all()
+        # New pages are the next ring entries, in batch order, with no gaps.
+        assert new_pages == [int(ring[(cursor + i) % len(ring)]) for i in range(len(new_pages))]
+        assert cur2 == cursor + len(new_pages)
+        # No slot is shared between rows (pages are disjoint by construction).
+        slots = [s for b in range(B) for s in _walk(pt2[b], int(cl2[b]), page_size)]
+        assert len(slots) == len(set(slots))
+
+
+def test_kv_commit_copy_moves_accepted_rows_only():
+    rng = np.random.default_rng(3)
+    kv = rng.standard_normal((3, 40, 8)).astype(np.float32)
+    branch = np.array([[30, 31, 32], [33, 34, 35]])
+    dst = np.array([[4, 5, -1], [9, -1, -1]])
+    out = og.kv_commit_copy(kv.copy(), branch, dst)
+    assert (out[:, 4] == kv[:, 30]).all() and (out[:, 5] == kv[:, 31]).all() and (out[:, 9] == kv[:, 33]).all()
+    mask = np.ones(40, bool)
+    mask[[4, 5, 9]] = False
+    assert (out[:, mask] == kv[:, mask]).all()
