@@ -24,6 +24,8 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth, GB/s
+METRIC = "verify+sample rows/s + achieved HBM GB/s (% of peak), vocab 49152, B=64, k=2"
+COPY_CAL_ROWS, COPY_CAL_ROW_BYTES = 4096, 65536  # 256 MiB plain copy for PMC byte calibration
 
 
 def _log(msg: str) -> None:
@@ -87,7 +89,7 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
     nbytes = workloads.greedy_algorithmic_bytes(cfg)
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     return {
-        "metric": "verify+sample rows/s (C2 greedy, vocab 49152, B=64, k=2)",
+        "metric": METRIC,
         "value": cfg.batch / (ms_per_step * 1e-3),
         "unit": "rows/s",
         "steps": timed_steps,
@@ -162,7 +164,7 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
     accepted = acc.sum().item() / nsets
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     return {
-        "metric": f"verify+sample rows/s ({cfg.name})",
+        "metric": METRIC if cfg.name == "C3" else f"verify+sample rows/s ({cfg.name})",
         "value": cfg.batch / (ms_per_step * 1e-3),
         "unit": "rows/s",
         "steps": timed,
@@ -178,6 +180,98 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None},
     }
+
+
+def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    """C5: C3 sampling verify at B=128, then the paged commit of each row's
+    accepted draft tokens' KV (24 layers x 4 loops x {K, V}, 16 heads x 128,
+    bf16, pages of 16) from the branch slots into the main timeline."""
+    from loopspec_amd import verify, workloads
+    from loopspec_amd.loopspec import graph_ops
+
+    cfg, kvc = workloads.C5_SAMPLING, workloads.C5_KV
+    _log(f"generating {nsets} input sets for {cfg.name}")
+    sets = []
+    for i in range(nsets):
+        inp = workloads.sampling_inputs(cfg, seed=3000 + i, device=device)
+        flat = inp["draft"].reshape(cfg.batch * cfg.k, cfg.vocab)
+        drafts = verify.sample_logits(flat, inp["draft_uniforms"].reshape(-1).contiguous(), cfg.temperature,
+                                      cfg.top_p)
+        inp["draft_tokens"] = drafts.reshape(cfg.batch, cfg.k)
+        sets.append(inp)
+    total_steps = steps + warmup + 4 * nsets
+    state = workloads.kv_commit_state(kvc, cfg.batch, cfg.k, total_steps, seed=5, device=device)
+    ws = torch.zeros(verify.spec_verify_workspace_bytes(cfg.batch, cfg.k, cfg.vocab), dtype=torch.uint8,
+                     device=device)
+    acc = torch.empty((nsets, cfg.batch), dtype=torch.int32, device=device)
+    tok = torch.empty((nsets, cfg.batch, cfg.k + 1), dtype=torch.int64, device=device)
+    dst = torch.empty((cfg.batch, cfg.k), dtype=torch.int64, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def step(i: int) -> None:
+        s = sets[i]
+        verify.speculative_verify(s["target"], s["draft"], s["draft_tokens"], s["uniforms"], cfg.temperature,
+                                  cfg.top_p, accept_len=acc[i], tokens=tok[i], workspace=ws)
+        graph_ops.commit_kv(state["kv"], acc[i], state["branch_slots"], state["page_table"], state["ctx_len"],
+                            state["free_pages"], state["page_cursor"], kvc.page_size, dst_slots=dst,
+                            status=status)
+
+    ms_per_step, timed, wsteps = _time_graph(step, nsets, steps, warmup)
+    if status.item() != 0:
+        raise RuntimeError("C5 commit reported an out-of-range page (page table too narrow)")
+    accepted = acc.sum().item() / nsets
+    logit_bytes = workloads.sampling_algorithmic_bytes(cfg)
+    kv_bytes = workloads.kv_commit_algorithmic_bytes(kvc, cfg.batch, cfg.k, int(round(accepted)))
+    nbytes = logit_bytes + kv_bytes
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": "verify+sample+commit rows/s (C5)",
+        "value": cfg.batch / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "steps": timed,
+        "warmup": wsteps,
+        "ms_per_step": ms_per_step,
+        "dtype": "f32",
+        "config": {"workload": "C5-" + cfg.name[3:] + "+" + kvc.name[3:], "batch": cfg.batch, "k": cfg.k,
+                   "vocab": cfg.vocab, "temperature": cfg.temperature, "top_p": cfg.top_p,
+                   "kv_planes": kvc.planes, "kv_token_bytes": kvc.token_bytes, "page_size": kvc.page_size,
+                   "input_sets": nsets, "logit_bytes": logit_bytes, "kv_commit_bytes": kv_bytes,
+                   "kernels": "ls::sample_rows_kernel<spec> + kv_plan_kernel + kv_copy_kernel",
+                   "submission": "hipGraph of three launches per step"},
+        "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
+        "acceptance_rate": accepted / (cfg.batch * cfg.k),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
+def copy_calibration(device: torch.device, launches: int) -> None:
+    """Plain copies of known size (COPY_CAL_ROWS x COPY_CAL_ROW_BYTES read and
+    written per launch, ls::copy_rows_kernel<16>) for scaling PMC byte counters."""
+    from loopspec_amd.loopspec import graph_ops
+
+    src = torch.ones((COPY_CAL_ROWS, COPY_CAL_ROW_BYTES), dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    idx = torch.arange(COPY_CAL_ROWS, dtype=torch.int64, device=device)
+    for _ in range(launches):
+        graph_ops.copy_state_rows(src, dst, idx, gather=True)
+    torch.cuda.synchronize()
+    if not torch.equal(src[:: COPY_CAL_ROWS // 8], dst[:: COPY_CAL_ROWS // 8]):
+        raise RuntimeError("copy calibration produced wrong data")
+
+
+def traffic_from_profile(kernel: str, workload: str) -> float | None:
+    """HBM bytes per launch recorded by the committed PMC summary
+    profiles/<kernel>_<workload>_traffic.md (line 'traffic_bytes_per_launch: N')."""
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "profiles" / f"{kernel}_{workload}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
 
 
 def _time_graph(step, nsets: int, steps: int, warmup: int):
@@ -251,6 +345,8 @@ def main() -> int:
     ap.add_argument("--config", default="C2")
     ap.add_argument("--sets", type=int, default=10, help="distinct input sets rotated through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="N",
+                    help="after timing, run N plain 256 MiB copies (for rocprofv3 --pmc byte scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -272,11 +368,19 @@ def main() -> int:
         cfg = workloads.C3 if args.config == "C3" else workloads.C4
         result = bench_spec(cfg, args.steps, args.warmup, device, args.sets)
         args.no_cpu_baseline = True
+    elif args.config == "C5":
+        result = bench_c5(args.steps, args.warmup, device, args.sets)
+        args.no_cpu_baseline = True
     else:
         print(f"unknown config {args.config}", file=sys.stderr)
         return 2
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                    "data": "synthetic (seeded N(0,3^2) logits, draft = target + N(0,1), 1% planted ties)"})
+    kernel_name = {"C2": "greedy_kernel", "C3": "sample_rows_kernel", "C4": "sample_rows_kernel"}.get(args.config)
+    if kernel_name:
+        result["roofline"]["traffic"] = traffic_from_profile(kernel_name, args.config)
+    if args.copy_calibration:
+        copy_calibration(device, args.copy_calibration)
     if not args.no_cpu_baseline:
         _log("timing CPU baseline")
         result["cpu_baseline"] = cpu_baseline_greedy()

@@ -1,0 +1,112 @@
+"""Greedy decisions and compact decision readback (drop-in).
+
+Same classes and methods as sglang_recurrent/loopspec/decisions.py:18-184.
+GreedyDecisionPolicy.queue runs the gfx950 argmax kernel (ls_argmax_rows:
+first index of the maximum, NaN first, lowest index on ties — torch.argmax's
+rule) over every endpoint row in one launch and stages the [M, 1] ids to pinned
+host memory; read() waits on one event; resolve() is the reference's host rule.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+
+from .. import _lib
+from ..verify import argmax_rows
+from .pipeline import PipelineLane, PipelineSchedule
+
+
+@dataclass
+class DecisionBatch:
+    """One pending readback and optional proposal distributions (decisions.py:18-28)."""
+
+    staged: tuple[int, int]
+    proposal_states: dict[int, torch.Tensor] = field(default_factory=dict)
+
+
+@dataclass(frozen=True, slots=True)
+class DecisionOutcome:
+    """Policy-independent result consumed by the pipeline executor (decisions.py:31-42)."""
+
+    prediction: int
+    proposed: bool = False
+    proposal_state: torch.Tensor | None = None
+    accepted_stage: int | None = None
+    proposal_action: str | None = None
+    first_rejected: bool = False
+    second_rejected: bool = False
+
+
+class DecisionReadback:
+    """GPU -> pinned host copy of [M, C] int64 decisions with one event (decisions.py:45-89)."""
+
+    def __init__(self, max_rows: int, device: torch.device | str) -> None:
+        if torch.device(device).type != "cuda":
+            raise RuntimeError("LoopSpec decision readback requires CUDA")
+        self.host = torch.empty(max_rows * 5, dtype=torch.int64, pin_memory=True)
+        self.ready = torch.cuda.Event()
+
+    def stage(self, decisions: torch.Tensor) -> tuple[int, int]:
+        rows, columns = decisions.shape
+        target = self.host[: rows * columns].view(rows, columns)
+        target.copy_(decisions, non_blocking=True)
+        self.ready.record()
+        return rows, columns
+
+    def read(self, staged: tuple[int, int]) -> list[list[int]]:
+        rows, columns = staged
+        self.ready.synchronize()
+        return self.host[: rows * columns].view(rows, columns).tolist()
+
+
+class GreedyDecisionPolicy:
+    """Greedy token selection with one synchronisation per batch (decisions.py:92-184)."""
+
+    def __init__(self, max_rows: int, device: torch.device | str) -> None:
+        self.readback = DecisionReadback(max_rows, device)
+        _lib.load()
+        self.choices = torch.empty(max_rows, dtype=torch.int64, device=torch.device(device))
+
+    def queue(self, post_output: Any, endpoints: Mapping[int, str], lanes: Sequence[PipelineLane]) -> DecisionBatch:
+        del endpoints, lanes
+        logits = post_output.next_token_logits
+        rows = logits.shape[0]
+        out = self.choices[:rows] if rows <= self.choices.numel() else None
+        choices = argmax_rows(logits, out=out)
+        return DecisionBatch(self.readback.stage(choices.view(rows, 1)))
+
+    def read(self, lanes: Sequence[PipelineLane], endpoints: Mapping[int, str],
+             batch: DecisionBatch) -> dict[int, list[int]]:
+        del lanes
+        decisions = self.readback.read(batch.staged)
+        return dict(zip(endpoints, decisions, strict=True))
+
+    def resolve(self, lane: PipelineLane, endpoint_kind: str, decision: list[int],
+                proposal_state: torch.Tensor | None, schedule: PipelineSchedule) -> DecisionOutcome:
+        """q1 always proposes; q2 proposes when its argmax differs from q1; final
+        accepts q1, else q2, else rejects (decisions.py:136-184)."""
+        prediction = decision[0]
+        proposed = endpoint_kind == "q1" or (endpoint_kind == "q2" and prediction != lane.first_token)
+        accepted_stage = None
+        first_rejected = second_rejected = False
+        if endpoint_kind == "final" and lane.first_token is not None:
+            first_rejected = prediction != lane.first_token
+            if not first_rejected:
+                accepted_stage = schedule.proposal_stage
+            elif lane.second_token is not None:
+                second_rejected = prediction != lane.second_token
+                if not second_rejected:
+                    accepted_stage = schedule.second_stage
+        return DecisionOutcome(
+            prediction=prediction,
+            proposed=proposed,
+            proposal_state=proposal_state,
+            accepted_stage=accepted_stage,
+            proposal_action="argmax" if endpoint_kind == "q2" and proposed else None,
+            first_rejected=first_rejected,
+            second_rejected=second_rejected,
+        )

@@ -150,3 +150,76 @@ def sampling_algorithmic_bytes(cfg: SamplingConfig, history_bytes: int = 0) -> i
     rows = cfg.batch * (2 * cfg.k + 1)
     small = cfg.batch * (2 * cfg.k + 1) * 4 + cfg.batch * cfg.k * 8 + cfg.batch * 4 + cfg.batch * (cfg.k + 1) * 8
     return rows * cfg.vocab * elem + small + history_bytes
+
+
+@dataclass(frozen=True)
+class KVCommitConfig:
+    """KV pool of the C5 commit: planes = layers x loops x {K, V}, one token row
+    of heads x head_dim elements per plane, pages of page_size tokens."""
+
+    name: str
+    layers: int
+    loops: int
+    heads: int
+    head_dim: int
+    page_size: int
+    ctx_min: int
+    ctx_max: int
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def planes(self) -> int:
+        return self.layers * self.loops * 2
+
+    @property
+    def token_bytes(self) -> int:
+        return self.heads * self.head_dim * torch.tensor([], dtype=self.dtype).element_size()
+
+
+C5_KV = KVCommitConfig("C5-kv-ouro1.4b-24x4-16h128-bf16-page16", 24, 4, 16, 128, 16, 512, 8192)
+
+
+def kv_commit_state(kv: KVCommitConfig, batch: int, k: int, steps: int, seed: int,
+                    device: torch.device | str = "cpu") -> dict:
+    """Resident state for repeated commits of up to k tokens per row per step.
+
+    Only the pages a commit can write are backed by memory: each row's
+    partially filled last page, a free-page ring that new pages cycle through,
+    and the branch slots (one page-aligned region after the ring). Page-table
+    entries of older, full pages are never touched by a commit and point at
+    page 0. Context lengths are U(ctx_min, ctx_max); the page table is wide
+    enough for `steps` commits of k tokens.
+    """
+    device = torch.device(device)
+    rng = np.random.default_rng(seed)
+    ps = kv.page_size
+    ctx = rng.integers(kv.ctx_min, kv.ctx_max + 1, size=batch).astype(np.int64)
+    max_pages = -(-(kv.ctx_max + steps * k) // ps) + 1
+    tail_pages = batch
+    ring_pages = 4 * batch * (k + ps - 1) // ps + 64
+    branch_pages = -(-(batch * k) // ps)
+    num_pages = tail_pages + ring_pages + branch_pages
+    pt = np.zeros((batch, max_pages), dtype=np.int32)
+    for b in range(batch):
+        owned = -(-int(ctx[b]) // ps)
+        if owned:
+            pt[b, owned - 1] = b  # the row's partially filled (or last full) page
+    ring = (tail_pages + rng.permutation(ring_pages)).astype(np.int64)
+    branch = ((tail_pages + ring_pages) * ps + np.arange(batch * k)).reshape(batch, k).astype(np.int64)
+    return {
+        "page_table": torch.from_numpy(pt).to(device),
+        "ctx_len": torch.from_numpy(ctx).to(device),
+        "free_pages": torch.from_numpy(ring).to(device),
+        "page_cursor": torch.zeros((), dtype=torch.int64, device=device),
+        "branch_slots": torch.from_numpy(branch).to(device),
+        "kv": torch.empty((kv.planes, num_pages * ps, kv.heads, kv.head_dim), dtype=kv.dtype, device=device),
+        "num_pages": num_pages,
+    }
+
+
+def kv_commit_algorithmic_bytes(kv: KVCommitConfig, batch: int, k: int, accepted_tokens: int) -> int:
+    """Each accepted token's row read from the branch slot and written to its
+    destination in every plane, plus the plan's integer traffic."""
+    copy = 2 * accepted_tokens * kv.planes * kv.token_bytes
+    plan = batch * (4 + 8 + 8) + batch * k * (8 + 8) + accepted_tokens * 4
+    return copy + plan

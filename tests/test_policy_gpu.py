@@ -1,0 +1,127 @@
+"""GPU parity of the decision policies (loopspec_amd.loopspec.decisions and
+sampling.policy) against the oracle, with the generator's uniforms replayed in
+the order the reference's policy consumes them (policy.py:78-283)."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import greedy as og
+from oracle import sampling as osmp
+from loopspec_amd.loopspec.decisions import GreedyDecisionPolicy
+from loopspec_amd.loopspec.pipeline import PipelineLane, PipelineSchedule
+from loopspec_amd.loopspec.sampling.policy import SamplingDecisionPolicy
+from loopspec_amd.loopspec.sampling.sampler import CategoricalSampler
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def test_greedy_policy_queue_read(gpu):
+    m, v = 7, 49152
+    g = torch.Generator().manual_seed(3)
+    logits = (torch.randn(m, v, generator=g) * 3).to(torch.bfloat16)
+    logits[2, 100] = logits[2, 5000] = logits[2].max() + 1  # planted tie -> 100
+    endpoints = {4: "q1", 1: "final", 0: "q2", 6: "final", 2: "q1", 3: "final", 5: "q1"}
+    pol = GreedyDecisionPolicy(16, gpu)
+    batch = pol.queue(SimpleNamespace(next_token_logits=logits.to(gpu)), endpoints, [])
+    got = pol.read([], endpoints, batch)
+    want = [og.argmax_first(logits[r].float().numpy()) for r in range(m)]
+    assert list(got) == list(endpoints)
+    assert [got[row][0] for row in endpoints] == want
+    assert batch.staged == (m, 1)
+
+
+def test_greedy_resolve_rules(gpu):
+    pol = GreedyDecisionPolicy(4, gpu)
+    s = PipelineSchedule(12, 2, 3)
+    lane = PipelineLane(stage=0, index=1, token=0, first_token=7, second_token=9)
+    assert pol.resolve(lane, "final", [7], None, s).accepted_stage == s.proposal_stage
+    o = pol.resolve(lane, "final", [9], None, s)
+    assert (o.first_rejected, o.second_rejected, o.accepted_stage) == (True, False, s.second_stage)
+    o = pol.resolve(lane, "final", [8], None, s)
+    assert (o.first_rejected, o.second_rejected, o.accepted_stage) == (True, True, None)
+    assert pol.resolve(lane, "q2", [7], None, s).proposed is False
+    o = pol.resolve(lane, "q2", [3], None, s)
+    assert o.proposed and o.proposal_action == "argmax"
+    fresh = PipelineLane(stage=0, index=1, token=0)
+    o = pol.resolve(fresh, "final", [0], None, s)
+    assert not o.first_rejected and o.accepted_stage is None
+
+
+def _dist(v, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.softmax(torch.randn(v, generator=g) * scale, dim=-1)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_sampling_policy_matches_oracle(gpu, seed):
+    v = 8192
+    opts = {"temperature": 0.8, "top_k": 1 << 30, "top_p": 0.7}
+    g = torch.Generator().manual_seed(100 + seed)
+    logits = torch.randn(7, v, generator=g) * 3
+    # Lanes: q1 draft, q2 proposal, direct final, and four verified finals.
+    q1_state = _dist(v, 11 + seed)
+    lanes = [PipelineLane(stage=0, index=1, token=0) for _ in range(7)]
+    lanes[1].first_token, lanes[1].first_state = 17, q1_state.to(gpu)
+    for r, (tok, second) in zip((3, 4, 5, 6), ((int(torch.argmax(logits[3])), None), (123, 55), (456, None),
+                                               (789, 31))):
+        st = torch.zeros(v)
+        st[tok] = 1.0  # one-hot q1: a rejection unless p[x] is large
+        if r == 3:
+            st = _dist(v, 40 + seed)
+        lanes[r].first_token, lanes[r].first_state = tok, st.to(gpu)
+        if second is not None:
+            lanes[r].second_token, lanes[r].second_state = second, _dist(v, 50 + r).to(gpu)
+    endpoints = {0: "q1", 1: "q2", 2: "final", 3: "final", 4: "final", 5: "final", 6: "final"}
+    sampler = CategoricalSampler(16, v, gpu)
+    sampler.capture_rejection_graph()
+    gen = torch.Generator(device=gpu).manual_seed(seed)
+    pol = SamplingDecisionPolicy(16, gpu, opts, sampler, generator=gen)
+    announce(f"sampling policy seed={seed}")
+    batch = pol.queue(SimpleNamespace(next_token_logits=logits.to(gpu)), endpoints, lanes)
+    got = pol.read(lanes, endpoints, batch)
+
+    # Oracle, with the generator's draws replayed in the policy's order.
+    rep = torch.Generator(device=gpu).manual_seed(seed)
+
+    def draw(n):
+        u = torch.empty(n, dtype=torch.float32, device=gpu)
+        torch.rand(n, out=u, generator=rep)
+        return u.cpu().numpy()
+
+    rows = [osmp.filter_row(osmp.process_logits(logits[r].numpy(), 0.8), 0.7) for r in range(7)]
+    P = [r.P for r in rows]
+    u_q2 = draw(1)
+    R, act, ids = osmp.conditional_residual(q1_state.numpy()[None], P[1][None], np.array([17]), u_q2)
+    u_q1 = draw(1)
+    q1_tok = osmp.sample_top_p_rows(np.stack([r.soft.p for r in rows]), np.array([r.cutoff for r in rows]),
+                                    u_q1, np.array([0]))[0]
+    u_direct = draw(1)
+    direct_tok = osmp.categorical_pick(P[2], u_direct[0])
+    ver_rows = [3, 4, 5, 6]
+    u_ver = draw(4)
+    want = {0: [int(q1_tok), 1, 0, 0, 0],
+            1: [int(ids[0]) if act[0] > 0 else 17, int(act[0] > 0), int(act[0]), 0, 0],
+            2: [int(direct_tok), 0, 0, 0, 0]}
+    for i, r in enumerate(ver_rows):
+        lane = lanes[r]
+        x = lane.first_token
+        q = lane.first_state.cpu().numpy()
+        a = osmp.accept(u_ver[i], P[r][x], q[x])
+        want[r] = [x if a else -1, 0, int(a), int(not a), 0]
+    for r in ver_rows:
+        if want[r][0] < 0:
+            lane = lanes[r]
+            u0, u1 = draw(2)
+            has = lane.second_state is not None
+            second = lane.second_state.cpu().numpy() if has else np.zeros(v, np.float32)
+            tok, sacc, srej = osmp.rejection_run(lane.first_state.cpu().numpy(), P[r], second,
+                                                 lane.second_token or 0, has, u0, u1)
+            want[r][0], want[r][2], want[r][4] = tok, 2 if sacc else 0, srej
+    assert {r: list(d) for r, d in got.items()} == want
+    assert any(want[r][3] == 1 for r in ver_rows)  # the rejection path ran
+    # The q2 proposal state is the normalised residual.
+    assert np.array_equal(batch.proposal_states[1].cpu().numpy(), R[0])
