@@ -78,6 +78,7 @@ uint64_t ls_argmax_rows_workspace(int64_t rows, int64_t vocab);
  *                   prefix followed by the correction or bonus token), -1 after.
  * row_argmax (optional, may be NULL): int64 [B, 2k+1] = target argmax at
  *   positions 0..k followed by the draft argmax at 0..k-1.
+ * batch <= 16384; 1 <= k <= 64. Workspace: ls_greedy_verify_workspace bytes.
  * Replaces the greedy final-endpoint rule of GreedyDecisionPolicy.resolve
  *   (sglang_recurrent/loopspec/decisions.py:157-170) applied along the
  *   pipeline's accept prefix (sglang_recurrent/loopspec/pipeline.py:365-412). */

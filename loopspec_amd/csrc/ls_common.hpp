@@ -198,6 +198,31 @@ __device__ __forceinline__ uint32_t atomic_arrive(uint32_t* p) {
 __device__ __forceinline__ uint32_t atomic_exchange_u32(uint32_t* p, uint32_t v) {
   return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Device-coherent (agent-scope, relaxed) plain stores and loads: emitted as
+// sc1 global memory operations that write through / bypass the per-XCD L2, so
+// values published by one workgroup are visible to a workgroup on another XCD
+// once the writer has drained its stores and signalled through an atomic.
+__device__ __forceinline__ void store_sc(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_sc64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_sc(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_sc64(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every store of this lane has been acknowledged by the device
+// coherence point (vmcnt also counts stores on gfx9), and keep the compiler
+// from moving memory operations across.
+__device__ __forceinline__ void drain_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ uint64_t atomic_load_u64(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -1,14 +1,17 @@
 // (b) Greedy verification for gfx950.
 //
-// One launch covers every row of the step. Each workgroup owns one segment of
-// one row, sized so that every lane issues about six 16-byte loads up front and
-// several workgroups share a CU; a lane keeps a (group-max, vector) candidate,
-// resolves the exact first index inside the winning vector, and the block
-// reduces packed (value, -index) keys. Rows of one batch element meet in the
-// fused epilogue: each workgroup publishes its key with an agent-scope
-// atomicMax, waits for it to return, and arrives on the element's counter; the
-// last arriver reads the keys back with atomic exchanges (which also re-zero
-// the workspace) and runs the accept-prefix scan.
+// One launch covers every row of the step. Rows are cut into `splits` equal
+// segments, with splits chosen so that the segments spread evenly over the CUs
+// (C2: 320 rows x 4 segments = 5 workgroups on each of 256 CUs) and every lane
+// issues all of its 16-byte non-temporal loads up front (J loads per lane, a
+// template constant when the segment is an exact multiple of the workgroup).
+// A lane keeps a (vector-max, vector) candidate, resolves the first index of
+// the maximum inside the winning vector, and the block reduces packed
+// (value, -index) keys. Segments meet in the fused epilogue without
+// same-address contention: each workgroup writes its key to its own slot with
+// a device-coherent store, drains it, and arrives on its batch element's
+// counter; the last arriver loads the element's keys, takes the per-row
+// maximum over segments and runs the accept-prefix scan.
 //
 // Reference semantics: torch.argmax over the endpoint rows
 // (sglang_recurrent/loopspec/decisions.py:116) and the final-endpoint rule
@@ -20,6 +23,15 @@ namespace ls {
 namespace {
 
 constexpr int kUnroll = 8;
+// Arrival counters sit one 64-byte line apart: device-scope atomics on one
+// line serialise, and adjacent counters of concurrently finishing groups
+// measured several microseconds of queueing on MI355X. They live at a fixed
+// place (the first kMaxGroups lines of the workspace) so that the key slots of
+// a call with another shape never overlap them.
+constexpr int kCounterStride = 16;
+constexpr int64_t kMaxGroups = 16384;
+constexpr int kMaxSplits = 16;
+constexpr int kMaxRowsPerGroup = 2 * 64 + 1;
 
 struct GreedyParams {
   const char* target;        // row (b, i) at target + b*t_bstride + i*t_pstride (bytes)
@@ -28,6 +40,8 @@ struct GreedyParams {
   int64_t d_bstride, d_pstride;
   const int64_t* draft_tokens;
   int64_t vocab;
+  int64_t nvec;              // 16-byte vectors per row (vector path)
+  int64_t seg;               // vectors (vector path) or elements (scalar path) per split
   int k;                     // draft positions (verify mode); 0 in argmax mode
   int rows_per_group;        // argmax: 1; verify: (k+1) [+ k when draft logits given]
   int splits;                // workgroups per row
@@ -36,62 +50,67 @@ struct GreedyParams {
   int32_t* accept_len;       // verify outputs
   int64_t* tokens;
   int64_t* row_argmax;
-  uint64_t* slots;           // workspace: one key per row
-  uint32_t* counters;        // workspace: one arrival counter per group
+  uint64_t* slots;           // workspace: one key per (row, split)
+  uint32_t* counters;        // workspace: one arrival counter per group, kCounterStride apart
 };
 
-// Row pointer of global row r (verify rows are grouped per batch element:
-// target positions 0..k first, then draft positions 0..k-1).
-__device__ __forceinline__ const char* row_ptr(const GreedyParams& p, int64_t r) {
-  if (p.k == 0) return p.target + r * p.t_pstride;
-  const int64_t b = r / p.rows_per_group;
-  const int j = static_cast<int>(r - b * p.rows_per_group);
-  if (j <= p.k) return p.target + b * p.t_bstride + j * p.t_pstride;
-  return p.draft + b * p.d_bstride + (j - p.k - 1) * p.d_pstride;
+// Row j of group g (verify rows: target positions 0..k, then draft positions
+// 0..k-1; argmax mode: row g).
+__device__ __forceinline__ const char* row_ptr(const GreedyParams& p, int64_t g, int j) {
+  if (j <= p.k) return p.target + g * p.t_bstride + j * p.t_pstride;
+  return p.draft + g * p.d_bstride + (j - p.k - 1) * p.d_pstride;
 }
 
 // First-index argmax key of this lane's share of vectors [v0, v1) of a row.
 // The lane's vectors are v0 + lane + j*BLOCK for j < n. Loads go through a
 // clamped address (lanes past their last vector re-read it and ignore the
-// result), so a batch of kUnroll loads is issued without branches and each
-// vector is consumed as soon as its own load returns.
-template <int DT, int BLOCK>
+// result), so a batch of loads is issued without branches and each vector is
+// consumed as soon as its own load returns. J > 0: the whole share is one batch
+// of exactly J loads (J = n for every lane when the segment is J*BLOCK
+// vectors); J == 0: batches of kUnroll.
+template <int DT, int BLOCK, int J>
 __device__ __forceinline__ uint64_t thread_argmax_vec(const u32x4* __restrict__ src, int64_t v0, int64_t v1) {
   constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int kBatch = J > 0 ? J : kUnroll;
   const int64_t first = v0 + threadIdx.x;
   if (first >= v1) return 0;
-  const int n = static_cast<int>((v1 - first + BLOCK - 1) / BLOCK);
+  const int n = J > 0 ? J : static_cast<int>((v1 - first + BLOCK - 1) / BLOCK);
   const u32x4* __restrict__ p = src + first;
   float best = -__builtin_inff();
   int bestj = 0;
   u32x4 bestd = {0u, 0u, 0u, 0u};
-  for (int j0 = 0; j0 < n; j0 += kUnroll) {
-    u32x4 d[kUnroll];
+  for (int j0 = 0; j0 < n; j0 += kBatch) {
+    u32x4 d[kBatch];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = j0 + u < n ? j0 + u : n - 1;
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = J > 0 ? u : (j0 + u < n ? j0 + u : n - 1);
       d[u] = __builtin_nontemporal_load(p + static_cast<int64_t>(j) * BLOCK);
     }
     // Seeding with the lane's first vector makes an all -inf share resolve to
     // its first element without a sentinel.
     if (j0 == 0) bestd = d[0];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const float g = vec_max<DT>(d[u]);
       // Vectors arrive in increasing index order, so a strict '>' keeps the
       // earliest vector holding the maximum; a NaN beats any number once.
-      const bool take = (j0 + u < n) & ((g > best) | ((g != g) & (best == best)));
+      const bool in = J > 0 ? true : (j0 + u < n);
+      const bool take = in & ((g > best) | ((g != g) & (best == best)));
       best = take ? g : best;
       bestj = take ? j0 + u : bestj;
       bestd = take ? d[u] : bestd;
     }
+    if constexpr (J > 0) break;
   }
+  // First element of the winning vector equal to the maximum (or the first
+  // NaN), by selects from the last element down.
   const bool is_nan = best != best;
   int e = 0;
 #pragma unroll
   for (int q = EPV - 1; q >= 0; --q) {
     const float x = vec_elem<DT>(bestd, q);
-    if (is_nan ? (x != x) : (x == best)) e = q;
+    const bool hit = (x == best) | (is_nan & (x != x));
+    e = hit ? q : e;
   }
   const int64_t v = first + static_cast<int64_t>(bestj) * BLOCK;
   return argmax_key(best, static_cast<uint32_t>(v * EPV + e));
@@ -114,17 +133,24 @@ __device__ __forceinline__ uint64_t thread_argmax_scalar(const char* row, int64_
 }
 
 // Runs on every lane of the last workgroup of group g (a block-uniform
-// branch). Lane j reads row j's combined key with an exchange, which also
-// leaves the slot zeroed, so all rows' reads are in flight together; lane 0
-// then runs the scan.
+// branch). Lane i loads key i of the group's rows_per_group * splits keys with
+// a device-coherent load; row j's key is the maximum over its splits; lane 0
+// runs the scan and re-arms the group's counter.
 template <int BLOCK>
-__device__ void finalize_group(const GreedyParams& p, int64_t g, int64_t* ids) {
-  uint64_t* slots = p.slots + g * p.rows_per_group;
+__device__ void finalize_group(const GreedyParams& p, int64_t g, int64_t* ids, uint64_t* keys) {
   const int lane = threadIdx.x;
-  for (int j = lane; j < p.rows_per_group; j += BLOCK) ids[j] = argmax_key_index(atomic_exchange_u64(slots + j, 0));
-  if (lane == 0) atomic_exchange_u32(p.counters + g, 0u);
+  const int nkeys = p.rows_per_group * p.splits;
+  const uint64_t* slots = p.slots + g * nkeys;
+  for (int i = lane; i < nkeys; i += BLOCK) keys[i] = load_sc64(slots + i);
+  __syncthreads();
+  for (int j = lane; j < p.rows_per_group; j += BLOCK) {
+    uint64_t best = 0;
+    for (int s = 0; s < p.splits; ++s) best = keys[j * p.splits + s] > best ? keys[j * p.splits + s] : best;
+    ids[j] = argmax_key_index(best);
+  }
   __syncthreads();
   if (lane != 0) return;
+  store_sc(p.counters + g * kCounterStride, 0u);
   if (p.k == 0) {
     p.out[g] = ids[0];
     return;
@@ -149,105 +175,137 @@ __device__ void finalize_group(const GreedyParams& p, int64_t g, int64_t* ids) {
   p.accept_len[g] = accepted;
 }
 
-template <int DT, bool VEC, int BLOCK>
+// Grid: direct mode (argmax, one workgroup per row) is 1-D over rows;
+// otherwise (splits, rows_per_group, groups), so no index division is needed.
+template <int DT, bool VEC, int BLOCK, int J>
 __global__ __launch_bounds__(BLOCK) void greedy_kernel(GreedyParams p) {
   __shared__ uint64_t red[BLOCK / kWave];
-  __shared__ int64_t ids[2 * 64 + 1];
+  __shared__ int64_t ids[kMaxRowsPerGroup];
+  __shared__ uint64_t keys[kMaxRowsPerGroup * 4];
   __shared__ int last;
-  const int64_t r = blockIdx.x / p.splits;
-  const int split = static_cast<int>(blockIdx.x - r * p.splits);
-  const char* row = row_ptr(p, r);
+  const int split = p.direct ? 0 : static_cast<int>(blockIdx.x);
+  const int j = p.direct ? 0 : static_cast<int>(blockIdx.y);
+  const int64_t g = p.direct ? static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.z);
+  const char* row = row_ptr(p, g, j);
 
   uint64_t key;
   if constexpr (VEC) {
-    constexpr int EPV = Elem<DT>::kPerVec;
-    const int64_t nvec = p.vocab / EPV;
-    const int64_t per = (nvec + p.splits - 1) / p.splits;
-    const int64_t v0 = split * per;
-    const int64_t v1 = v0 + per < nvec ? v0 + per : nvec;
-    key = thread_argmax_vec<DT, BLOCK>(reinterpret_cast<const u32x4*>(row), v0, v1);
+    const int64_t v0 = split * p.seg;
+    const int64_t v1 = v0 + p.seg < p.nvec ? v0 + p.seg : p.nvec;
+    key = thread_argmax_vec<DT, BLOCK, J>(reinterpret_cast<const u32x4*>(row), v0, v1);
   } else {
-    const int64_t per = (p.vocab + p.splits - 1) / p.splits;
-    const int64_t i0 = split * per;
-    const int64_t i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
+    const int64_t i0 = split * p.seg;
+    const int64_t i1 = i0 + p.seg < p.vocab ? i0 + p.seg : p.vocab;
     key = thread_argmax_scalar<DT, BLOCK>(row, i0, i1);
   }
   key = block_max_u64<BLOCK>(key, red);
 
   if (p.direct) {
-    if (threadIdx.x == 0) p.out[r] = argmax_key_index(key);
+    if (threadIdx.x == 0) p.out[g] = argmax_key_index(key);
     return;
   }
-  const int64_t g = r / p.rows_per_group;
   if (threadIdx.x == 0) {
-    await_value(atomic_max_u64(p.slots + r, key));
-    const uint32_t prev = atomic_arrive(p.counters + g);
+    store_sc64(p.slots + (g * p.rows_per_group + j) * p.splits + split, key);
+    drain_stores();
+    const uint32_t prev = atomic_arrive(p.counters + g * kCounterStride);
     last = prev == static_cast<uint32_t>(p.rows_per_group * p.splits - 1);
   }
   __syncthreads();
-  if (last) finalize_group<BLOCK>(p, g, ids);
+  if (last) finalize_group<BLOCK>(p, g, ids, keys);
 }
 
-uint64_t workspace_bytes(int64_t rows, int64_t groups) {
-  const uint64_t slots = static_cast<uint64_t>(rows) * 8u;
-  const uint64_t counters = (static_cast<uint64_t>(groups) * 4u + 7u) & ~7ull;
-  return (slots + counters + 255u) & ~255ull;
+// Workspace: kMaxGroups counter lines, then rows * kMaxSplits key slots.
+uint64_t workspace_bytes(int64_t rows) {
+  const uint64_t counters = static_cast<uint64_t>(kMaxGroups) * kCounterStride * 4u;
+  const uint64_t slots = static_cast<uint64_t>(rows) * kMaxSplits * 8u;
+  return (counters + slots + 255u) & ~255ull;
 }
 
 struct Shape {
   int block;
   int splits;
+  int j;  // loads per lane as a template constant (0: generic batches)
 };
 
-// Workgroup shape. Measured on MI355X (C2: 320 bf16 rows of 49152): 256-lane
-// workgroups, one per row, each lane streaming 24 vectors in batches of
-// kUnroll, beat both larger workgroups and split rows -- splitting adds
-// same-address atomics to the epilogue. Rows are split only when there are
-// fewer rows than CUs, keeping at least one full batch of loads per lane.
-Shape choose_shape(int64_t rows, int64_t vocab, int elem_bytes) {
+// Workgroup shape. Each row is cut into `splits` equal segments; the split
+// count minimises the bytes on the busiest CU, ceil(rows*splits / CUs)
+// segments of ceil(nvec/splits) vectors each, preferring fewer splits on
+// near-ties (each split adds one key to the epilogue). Measured on MI355X
+// (C2: 320 bf16 rows of 49152): 4 splits = 5 equal workgroups per CU, 6 loads
+// per lane, all in flight at once.
+Shape choose_shape(int64_t rows, int64_t vocab, int elem_bytes, int rows_per_group) {
   const int64_t nvec = vocab * elem_bytes / 16 > 0 ? vocab * elem_bytes / 16 : 1;
   int64_t block = option("greedy_block");
   if (block != 256 && block != 512 && block != 1024) block = 256;
+  const int64_t max_by_len = nvec / block > 1 ? nvec / block : 1;  // >= one vector per lane
+  int64_t max_s = max_by_len < kMaxSplits ? max_by_len : kMaxSplits;
+  const int64_t max_by_lds = 4 * kMaxRowsPerGroup / rows_per_group;  // finalizer key buffer
+  if (max_s > max_by_lds) max_s = max_by_lds;
   int64_t s = option("greedy_splits");
   if (s <= 0) {
     const int64_t cus = static_cast<int64_t>(device_cu_count());
-    s = rows >= cus ? 1 : (cus + rows - 1) / rows;
-    const int64_t by_loads = nvec / (block * kUnroll);
-    if (s > by_loads) s = by_loads;
+    double best = 0.0;
+    s = 1;
+    for (int64_t c = 1; c <= max_s; ++c) {
+      const double busiest = static_cast<double>((rows * c + cus - 1) / cus) * static_cast<double>((nvec + c - 1) / c);
+      if (c == 1 || busiest < best * 0.97) {
+        best = busiest;
+        s = c;
+      }
+    }
   }
-  const int64_t max_s = nvec / (block * 2) > 0 ? nvec / (block * 2) : 1;
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
-  if (s > 64) s = 64;
-  return Shape{static_cast<int>(block), static_cast<int>(s)};
+  const int64_t seg = (nvec + s - 1) / s;
+  int j = 0;
+  if (block == 256 && seg % 256 == 0 && seg / 256 >= 1 && seg / 256 <= 8 && nvec % s == 0) j = static_cast<int>(seg / 256);
+  return Shape{static_cast<int>(block), static_cast<int>(s), j};
 }
 
-template <int DT, int BLOCK>
-void launch_block(const GreedyParams& p, int64_t total_rows, bool vec, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(total_rows * p.splits));
-  if (vec) {
-    hipLaunchKernelGGL((greedy_kernel<DT, true, BLOCK>), grid, dim3(BLOCK), 0, st, p);
-  } else {
-    hipLaunchKernelGGL((greedy_kernel<DT, false, BLOCK>), grid, dim3(BLOCK), 0, st, p);
-  }
+template <int DT, bool VEC, int BLOCK, int J>
+void launch_one(const GreedyParams& p, int64_t groups, hipStream_t st) {
+  const dim3 grid = p.direct ? dim3(static_cast<unsigned>(groups))
+                             : dim3(static_cast<unsigned>(p.splits), static_cast<unsigned>(p.rows_per_group),
+                                    static_cast<unsigned>(groups));
+  hipLaunchKernelGGL((greedy_kernel<DT, VEC, BLOCK, J>), grid, dim3(BLOCK), 0, st, p);
 }
 
 template <int DT>
-void launch_dt(const GreedyParams& p, int block, int64_t total_rows, bool vec, hipStream_t st) {
-  if (block == 1024) {
-    launch_block<DT, 1024>(p, total_rows, vec, st);
-  } else if (block == 512) {
-    launch_block<DT, 512>(p, total_rows, vec, st);
+void launch_dt(const GreedyParams& p, const Shape& sh, int64_t groups, bool vec, hipStream_t st) {
+  if (!vec) {
+    if (sh.block == 1024) {
+      launch_one<DT, false, 1024, 0>(p, groups, st);
+    } else if (sh.block == 512) {
+      launch_one<DT, false, 512, 0>(p, groups, st);
+    } else {
+      launch_one<DT, false, 256, 0>(p, groups, st);
+    }
+    return;
+  }
+  if (sh.block == 1024) {
+    launch_one<DT, true, 1024, 0>(p, groups, st);
+  } else if (sh.block == 512) {
+    launch_one<DT, true, 512, 0>(p, groups, st);
   } else {
-    launch_block<DT, 256>(p, total_rows, vec, st);
+    switch (sh.j) {
+      case 1: launch_one<DT, true, 256, 1>(p, groups, st); break;
+      case 2: launch_one<DT, true, 256, 2>(p, groups, st); break;
+      case 3: launch_one<DT, true, 256, 3>(p, groups, st); break;
+      case 4: launch_one<DT, true, 256, 4>(p, groups, st); break;
+      case 5: launch_one<DT, true, 256, 5>(p, groups, st); break;
+      case 6: launch_one<DT, true, 256, 6>(p, groups, st); break;
+      case 7: launch_one<DT, true, 256, 7>(p, groups, st); break;
+      case 8: launch_one<DT, true, 256, 8>(p, groups, st); break;
+      default: launch_one<DT, true, 256, 0>(p, groups, st); break;
+    }
   }
 }
 
-int launch(const GreedyParams& p, int dtype, int block, int64_t total_rows, bool vec, hipStream_t st) {
+int launch(const GreedyParams& p, int dtype, const Shape& sh, int64_t groups, bool vec, hipStream_t st) {
   switch (dtype) {
-    case LS_DTYPE_F32: launch_dt<F32>(p, block, total_rows, vec, st); break;
-    case LS_DTYPE_BF16: launch_dt<BF16>(p, block, total_rows, vec, st); break;
-    case LS_DTYPE_F16: launch_dt<F16>(p, block, total_rows, vec, st); break;
+    case LS_DTYPE_F32: launch_dt<F32>(p, sh, groups, vec, st); break;
+    case LS_DTYPE_BF16: launch_dt<BF16>(p, sh, groups, vec, st); break;
+    case LS_DTYPE_F16: launch_dt<F16>(p, sh, groups, vec, st); break;
     default: return fail(LS_ERR_VALUE, "unsupported logits dtype");
   }
   return check_launch("greedy kernel launch");
@@ -262,7 +320,7 @@ extern "C" {
 
 uint64_t ls_argmax_rows_workspace(int64_t rows, int64_t vocab) {
   (void)vocab;
-  return rows > 0 ? workspace_bytes(rows, rows) : 0;
+  return rows > 0 ? workspace_bytes(rows < kMaxGroups ? rows : kMaxGroups) : 0;
 }
 
 int ls_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t row_stride,
@@ -272,34 +330,37 @@ int ls_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab, i
   if (rows < 0 || vocab <= 0 || vocab > 0x7fffffffLL) return fail(LS_ERR_VALUE, "argmax: invalid rows/vocab");
   if (rows == 0) return LS_OK;
   if (logits == nullptr || out == nullptr) return fail(LS_ERR_VALUE, "argmax: NULL pointer");
-  if (rows > 0x7fffffffLL / 64) return fail(LS_ERR_VALUE, "argmax: too many rows");
+  if (rows > 0x7fffffffLL) return fail(LS_ERR_VALUE, "argmax: too many rows");
   GreedyParams p{};
   p.target = static_cast<const char*>(logits);
-  p.t_pstride = row_stride * eb;
+  p.t_bstride = row_stride * eb;  // argmax rows are groups of one row
   p.vocab = vocab;
   p.k = 0;
   p.rows_per_group = 1;
-  const Shape shape = choose_shape(rows, vocab, eb);
-  p.splits = shape.splits;
-  p.out = out;
-  if (p.splits > 1) {
-    if (workspace == nullptr || ws_bytes < workspace_bytes(rows, rows)) {
-      // Without scratch fall back to one workgroup per row.
-      p.splits = 1;
-    } else {
-      p.slots = static_cast<uint64_t*>(workspace);
-      p.counters = reinterpret_cast<uint32_t*>(p.slots + rows);
-    }
-  }
-  p.direct = p.splits == 1;
   const bool vec = aligned16(logits) && ((row_stride * eb) % 16 == 0) && ((vocab * eb) % 16 == 0);
-  return launch(p, dtype, shape.block, rows, vec, static_cast<hipStream_t>(stream));
+  Shape shape = choose_shape(rows, vocab, eb, 1);
+  if (shape.splits > 1 && (rows > kMaxGroups || workspace == nullptr || ws_bytes < workspace_bytes(rows))) {
+    // Without scratch (or beyond the counter area) one workgroup per row.
+    shape.splits = 1;
+    shape.j = 0;
+  }
+  if (!vec) shape.j = 0;
+  p.splits = shape.splits;
+  p.direct = p.splits == 1;
+  p.out = out;
+  p.nvec = vocab * eb / 16;
+  p.seg = vec ? (p.nvec + p.splits - 1) / p.splits : (vocab + p.splits - 1) / p.splits;
+  if (!p.direct) {
+    p.counters = static_cast<uint32_t*>(workspace);
+    p.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kMaxGroups * kCounterStride * 4);
+  }
+  return launch(p, dtype, shape, rows, vec, static_cast<hipStream_t>(stream));
 }
 
 uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab) {
   (void)vocab;
   if (batch <= 0 || k < 0) return 0;
-  return workspace_bytes(batch * (2 * k + 1), batch);
+  return workspace_bytes(batch * (2 * k + 1));
 }
 
 int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int64_t target_pos_stride,
@@ -309,8 +370,8 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int
                      uint64_t ws_bytes, ls_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(LS_ERR_VALUE, "unsupported logits dtype");
-  if (batch < 0 || k < 1 || k > 64 || vocab <= 0 || vocab > 0x7fffffffLL)
-    return fail(LS_ERR_VALUE, "greedy_verify: invalid batch/k/vocab (need 1 <= k <= 64)");
+  if (batch < 0 || batch > kMaxGroups || k < 1 || k > 64 || vocab <= 0 || vocab > 0x7fffffffLL)
+    return fail(LS_ERR_VALUE, "greedy_verify: need 0 <= batch <= 16384, 1 <= k <= 64, 0 < vocab < 2^31");
   if (batch == 0) return LS_OK;
   if (target_logits == nullptr || accept_len == nullptr || tokens == nullptr)
     return fail(LS_ERR_VALUE, "greedy_verify: NULL pointer");
@@ -318,8 +379,7 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int
     return fail(LS_ERR_VALUE, "greedy_verify: need draft logits or draft tokens");
   const int rpg = static_cast<int>(draft_logits ? 2 * k + 1 : k + 1);
   const int64_t total = batch * rpg;
-  if (total > 0x7fffffffLL / 64) return fail(LS_ERR_VALUE, "greedy_verify: too many rows");
-  if (workspace == nullptr || ws_bytes < workspace_bytes(total, batch))
+  if (workspace == nullptr || ws_bytes < workspace_bytes(total))
     return fail(LS_ERR_VALUE, "greedy_verify: workspace too small");
   GreedyParams p{};
   p.target = static_cast<const char*>(target_logits);
@@ -332,19 +392,22 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int
   p.vocab = vocab;
   p.k = static_cast<int>(k);
   p.rows_per_group = rpg;
-  const Shape shape = choose_shape(total, vocab, eb);
-  p.splits = shape.splits;
-  p.direct = 0;
-  p.accept_len = accept_len;
-  p.tokens = tokens;
-  p.row_argmax = row_argmax;
-  p.slots = static_cast<uint64_t*>(workspace);
-  p.counters = reinterpret_cast<uint32_t*>(p.slots + total);
   bool vec = aligned16(target_logits) && (p.t_bstride % 16 == 0) && (p.t_pstride % 16 == 0) &&
              ((vocab * eb) % 16 == 0);
   if (draft_logits)
     vec = vec && aligned16(draft_logits) && (p.d_bstride % 16 == 0) && (p.d_pstride % 16 == 0);
-  return launch(p, dtype, shape.block, total, vec, static_cast<hipStream_t>(stream));
+  Shape shape = choose_shape(total, vocab, eb, rpg);
+  if (!vec) shape.j = 0;
+  p.splits = shape.splits;
+  p.direct = 0;
+  p.nvec = vocab * eb / 16;
+  p.seg = vec ? (p.nvec + p.splits - 1) / p.splits : (vocab + p.splits - 1) / p.splits;
+  p.accept_len = accept_len;
+  p.tokens = tokens;
+  p.row_argmax = row_argmax;
+  p.counters = static_cast<uint32_t*>(workspace);
+  p.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kMaxGroups * kCounterStride * 4);
+  return launch(p, dtype, shape, batch, vec, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -101,27 +101,6 @@ struct SampParams {
 // ---------------------------------------------------------------------------
 // Device-coherent publication helpers (see ls_common.hpp for the protocol).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void store_sc(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_sc64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t load_sc(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_sc64(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Wait until every store of this lane has been acknowledged by the device
-// coherence point (vmcnt also counts stores on gfx9), and keep the compiler
-// from moving memory operations across.
-__device__ __forceinline__ void drain_stores() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 __device__ __forceinline__ void put_stat(RowStat* st, const RowStat& v) {
   uint32_t* w = reinterpret_cast<uint32_t*>(st);
   store_sc(w + 0, __float_as_uint(v.m));
