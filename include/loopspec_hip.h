@@ -98,14 +98,17 @@ uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
  * 16-byte aligned rows, vocab*elem_bytes a multiple of 16):
  *   x = logits; for ids in the row's history (if penalty != 1):
  *       x <- x < 0 ? x*penalty : x*RN(1/penalty);  then x <- x*RN(1/T) (T != 1);
- *   p = softmax(x) in the library's declared arithmetic (a fixed polynomial
- *   exp, exact 2^-46 fixed-point masses, p = RN(e / RN32(mass)));
+ *   p = softmax(x) in the library's declared arithmetic: chunks of 8192
+ *   elements, e = exp(x - chunk max) by a fixed polynomial, exact 2^-46
+ *   fixed-point chunk masses combined with f_j = exp(chunk max - row max),
+ *   p = RN(RN(e * f_j) / S);
  *   top_p < 1: keep p >= c with c = max{v : sum_{p>=v} fx46(p) >= fx46(top_p)}
  *   (ties kept; the whole row if no v qualifies), renormalise by the retained
  *   mass -- the value semantics of sort + cumsum + searchsorted(right=False)
  *   + gather + where + sum of filtered_probabilities
  *   (sglang_recurrent/loopspec/sampling/distributions.py:14-86).
- *   top_k must be 0 or >= vocab (top-k filtering is not offered here).
+ *   top_k must be 0 or >= vocab (top-k filtering is not offered here);
+ *   vocab <= 262144.
  * ------------------------------------------------------------------------------ */
 
 /* Fused chain verify, one launch for B batch elements of k draft positions:
@@ -137,27 +140,32 @@ uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 
 /* Filter each logits row and draw one token per row with uniforms[row]
  * (float32 [rows]) into out_tokens (int64 [rows]); history rows as above,
- * one per logits row. Replaces prepare_sampling_probabilities followed by
- * sample_probabilities / CategoricalSampler.sample
+ * one per logits row; rows <= 65535. Workspace: ls_sample_logits_workspace
+ * bytes (no zero-fill needed). Replaces prepare_sampling_probabilities followed
+ * by sample_probabilities / CategoricalSampler.sample
  * (sglang_recurrent/loopspec/sampling/distributions.py:89-171). */
 int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows,
                      int64_t vocab, float temperature, float top_p, int64_t top_k,
                      float penalty, const int32_t* history, int64_t history_stride,
                      const int32_t* history_len, const float* uniforms, int64_t* out_tokens,
-                     ls_stream_t stream);
+                     void* workspace, uint64_t workspace_bytes, ls_stream_t stream);
+uint64_t ls_sample_logits_workspace(int64_t rows, int64_t vocab);
 
 /* Dense filtering: probs_out (optional, [rows, V] float32, row stride
  * probs_stride) receives p; filtered_out (optional) the filtered, renormalised
  * distribution (p itself when top_p == 1); cutoff_out / mass_out (optional,
- * float32 [rows]) the cutoff value and binary32 retained mass. top_p_rows
- * (optional, float32 [rows]) overrides top_p per row when top_p < 1.
+ * float32 [rows]) the cutoff value (0 when unfiltered) and binary32 retained
+ * mass. top_p_rows (optional, float32 [rows]) overrides top_p per row when
+ * top_p < 1. rows <= 65535. Workspace: ls_filter_logits_workspace bytes.
  * Replaces filtered_probabilities and the probability/cutoff part of
  * prepare_sampling_probabilities (distributions.py:14-149). */
 int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows,
                      int64_t vocab, float temperature, float top_p, const float* top_p_rows,
                      int64_t top_k, float* probs_out, int64_t probs_stride,
                      float* filtered_out, int64_t filtered_stride, float* cutoff_out,
-                     float* mass_out, ls_stream_t stream);
+                     float* mass_out, void* workspace, uint64_t workspace_bytes,
+                     ls_stream_t stream);
+uint64_t ls_filter_logits_workspace(int64_t rows, int64_t vocab);
 
 /* Top-k filtering of probability rows (float32, row stride row_stride): c_k =
  * the k-th largest value of the row (duplicates counted, 1 <= k <= vocab),

@@ -47,11 +47,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ls_spec_verify_workspace": (_U64, [_I64, _I64, _I64]),
     "ls_sample_logits": (
-        _I32, [_P, _I64, _I32, _I64, _I64, _F32, _F32, _I64, _F32, _P, _I64, _P, _P, _P, _P],
+        _I32, [_P, _I64, _I32, _I64, _I64, _F32, _F32, _I64, _F32, _P, _I64, _P, _P, _P, _P, _U64, _P],
     ),
+    "ls_sample_logits_workspace": (_U64, [_I64, _I64]),
     "ls_filter_logits": (
-        _I32, [_P, _I64, _I32, _I64, _I64, _F32, _F32, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P],
+        _I32, [_P, _I64, _I32, _I64, _I64, _F32, _F32, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _U64, _P],
     ),
+    "ls_filter_logits_workspace": (_U64, [_I64, _I64]),
     "ls_top_k_filter": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P]),
     "ls_sample_probs": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P]),
     "ls_sample_top_p": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P]),

@@ -42,12 +42,12 @@ constexpr double kFxOne = 70368744177664.0;  // 2^46
 // kExpNoBucket when t < kExpMin (e == 0).
 constexpr int kExpNoBucket = -1000;
 __device__ __forceinline__ float ls_exp_k(float t, int* k) {
-  if (!(t >= kExpMin)) {
-    *k = kExpNoBucket;
-    return 0.0f;
-  }
-  const float kf = __builtin_rintf(t * kLog2e);
-  float r = __builtin_fmaf(kf, -kLn2Hi, t);
+  // Branch-free: the polynomial runs on a clamped argument and the result is
+  // selected afterwards, so unrolled loops keep independent exps interleaved.
+  const bool in = t >= kExpMin;  // false for NaN too
+  const float tt = in ? t : 0.0f;
+  const float kf = __builtin_rintf(tt * kLog2e);
+  float r = __builtin_fmaf(kf, -kLn2Hi, tt);
   r = __builtin_fmaf(kf, -kLn2Lo, r);
   float p = kExpC6;
   p = __builtin_fmaf(p, r, kExpC5);
@@ -57,8 +57,8 @@ __device__ __forceinline__ float ls_exp_k(float t, int* k) {
   p = __builtin_fmaf(p, r, kExpC1);
   p = __builtin_fmaf(p, r, kExpC0);
   const int ki = static_cast<int>(kf);
-  *k = ki;
-  return __builtin_ldexpf(p, ki);
+  *k = in ? ki : kExpNoBucket;
+  return in ? __builtin_ldexpf(p, ki) : 0.0f;
 }
 
 __device__ __forceinline__ float ls_exp(float t) {

@@ -64,7 +64,7 @@ int64_t option(const char* name) {
 
 extern "C" {
 
-int ls_abi_version(void) { return 1; }
+int ls_abi_version(void) { return 2; }
 
 const char* ls_last_error(void) { return ls::g_last_error.c_str(); }
 

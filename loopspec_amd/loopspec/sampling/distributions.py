@@ -2,12 +2,13 @@
 
 Same functions, arguments and results as the reference
 (sglang_recurrent/loopspec/sampling/distributions.py:14-171). Softmax,
-temperature and the top-p cutoff run in one fused gfx950 pass per row (no sort:
-the cutoff is found by a mass-ordered radix select in LDS); joint top-k/top-p
-adds one row pass for the k-th largest value. The arithmetic is the library's
-declared one (a fixed polynomial exp, exact 2^-46 fixed-point masses), so
-values agree with the reference's float32 torch path to rounding while the
-cutoff rule, ties included, is the same.
+temperature and the top-p cutoff run as gfx950 kernels that read the logits
+once with one workgroup per 8192-element chunk (no sort: the cutoff is found
+by a mass-ordered radix select over the chunks' largest entries); joint
+top-k/top-p adds one row pass for the k-th largest value. The arithmetic is
+the library's declared one (chunked softmax with a fixed polynomial exp, exact
+2^-46 fixed-point masses), so values agree with the reference's float32 torch
+path to rounding while the cutoff rule, ties included, is the same.
 
 The top-p context returned by prepare_sampling_probabilities keeps arity 3 but
 carries (unfiltered probs [B, V], cutoff values [B, 1], zero ranks [B, 1]) in
@@ -44,12 +45,13 @@ def _filter(logits: torch.Tensor, temperature: float, top_p: float, thresholds: 
     mass = torch.empty(rows, dtype=torch.float32, device=logits.device)
     if cutoff is None:
         cutoff = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    ws = _lib.WORKSPACE.get(logits.device, _lib.query("ls_filter_logits_workspace", rows, vocab), "filter")
     _lib.call(
         "ls_filter_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
         float(temperature), float(top_p), _lib.ptr(thresholds), 0,
         _lib.ptr(probs), probs.stride(0) if probs is not None else 0,
         _lib.ptr(filtered), filtered.stride(0) if filtered is not None else 0,
-        cutoff.data_ptr(), mass.data_ptr(), _lib.stream(logits.device),
+        cutoff.data_ptr(), mass.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(logits.device),
     )
 
 

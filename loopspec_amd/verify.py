@@ -209,10 +209,11 @@ def sample_logits(
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=dev)
     h_ptr, h_stride, hl_ptr = _history_args(history, history_len, rows, dev) if penalty != 1.0 else (None, 0, None)
+    ws = _lib.WORKSPACE.get(dev, _lib.query("ls_sample_logits_workspace", rows, vocab), "sample")
     _lib.call(
         "ls_sample_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
         float(temperature), float(top_p), int(top_k), float(penalty), h_ptr, h_stride, hl_ptr,
-        uniforms.data_ptr(), out.data_ptr(), _lib.stream(dev),
+        uniforms.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev),
     )
     return out
 
@@ -248,11 +249,12 @@ def filter_logits(
             raise ValueError("top_p_rows must be float32 with at least one entry per row")
         top_p_rows = top_p_rows.reshape(-1).contiguous()
     probs, filt = res.get("probs"), res.get("filtered")
+    ws = _lib.WORKSPACE.get(dev, _lib.query("ls_filter_logits_workspace", rows, vocab), "filter")
     _lib.call(
         "ls_filter_logits", logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits), rows, vocab,
         float(temperature), float(top_p), _lib.ptr(top_p_rows), int(top_k),
         _lib.ptr(probs), probs.stride(0) if probs is not None else 0,
         _lib.ptr(filt), filt.stride(0) if filt is not None else 0,
-        res["cutoff"].data_ptr(), res["mass"].data_ptr(), _lib.stream(dev),
+        res["cutoff"].data_ptr(), res["mass"].data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev),
     )
     return res

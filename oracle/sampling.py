@@ -27,7 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from .numerics import (
-    F32, F64, FX_BITS, fx46, floor_u_times, ls_exp, ls_exp_k, mass_to_f32,
+    F32, F64, FX_BITS, fx46, floor_u_times, ls_exp, mass_to_f32,
 )
 
 
@@ -70,31 +70,52 @@ def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float 
     return x
 
 
+CHUNK = 8192  # elements per softmax chunk (a constant of the declared arithmetic)
+
+
 @dataclass
 class RowSoftmax:
     x: np.ndarray      # processed logits
-    m: np.float32      # max
-    e: np.ndarray      # ls_exp(x - m)
-    k: np.ndarray      # binary exponents used by ls_exp
-    s_fx: int          # exact mass of e
+    m: np.float32      # row max
+    e: np.ndarray      # ls_exp(x - m_chunk), chunk-relative
+    m_chunks: np.ndarray   # per-chunk max
+    f_chunks: np.ndarray   # ls_exp(m_chunk - m)
+    mass_chunks: list      # exact chunk masses sum fx46(e)
+    s_fx: int          # exact normaliser mass T
     s: np.float32      # binary32 normaliser
-    p: np.ndarray      # probabilities e / s
+    w: np.ndarray      # RN(e * f_chunk)
+    p: np.ndarray      # probabilities RN(w / s)
 
 
 def softmax_row(x: np.ndarray) -> RowSoftmax:
-    """softmax(x) in the declared arithmetic (distributions.py:44-48).
+    """softmax(x) in the declared chunked arithmetic (distributions.py:44-48).
 
-    m = max(x); e_i = ls_exp(x_i - m); S = RN32(sum fx46(e_i)) * 2^-46;
-    p_i = RN(e_i / S).
+    The row is cut into chunks of CHUNK elements. Chunk j: m_j = max x,
+    e_i = ls_exp(x_i - m_j), M_j = sum fx46(e_i) (exact). Row: m = max m_j,
+    f_j = ls_exp(m_j - m), T = sum_j floor(f_j * M_j) (exact), S = RN32(T) 2^-46,
+    w_i = RN(e_i * f_j), p_i = RN(w_i / S). For rows of at most CHUNK elements
+    this is e_i = ls_exp(x_i - m), p_i = RN(e_i / S). Every chunk can be
+    processed on its own before the row-wide values are known, which is what
+    lets the kernels read the logits once with many workgroups per row.
     """
     x = np.asarray(x, dtype=F32)
-    m = F32(np.max(x))
-    t = (x - m).astype(F32)
-    e, k = ls_exp_k(t)
-    s_fx = int(fx46(e).sum(dtype=np.uint64))
+    v = len(x)
+    nch = -(-v // CHUNK)
+    with np.errstate(invalid="ignore"):
+        m_chunks = np.array([np.max(x[j * CHUNK:(j + 1) * CHUNK]) for j in range(nch)], dtype=F32)
+    m = F32(np.max(m_chunks))
+    cidx = np.arange(v) // CHUNK
+    with np.errstate(invalid="ignore"):
+        t = (x - m_chunks[cidx]).astype(F32)
+    e = ls_exp(t)
+    mass_chunks = [int(fx46(e[j * CHUNK:(j + 1) * CHUNK]).sum(dtype=np.uint64)) for j in range(nch)]
+    with np.errstate(invalid="ignore"):
+        f_chunks = ls_exp((m_chunks - m).astype(F32))
+    s_fx = sum(floor_u_times(f_chunks[j], mass_chunks[j]) for j in range(nch))
     s = mass_to_f32(s_fx)
-    p = (e / s).astype(F32)
-    return RowSoftmax(x, m, e, k, s_fx, s, p)
+    w = (e * f_chunks[cidx]).astype(F32)
+    p = (w / s).astype(F32)
+    return RowSoftmax(x, m, e, m_chunks, f_chunks, mass_chunks, s_fx, s, w, p)
 
 
 def threshold_fx(top_p: float) -> int:
@@ -371,4 +392,4 @@ def rejection_run(first, target, second, token: int, has_second: bool, u0: float
     return (int(token) if a else sampled, int(a), int(has_second and not a))
 
 
-__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "ls_exp"]
+__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "ls_exp", "CHUNK"]

@@ -26,6 +26,34 @@ def test_softmax_matches_torch():
         assert np.max(np.abs(soft.p[big] - ref32[big]) / ref32[big]) < 1e-5  # the contract tolerance
 
 
+def test_chunked_softmax_closed_forms():
+    c = os_.CHUNK
+    # A row no longer than one chunk is the plain formula e = ls_exp(x - m), p = RN(e / S).
+    x = (np.random.default_rng(1).standard_normal(c) * 3).astype(np.float32)
+    soft = os_.softmax_row(x)
+    e = nm.ls_exp((x - x.max()).astype(np.float32))
+    s = nm.mass_to_f32(int(nm.fx46(e).sum(dtype=np.uint64)))
+    assert np.array_equal(soft.p, (e / s).astype(np.float32))
+    # A constant row of n chunks: every e = 1, every f = 1, p = RN(1 / RN32(V)).
+    v = 3 * c + 5
+    soft = os_.softmax_row(np.full(v, 2.5, np.float32))
+    assert soft.s_fx == v << 46 and np.all(soft.p == np.float32(1) / np.float32(v))
+    # A chunk of -inf contributes nothing and the others are unaffected; the
+    # maximum may sit in any chunk.
+    x = (np.random.default_rng(2).standard_normal(3 * c) * 2).astype(np.float32)
+    x[c:2 * c] = -np.inf
+    x[2 * c + 7] = 30.0
+    soft = os_.softmax_row(x)
+    assert soft.f_chunks[1] == 0 and soft.mass_chunks[1] == 0 and not soft.p[c:2 * c].any()
+    assert soft.f_chunks[2] == 1 and soft.p.argmax() == 2 * c + 7
+    ref = torch.softmax(torch.from_numpy(x).double(), -1).numpy()
+    big = ref > 1e-30
+    assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 3e-6
+    # The normaliser is the exact sum of the chunk masses scaled by f_j.
+    assert soft.s_fx == sum(nm.floor_u_times(soft.f_chunks[j], soft.mass_chunks[j]) for j in range(3))
+    assert abs(float(soft.p.astype(np.float64).sum()) - 1.0) < 1e-5
+
+
 def test_temperature_and_penalty_closed_form():
     x = np.float32([-2.0, -0.5, 0.0, 0.5, 3.0])
     y = os_.process_logits(x, temperature=0.7, penalty=1.1, history=[0, 3, 3, 4])
