@@ -9,12 +9,8 @@
 namespace ls {
 
 __device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint64_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  (void)lane;
+  return wave_scan_add_u64(x);
 }
 
 // Exclusive scan in lane order; *total receives the block sum. smem >= BLOCK/64.

@@ -98,27 +98,84 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave / block reductions (wave64).
+// Wave scans and reductions (wave64) on DPP: row_shr 1, 2, 4, 8 build the
+// inclusive scan inside each row of 16 lanes, row_bcast:15 and row_bcast:31
+// carry the row totals forward, all in the VALU (a __shfl is an LDS
+// ds_bpermute round trip per step). Every lane of the wave must be active.
+// Reductions read the scan's last lane.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp32(uint32_t ident, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(ident), static_cast<int>(v), CTRL, ROWS, 0xf, false));
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp64(uint64_t ident, uint64_t v) {
+  const uint32_t lo = dpp32<CTRL, ROWS>(static_cast<uint32_t>(ident), static_cast<uint32_t>(v));
+  const uint32_t hi = dpp32<CTRL, ROWS>(static_cast<uint32_t>(ident >> 32), static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Inclusive scans.
+__device__ __forceinline__ uint32_t wave_scan_add_u32(uint32_t v) {
+  v += dpp32<kDppRowShr1, 0xf>(0u, v);
+  v += dpp32<kDppRowShr2, 0xf>(0u, v);
+  v += dpp32<kDppRowShr4, 0xf>(0u, v);
+  v += dpp32<kDppRowShr8, 0xf>(0u, v);
+  v += dpp32<kDppRowBcast15, 0xa>(0u, v);
+  v += dpp32<kDppRowBcast31, 0xc>(0u, v);
   return v;
 }
 
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+__device__ __forceinline__ uint64_t wave_scan_add_u64(uint64_t v) {
+  v += dpp64<kDppRowShr1, 0xf>(0ull, v);
+  v += dpp64<kDppRowShr2, 0xf>(0ull, v);
+  v += dpp64<kDppRowShr4, 0xf>(0ull, v);
+  v += dpp64<kDppRowShr8, 0xf>(0ull, v);
+  v += dpp64<kDppRowBcast15, 0xa>(0ull, v);
+  v += dpp64<kDppRowBcast31, 0xc>(0ull, v);
   return v;
 }
 
+__device__ __forceinline__ uint64_t wave_scan_max_u64(uint64_t v) {
+  uint64_t w;
+  w = dpp64<kDppRowShr1, 0xf>(0ull, v); v = w > v ? w : v;
+  w = dpp64<kDppRowShr2, 0xf>(0ull, v); v = w > v ? w : v;
+  w = dpp64<kDppRowShr4, 0xf>(0ull, v); v = w > v ? w : v;
+  w = dpp64<kDppRowShr8, 0xf>(0ull, v); v = w > v ? w : v;
+  w = dpp64<kDppRowBcast15, 0xa>(0ull, v); v = w > v ? w : v;
+  w = dpp64<kDppRowBcast31, 0xc>(0ull, v); v = w > v ? w : v;
+  return v;
+}
+
+__device__ __forceinline__ float wave_scan_max_f32(float v) {
+  constexpr uint32_t kNegInf = 0xff800000u;
+  v = nmax(v, __uint_as_float(dpp32<kDppRowShr1, 0xf>(kNegInf, __float_as_uint(v))));
+  v = nmax(v, __uint_as_float(dpp32<kDppRowShr2, 0xf>(kNegInf, __float_as_uint(v))));
+  v = nmax(v, __uint_as_float(dpp32<kDppRowShr4, 0xf>(kNegInf, __float_as_uint(v))));
+  v = nmax(v, __uint_as_float(dpp32<kDppRowShr8, 0xf>(kNegInf, __float_as_uint(v))));
+  v = nmax(v, __uint_as_float(dpp32<kDppRowBcast15, 0xa>(kNegInf, __float_as_uint(v))));
+  v = nmax(v, __uint_as_float(dpp32<kDppRowBcast31, 0xc>(kNegInf, __float_as_uint(v))));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lane_bcast_u32(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+__device__ __forceinline__ uint64_t lane_bcast_u64(uint64_t v, int lane) {
+  return (static_cast<uint64_t>(lane_bcast_u32(static_cast<uint32_t>(v >> 32), lane)) << 32) |
+         lane_bcast_u32(static_cast<uint32_t>(v), lane);
+}
+
+// Reductions, result on every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return lane_bcast_u64(wave_scan_max_u64(v), kWave - 1); }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { return lane_bcast_u64(wave_scan_add_u64(v), kWave - 1); }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = nmax(v, __shfl_xor(v, o));
-  return v;
+  return __uint_as_float(lane_bcast_u32(__float_as_uint(wave_scan_max_f32(v)), kWave - 1));
 }
 
 // Block-wide reductions; `smem` needs BLOCK/64 slots. Result broadcast to all.

@@ -23,12 +23,8 @@ constexpr int kScanBlock = 1024;
 constexpr int kCopyBlock = 256;
 
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  (void)lane;
+  return wave_scan_add_u32(x);
 }
 
 // Exclusive scan over a 1024-lane block; *total receives the sum.

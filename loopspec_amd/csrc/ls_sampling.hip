@@ -53,6 +53,7 @@ constexpr int kSupCap = 2048;                // support entries per row in the w
 constexpr int kBins = 2048;                  // radix digits per round
 constexpr int kBinsPerLane = kBins / kRB;
 constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
+constexpr int kChunkWgsPerCu = 3;            // persistent chunk workgroups per CU
 constexpr int64_t kMaxSpecBatch = 16384;
 constexpr int64_t kMaxGridYZ = 65535;
 
@@ -161,72 +162,91 @@ __device__ __forceinline__ float chunk_p(float x, float mj, float m, float s) {
 }
 
 // ===========================================================================
+// bitmap_kernel: the penalty bitmap of each group's token history
+// ===========================================================================
+constexpr int kBmB = 1024;
+
+__global__ __launch_bounds__(kBmB) void bitmap_kernel(const SampParams p) {
+  __shared__ uint32_t bm[kMaxVocab / 32];
+  const int t = threadIdx.x;
+  const int64_t g = blockIdx.x;
+  const int words = p.bm_words;
+  for (int w = t; w < words; w += kBmB) bm[w] = 0u;
+  __syncthreads();
+  const int n = p.hist_len[g];
+  const int32_t* h = p.hist + g * p.hist_stride;
+  for (int i = t; i < n; i += kBmB) {
+    const int id = h[i];
+    if (static_cast<unsigned>(id) < static_cast<unsigned>(p.vocab))
+      __hip_atomic_fetch_or(&bm[id >> 5], 1u << (id & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  uint32_t* out = p.bitmap + g * words;
+  for (int w = t; w < words; w += kBmB) out[w] = bm[w];
+}
+
+// ===========================================================================
 // chunk_kernel
 // ===========================================================================
 struct ChunkShared {
-  uint32_t bitmap[kChunk / 32];        // penalty bits of the chunk's index range
   uint32_t oct[kCW][kOct];             // per-wave octave counts
   float wmax[kCW];
   uint64_t wmass[kCW];
   int wcnt[8][kCW];                    // candidates per (vector slot, wave)
 };
 
-// Inclusive wave scan of a 32-bit value.
+// Inclusive wave scan of a 32-bit value (DPP).
 __device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  (void)lane;
+  return wave_scan_add_u32(x);
 }
 
-// Three barriers: after the chunk max, after the mass / histogram (every
-// wave then derives K on its own), after the per-(slot, wave) candidate
-// counts (every wave then derives its output offsets on its own). The row
-// data stays in the load registers (fp32: x and then e in place).
-template <int DT>
-__global__ __launch_bounds__(kCB, 6) void chunk_kernel(const SampParams p) {
+// Loads of one chunk (clamped: lanes past the chunk end re-read its last
+// vector), plus, with a penalty, the bitmap word of each vector (the EPV bits
+// of a 16-byte vector always sit in one 32-bit word).
+template <int DT, int NVC>
+__device__ __forceinline__ void load_chunk(const SampParams& p, int item, u32x4 (&d)[NVC], uint32_t (&pw)[NVC]) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int NVC = kChunk / (kCB * EPV);  // vectors per lane: 8 (f32) or 4
-  constexpr int NE = NVC * EPV;              // 32 elements per lane
-  __shared__ ChunkShared sh;
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  const int cj = blockIdx.x, jr = blockIdx.y;
-  const int64_t g = blockIdx.z;
-  const int64_t r = g * p.rpg + jr;
-  const char* rowp = row_of(p, g, jr);
+  const int r = item / p.nch;
+  const int cj = item - r * p.nch;
+  const int g = r / p.rpg;
+  const int jr = r - g * p.rpg;
   const int c0 = cj * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
-  const u32x4* src = reinterpret_cast<const u32x4*>(rowp) + c0 / EPV;
-
-  // 1. loads (clamped: lanes past the chunk end re-read its last vector)
-  u32x4 d[NVC];
+  const u32x4* src = reinterpret_cast<const u32x4*>(row_of(p, g, jr)) + c0 / EPV;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    const int v = u * kCB + t;
+    const int v = u * kCB + static_cast<int>(threadIdx.x);
     d[u] = __builtin_nontemporal_load(src + (v < nvc ? v : nvc - 1));
   }
+  if (p.use_pen) {
+    const uint32_t* bm = p.bitmap + static_cast<int64_t>(g) * p.bm_words + c0 / 32;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) pw[u] = bm[((u * kCB + static_cast<int>(threadIdx.x)) * EPV) >> 5];
+  }
+}
+
+// One chunk. Three barriers: after the chunk max, after the mass / histogram
+// (every wave then derives K on its own), after the per-(slot, wave)
+// candidate counts (every wave then derives its output offsets on its own).
+// The LDS of the previous chunk is safe to reuse without a barrier: every
+// read of it precedes a barrier that each wave passes before the writes here.
+template <int DT, int NVC>
+__device__ __forceinline__ void process_chunk(const SampParams& p, ChunkShared& sh, int item, const u32x4 (&d)[NVC],
+                                              const uint32_t (&pw)[NVC]) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int NE = NVC * EPV;  // 32 elements per lane
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int r = item / p.nch;
+  const int cj = item - r * p.nch;
+  const int g = r / p.rpg;
+  const int jr = r - g * p.rpg;
+  const int c0 = cj * kChunk;
+  const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
+  const int nvc = nel / EPV;
   const Xf xf = make_xf(p);
   sh.oct[wid][lane] = 0u;
-  // 2. penalty bits of [c0, c0 + nel) (while the loads fly)
-  if (p.use_pen) {
-    sh.bitmap[t] = 0u;
-    __syncthreads();
-    const int n = p.hist_len[g];
-    const int32_t* h = p.hist + g * p.hist_stride;
-    for (int i = t; i < n; i += kCB) {
-      const int id = h[i] - c0;
-      if (static_cast<unsigned>(id) < static_cast<unsigned>(nel))
-        __hip_atomic_fetch_or(&sh.bitmap[id >> 5], 1u << (id & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    __syncthreads();
-    if (jr == 0) {  // publish the group's bits of this chunk for row_kernel
-      uint32_t* gb = p.bitmap + g * p.bm_words + c0 / 32;
-      if (t < (nel + 31) / 32) gb[t] = sh.bitmap[t];
-    }
-  }
   // 3. processed logits x (kept as binary32 bit patterns) and the chunk max
   uint32_t xe[NE];
   float mx = -__builtin_inff();
@@ -236,7 +256,7 @@ __global__ __launch_bounds__(kCB, 6) void chunk_kernel(const SampParams p) {
     for (int u = 0; u < NVC; ++u) {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
-        const bool seen = xf.use_pen && bit_of(sh.bitmap, (u * kCB + t) * EPV + e);
+        const bool seen = xf.use_pen && ((pw[u] >> ((((u * kCB + t) * EPV) & 31) + e)) & 1u);
         xe[u * EPV + e] = __float_as_uint(xform_seen(xf, vec_elem<DT>(d[u], e), seen));
       }
     }
@@ -301,7 +321,7 @@ __global__ __launch_bounds__(kCB, 6) void chunk_kernel(const SampParams p) {
     for (int e = 0; e < EPV; ++e) c += xe[u * EPV + e] >= thr_bits ? 1u : 0u;
     cs[u] = c;
     int tot = 0;
-    if (__ballot(c != 0)) tot = __shfl(static_cast<int>(wave_scan_u32(c, lane)), kWave - 1);
+    if (__ballot(c != 0)) tot = static_cast<int>(lane_bcast_u32(wave_scan_u32(c, lane), kWave - 1));
     if (lane == 0) sh.wcnt[u][wid] = tot;
   }
   __syncthreads();
@@ -310,15 +330,16 @@ __global__ __launch_bounds__(kCB, 6) void chunk_kernel(const SampParams p) {
   int flat = 0;
   if (lane < NVC * kCW) flat = sh.wcnt[lane / kCW][lane % kCW];
   const int incl = static_cast<int>(wave_scan_u32(static_cast<uint32_t>(flat), lane));
-  const int total = __shfl(incl, NVC * kCW - 1);
-  uint64_t* out = p.cands + (r * p.nch + cj) * static_cast<int64_t>(kChunkCand);
+  const int total = static_cast<int>(lane_bcast_u32(static_cast<uint32_t>(incl), NVC * kCW - 1));
+  uint64_t* out = p.cands + (static_cast<int64_t>(r) * p.nch + cj) * kChunkCand;
   const int cap = p.chunk_cap;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
     const uint32_t c = cs[u];
     if (__ballot(c != 0)) {
       const int slot = u * kCW + wid;
-      const int base = __shfl(incl, slot) - __shfl(flat, slot);
+      const int base = static_cast<int>(lane_bcast_u32(static_cast<uint32_t>(incl), slot) -
+                                        lane_bcast_u32(static_cast<uint32_t>(flat), slot));
       int pos = base + static_cast<int>(wave_scan_u32(c, lane) - c);
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
@@ -340,7 +361,33 @@ __global__ __launch_bounds__(kCB, 6) void chunk_kernel(const SampParams p) {
     rec.flags = K >= kOct ? kChunkComplete : 0u;
     rec.mass = sh.wmass[0] + sh.wmass[1] + sh.wmass[2] + sh.wmass[3];
     rec.pad = 0;
-    p.chunks[r * p.nch + cj] = rec;
+    p.chunks[static_cast<int64_t>(r) * p.nch + cj] = rec;
+  }
+}
+
+// Persistent over (row, chunk) items in row-major order, double-buffered: the
+// next item's loads are in flight while the current one is processed.
+template <int DT>
+__global__ __launch_bounds__(kCB, 3) void chunk_kernel(const SampParams p, int items) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int NVC = kChunk / (kCB * EPV);  // vectors per lane: 8 (f32) or 4
+  __shared__ ChunkShared sh;
+  int item = blockIdx.x;
+  if (item >= items) return;
+  u32x4 cur[NVC], nxt[NVC];
+  uint32_t pcur[NVC] = {}, pnxt[NVC] = {};
+  load_chunk<DT, NVC>(p, item, cur, pcur);
+  while (true) {
+    const int next = item + static_cast<int>(gridDim.x);
+    if (next < items) load_chunk<DT, NVC>(p, next, nxt, pnxt);
+    process_chunk<DT, NVC>(p, sh, item, cur, pcur);
+    if (next >= items) break;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      cur[u] = nxt[u];
+      pcur[u] = pnxt[u];
+    }
+    item = next;
   }
 }
 
@@ -368,12 +415,8 @@ struct RowShared {
 };
 
 __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint64_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  (void)lane;
+  return wave_scan_add_u64(x);
 }
 
 // Exclusive scan in lane order over the 1024 lanes; *total receives the sum.
@@ -528,8 +571,8 @@ __device__ bool select_candidates(RowShared& sh, int n, uint64_t thr, float* cut
     const uint64_t w = lane < cnt ? sh.gw[lane] : 0;
     uint64_t A = above;
     for (int j = 0; j < cnt; ++j) {
-      const uint32_t bj = __shfl(b, j);
-      const uint64_t wj = __shfl(w, j);
+      const uint32_t bj = lane_bcast_u32(b, j);
+      const uint64_t wj = lane_bcast_u64(w, j);
       A += bj >= b ? wj : 0;
     }
     const bool ok = lane < cnt && A >= thr;
@@ -859,12 +902,7 @@ __global__ __launch_bounds__(kRB, 4) void row_kernel(const SampParams p) {
     const float f = lane < nch ? ls_exp(rec.m - rm) : 0.0f;
     const uint64_t T = wave_sum_u64(lane < nch ? floor_u_times(f, rec.mass) : 0);
     const uint32_t cnt = lane < nch ? rec.n : 0u;
-    uint32_t inc = cnt;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o);
-      if (lane >= o) inc += y;
-    }
+    const uint32_t inc = wave_scan_add_u32(cnt);
     if (lane < nch) {
       sh.cm[lane] = rec.m;
       sh.cf[lane] = f;
@@ -1103,7 +1141,10 @@ int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChu
 template <int DT, int MODE>
 void launch_dt(const SampParams& p, int64_t groups, hipStream_t st) {
   const unsigned gz = static_cast<unsigned>(groups);
-  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(p.nch, p.rpg, gz), dim3(kCB), 0, st, p);
+  if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(gz), dim3(kBmB), 0, st, p);
+  const int items = static_cast<int>(groups * p.rpg * p.nch);
+  const int wgs = static_cast<int>(device_cu_count()) * kChunkWgsPerCu;
+  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(items < wgs ? items : wgs), dim3(kCB), 0, st, p, items);
   hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(p.rpg, gz), dim3(kRB), 0, st, p);
   if constexpr (MODE == kModeDense) {
     hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.nch, 1, gz), dim3(kCB), 0, st, p);
