@@ -1,15 +1,16 @@
 // Declared arithmetic of the sampling path, device side.
 //
 // Every operation here is exactly reproducible: binary32 mul/add/div with
-// round-to-nearest-even, single-rounding fma (v_fma_f32), v_rndne_f32, exact
-// power-of-two scaling (v_ldexp_f32) and integer arithmetic. The library is
-// compiled with -ffp-contract=off, so no other fusion happens. The same
-// sequence of operations is restated on the CPU (oracle/numerics.py) and the
-// two agree bit for bit.
+// round-to-nearest-even, single-rounding fma (v_fma_f32), v_rndne_f32, v_max_f32
+// (a NaN operand yields the other one), exact power-of-two scaling
+// (v_ldexp_f32) and integer arithmetic. The library is compiled with
+// -ffp-contract=off, so no other fusion happens. The same sequence of
+// operations is restated on the CPU (oracle/numerics.py) and the two agree
+// bit for bit.
 //
-//  ls_exp(t)    Cody-Waite reduction k = rint(RN(t*log2e)), r = t - k*ln2 in two
-//               fmas, e^r by a degree-6 polynomial (Horner, fma), result
-//               P(r)*2^k; t < -87 (or NaN) gives 0. Within 2 ulp of exp.
+//  exp2q(t)     k = rint(max(t, -200)), r = t - k (exact), 2^r by a degree-5
+//               polynomial (Horner, fma), result P(r) * 2^k; NaN gives 0.
+//               Within 4 ulp of 2^t.
 //  fx46(w)      floor(w * 2^46): masses of weights in [0, 1] as exact integers.
 //               Any summation order gives the same total.
 //  u64_to_f32   round-to-nearest-even of an exact mass; mass_to_f32 scales by
@@ -23,47 +24,35 @@
 namespace ls {
 
 constexpr float kLog2e = 1.44269504f;          // 0x3FB8AA3B
-constexpr float kLn2Hi = 0.693145752f;         // 0x3F317200, 16 significant bits
-constexpr float kLn2Lo = 1.42860677e-06f;      // ln 2 - kLn2Hi, rounded
-constexpr float kExpMin = -87.0f;
-constexpr float kExpC0 = 1.0f;
-constexpr float kExpC1 = 1.0f;
-constexpr float kExpC2 = 0x1.fffffcp-2f;
-constexpr float kExpC3 = 0x1.55540cp-3f;
-constexpr float kExpC4 = 0x1.55584p-5f;
-constexpr float kExpC5 = 0x1.126e3ap-7f;
-constexpr float kExpC6 = 0x1.6ae0eep-10f;
-// Upper bound of e^r over the reduced range |r| <= ln2/2 + 87 * 2^-24 * ln2.
-constexpr float kExpPolyMax = 1.4143f;
+constexpr float kExp2Floor = -200.0f;
+constexpr float kExp2C0 = 1.0f;
+constexpr float kExp2C1 = 0x1.62e428p-1f;
+constexpr float kExp2C2 = 0x1.ebf918p-3f;
+constexpr float kExp2C3 = 0x1.c6b6e4p-5f;
+constexpr float kExp2C4 = 0x1.3d0c54p-7f;
+constexpr float kExp2C5 = 0x1.5c08e4p-10f;
 constexpr int kFxBits = 46;
 constexpr double kFxOne = 70368744177664.0;  // 2^46
 
-// e = ls_exp(t); *k receives the binary exponent used for the scaling, or
-// kExpNoBucket when t < kExpMin (e == 0).
-constexpr int kExpNoBucket = -1000;
-__device__ __forceinline__ float ls_exp_k(float t, int* k) {
-  // Branch-free: the polynomial runs on a clamped argument and the result is
-  // selected afterwards, so unrolled loops keep independent exps interleaved.
-  const bool in = t >= kExpMin;  // false for NaN too
-  const float tt = in ? t : 0.0f;
-  const float kf = __builtin_rintf(tt * kLog2e);
-  float r = __builtin_fmaf(kf, -kLn2Hi, tt);
-  r = __builtin_fmaf(kf, -kLn2Lo, r);
-  float p = kExpC6;
-  p = __builtin_fmaf(p, r, kExpC5);
-  p = __builtin_fmaf(p, r, kExpC4);
-  p = __builtin_fmaf(p, r, kExpC3);
-  p = __builtin_fmaf(p, r, kExpC2);
-  p = __builtin_fmaf(p, r, kExpC1);
-  p = __builtin_fmaf(p, r, kExpC0);
+// e = exp2q(t); *k receives the rounded argument. Branch-free.
+__device__ __forceinline__ float exp2q_k(float t, int* k) {
+  const float tc = __builtin_fmaxf(t, kExp2Floor);
+  const float kf = __builtin_rintf(tc);
+  const float r = tc - kf;
+  float p = kExp2C5;
+  p = __builtin_fmaf(p, r, kExp2C4);
+  p = __builtin_fmaf(p, r, kExp2C3);
+  p = __builtin_fmaf(p, r, kExp2C2);
+  p = __builtin_fmaf(p, r, kExp2C1);
+  p = __builtin_fmaf(p, r, kExp2C0);
   const int ki = static_cast<int>(kf);
-  *k = in ? ki : kExpNoBucket;
-  return in ? __builtin_ldexpf(p, ki) : 0.0f;
+  *k = ki;
+  return __builtin_ldexpf(p, ki);
 }
 
-__device__ __forceinline__ float ls_exp(float t) {
+__device__ __forceinline__ float exp2q(float t) {
   int k;
-  return ls_exp_k(t, &k);
+  return exp2q_k(t, &k);
 }
 
 // floor(w * 2^46) for w in [0, 1], as a double holding an exact integer.

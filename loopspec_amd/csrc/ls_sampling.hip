@@ -1,37 +1,33 @@
 // (a) logit processing and (c) lossless speculative sampling for gfx950.
 //
-// The logits are read once, by many workgroups per row. The declared softmax
-// is chunked (kChunk elements per chunk; see oracle/sampling.py): everything a
-// chunk needs depends only on the chunk, and the row-wide values combine the
-// chunks' results exactly. Two or three launches per call, stream-ordered:
-//
-//   chunk_kernel  one 256-lane workgroup per (row, chunk): penalty bits of
-//                 the chunk's index range, x = pen(l) * RN(1/T), chunk max m_j,
-//                 e = ls_exp(x - m_j), exact chunk mass M_j = sum fx46(e), an
-//                 octave histogram of e, and the chunk's largest entries (all
-//                 e >= 2^(1-K_j), at most kChunkCand, K_j from the histogram)
-//                 compacted in index order into the workspace. No
-//                 cross-workgroup communication.
-//   row_kernel    one 1024-lane workgroup per row: m = max m_j,
-//                 f_j = ls_exp(m_j - m), S from the exact sum of f_j * M_j,
-//                 p = RN(RN(e f_j) / S) for the candidates, exact top-p cutoff
-//                 by a 3-round radix select on the binary32 bits of p with
-//                 fixed-point masses (replacing sort + cumsum + searchsorted,
-//                 distributions.py:59-70), valid for the whole row iff it
-//                 exceeds every p outside the candidates (else an exact select
-//                 over the re-streamed row). Then per mode:
-//                   spec   publish the row's stats and support {p >= c} with
-//                          device-coherent stores and arrive on the batch
-//                          element's counter; the last of its 2k+1 rows runs
-//                          the chain verify (accept tests, residual / bonus
-//                          draw);
-//                   sample draw one token from the filtered distribution;
-//                   dense  publish the row's stats for dense_kernel.
-//   dense_kernel  (dense mode) one workgroup per (row, chunk) writes p and/or
-//                 the filtered, renormalised distribution.
-//
-// All arithmetic is the declared arithmetic of ls_numerics.hpp, so every
-// output is bit-identical to the oracle's.
+// One persistent launch does the whole path (plus a penalty-bitmap pre-pass
+// when a repetition penalty is on, and a dense-output pass in filter mode).
+// Workgroups of 256 lanes stream (row, chunk) items of kChunk logits in
+// row-major order, with the next item's loads in flight while the current one
+// is processed. Per item:
+//   chunk max m_j of the penalised logits, mc_j = RN(m_j c) (c = log2 e / T),
+//   e = exp2q(fma(x, c, -mc_j)), the chunk mass M_j (binary32, fixed
+//   summation order), a histogram of the binary exponents of e, and the
+//   chunk's largest entries (every e >= 2^(1-K_j), at most cap of them, K_j
+//   the most leading exponent bins that fit) compacted in index order into
+//   the workspace; then
+//   each wave arrives on the row's counter.
+// The wave that arrives last makes its workgroup finalise the row: row max,
+// f_j = exp2q(mc_j - max), S = sum f_j M_j, g_j = RN(f_j / S), p = RN(e g_j)
+// for the candidates, and the exact top-p cutoff by a radix select on the
+// binary32 bits of p with 2^-46 fixed-point masses (replacing sort + cumsum +
+// searchsorted, distributions.py:59-70). The cutoff is valid for the whole
+// row iff it exceeds every p outside the candidates; otherwise the row is
+// re-streamed for an exact select. Then, per mode:
+//   spec    publish the row's statistics and the filtered probability of its
+//           draft token, arrive on the batch element's counter; the last of
+//           its 2k+1 rows runs the chain verify: accept tests, then the
+//           residual or bonus draw over the target row's candidates;
+//   sample  draw one token from the filtered distribution;
+//   dense   publish the statistics for dense_kernel, which writes p and/or the
+//           filtered, renormalised rows.
+// The arithmetic is the declared arithmetic of ls_numerics.hpp (restated by
+// oracle/sampling.py), so every output is bit-identical to the oracle's.
 #include "ls_common.hpp"
 #include "ls_numerics.hpp"
 #include "ls_runtime.hpp"
@@ -40,50 +36,55 @@ namespace ls {
 namespace {
 
 constexpr int kChunk = 8192;                 // softmax chunk (declared arithmetic)
-constexpr int kCB = 256;                     // chunk kernel lanes
+constexpr int kChunkShift = 13;
+constexpr int kCB = 256;                     // lanes per workgroup
 constexpr int kCW = kCB / kWave;
-constexpr int kChunkCand = 256;              // candidates kept per chunk (at most)
-constexpr int kOct = 64;                     // octave bins of e
-constexpr int kRB = 512;                     // row kernel lanes
-constexpr int kRW = kRB / kWave;
-constexpr int kRowCand = 4096;               // candidates of a row held in LDS
+constexpr int kPerLane = kChunk / kCB;       // 32 elements per lane and chunk
+constexpr int kChunkCand = 256;              // candidate slots per chunk in the workspace
+constexpr int kOctBins = 16;                 // exponent bins of e
+constexpr int kHistStride = kOctBins + 1;    // lane-private bins, padded against bank conflicts
+constexpr int kRowCand = 2048;               // candidate slots of a row
+constexpr int kSlotsPerLane = kRowCand / kCB;
 constexpr int kMaxChunks = 32;               // vocab <= 262144
 constexpr int kMaxVocab = kMaxChunks * kChunk;
-constexpr int kSupCap = 2048;                // support entries per row in the workspace
 constexpr int kBins = 2048;                  // radix digits per round
-constexpr int kBinsPerLane = kBins / kRB;
+constexpr int kBinsPerLane = kBins / kCB;
+constexpr int kGather = kWave;               // bucket size finished by one wave
 constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
-constexpr int kChunkWgsPerCu = 3;            // persistent chunk workgroups per CU
+constexpr int kChunkWgsPerCu = 3;
+constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
-constexpr int64_t kMaxGridYZ = 65535;
+constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
 enum RowFlag : uint32_t { kFlagUnfiltered = 1u, kFlagDense = 2u, kFlagSlow = 4u };
-enum ChunkFlag : uint32_t { kChunkComplete = 1u };
+enum ChunkFlag : uint32_t { kChunkComplete = 1u, kChunkHasTok = 2u };
 
-// Per-chunk result of chunk_kernel.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Per-chunk result, published by the chunk's workgroup.
 struct ChunkRec {
-  float m;          // chunk max of the processed logits
-  int32_t K;        // candidates are the e >= 2^(1-K) (all e > 0 when complete)
+  float mc;         // RN(chunk max * c)
+  int32_t K;        // candidates are the e >= 2^(1-K) (every e > 0 when complete)
   uint32_t n;       // candidates written
   uint32_t flags;
-  uint64_t mass;    // exact chunk mass sum fx46(e)
-  uint64_t pad;
+  float mass;       // chunk mass M_j
+  float e_tok;      // e of the row's draft token when it lies in this chunk
+  uint32_t pad0, pad1;
 };
 static_assert(sizeof(ChunkRec) == 32, "ChunkRec layout");
 
 // Published per-row statistics.
 struct RowStat {
-  float m;          // row max of the processed logits
-  float s;          // binary32 normaliser
+  float mcmax;      // row max of mc_j
+  float s;          // normaliser S
   float cutoff;     // top-p cutoff value (0 when unfiltered)
-  float mass;       // binary32 retained mass (renormaliser)
-  uint32_t n_sup;   // support entries published
+  float mass;       // binary32 retained mass (renormaliser; 1 when unfiltered)
   uint32_t flags;
-  uint64_t s_fx;    // exact normaliser
+  float p_tok;      // filtered probability of the row's draft token
   uint64_t mass_fx; // exact retained mass
 };
-static_assert(sizeof(RowStat) == 40, "RowStat layout");
+static_assert(sizeof(RowStat) == 32, "RowStat layout");
 
 struct SampParams {
   const char* base0;           // target / row logits
@@ -94,14 +95,14 @@ struct SampParams {
   int k;                       // spec: draft positions; 0 otherwise
   int vocab;
   int nch;                     // chunks per row
-  int chunk_cap;               // candidates kept per chunk: min(kChunkCand, kRowCand / nch)
-  int bm_words;                // penalty bitmap words per group (0 without penalty)
-  float inv_t;
-  int use_t;
+  int cap, cap_log2;           // candidates kept per chunk (a power of two)
+  int bm_words;                // penalty bitmap words per group
+  int items;                   // rows * nch
+  float c;                     // exponent scale RN(log2e * RN(1/T))
   float pen, inv_pen;
   int use_pen;
   float top_p;                 // >= 1: unfiltered
-  const float* top_p_rows;     // optional per-row top_p (dense/sample modes)
+  const float* top_p_rows;     // optional per-row top_p (dense mode)
   const int32_t* hist;
   int64_t hist_stride;
   const int32_t* hist_len;
@@ -124,9 +125,10 @@ struct SampParams {
   ChunkRec* chunks;             // [rows, nch]
   uint64_t* cands;              // [rows, nch, kChunkCand] of (idx << 32 | bits(e))
   RowStat* stats;               // [rows]
-  uint64_t* support;            // [rows, kSupCap] of (idx << 32 | bits(p)) (spec)
-  uint32_t* counters;           // [kMaxSpecBatch * kCounterStride] (spec)
-  uint32_t* bitmap;             // [groups, bm_words] penalty bits (written by chunk_kernel)
+  uint32_t* row_cnt;            // [kMaxRows * kCounterStride]
+  uint32_t* grp_cnt;            // [kMaxSpecBatch * kCounterStride]
+  uint32_t* bitmap;             // [groups, bm_words] penalty bits
+  int64_t* draws;               // spec: [B, k+1] residual draws, then the bonus draw
 };
 
 // Row jr of group g: spec rows are target positions 0..k, then draft 0..k-1.
@@ -135,30 +137,181 @@ __device__ __forceinline__ const char* row_of(const SampParams& p, int64_t g, in
   return p.base1 + g * p.bstride1 + (jr - p.k - 1) * p.pstride1;
 }
 
-// Per-element logit transform (penalty, temperature); passed by value so no
-// helper needs the address of the kernel-argument block.
-struct Xf {
-  float inv_t, pen, inv_pen;
-  int use_t, use_pen;
-};
-
-__device__ __forceinline__ Xf make_xf(const SampParams& p) {
-  return Xf{p.inv_t, p.pen, p.inv_pen, p.use_t, p.use_pen};
-}
-
-__device__ __forceinline__ float xform_seen(const Xf& f, float l, bool seen) {
-  if (f.use_pen && seen) l = l < 0.0f ? l * f.pen : l * f.inv_pen;
-  if (f.use_t) l = l * f.inv_t;
-  return l;
+// The draft token whose probability row jr of group g contributes to the
+// accept test (target position i and draft position i both test x_i); -1 for
+// the bonus row and outside spec mode.
+__device__ __forceinline__ int64_t row_token(const SampParams& p, int64_t g, int jr) {
+  if (p.k == 0 || jr == p.k) return -1;
+  const int i = jr < p.k ? jr : jr - p.k - 1;
+  return p.draft_tokens[g * p.k + i];
 }
 
 __device__ __forceinline__ bool bit_of(const uint32_t* bm, int idx) { return (bm[idx >> 5] >> (idx & 31)) & 1u; }
 
-// p of one element from its chunk max m_j, the row max m and the normaliser s.
-__device__ __forceinline__ float chunk_p(float x, float mj, float m, float s) {
-  const float e = ls_exp(x - mj);
-  const float f = ls_exp(mj - m);
-  return (e * f) / s;
+// ---------------------------------------------------------------------------
+// Wave sums in the declared pairwise order (lanes 2i and 2i+1 first, then
+// pairs of those ...): quad_perm swaps for distance 1 and 2, then the half-row
+// and row mirrors (equivalent to distance 4 and 8 once every quad / half-row
+// holds one value), then the row broadcasts.
+// ---------------------------------------------------------------------------
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+  return __uint_as_float(dpp32<CTRL, ROWS>(0u, __float_as_uint(v))) + v;
+}
+
+// Pairwise sum over the 16 lanes of each row (every lane of the row gets it).
+__device__ __forceinline__ float row_tree_sum(float v) {
+  v = dpp_add<kDppQuadXor1, 0xf>(v);
+  v = dpp_add<kDppQuadXor2, 0xf>(v);
+  v = dpp_add<kDppRowHalfMirror, 0xf>(v);
+  v = dpp_add<kDppRowMirror, 0xf>(v);
+  return v;
+}
+
+// Pairwise sum over the 64 lanes (wave-uniform result).
+__device__ __forceinline__ float wave_tree_sum(float v) {
+  v = row_tree_sum(v);
+  v = dpp_add<kDppRowBcast15, 0xa>(v);  // rows 1, 3: r0 + r1, r2 + r3
+  v = dpp_add<kDppRowBcast31, 0xc>(v);  // row 3: (r0 + r1) + (r2 + r3)
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), kWave - 1));
+}
+
+// Pairwise sum over lanes 0..31 (wave-uniform result).
+__device__ __forceinline__ float half_tree_sum(float v) {
+  v = row_tree_sum(v);
+  v = dpp_add<kDppRowBcast15, 0xa>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 31));
+}
+
+// Pairwise sum of N values held by one lane, adjacent pairs first.
+template <int N>
+__device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
+#pragma unroll
+  for (int w = 1; w < N; w *= 2) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2 * w) a[i] = a[i] + a[i + w];
+  }
+  return a[0];
+}
+
+// ---------------------------------------------------------------------------
+// Shared memory: the chunk phase and the row / tail phases share one region.
+// ---------------------------------------------------------------------------
+struct ChunkSh {
+  float est[kChunk];                   // e of the chunk, 16-byte slots XOR-swizzled
+  uint32_t hist[kCB * kHistStride];    // lane-private exponent bins
+  float wmax[kCW];
+  float wmass[kCW];
+  uint32_t binw[kCW][kOctBins];
+  uint32_t wcnt[kCW];
+};
+
+struct FinSh {
+  uint64_t slot[kRowCand];             // the row's candidate slots (idx << 32 | bits)
+  union {
+    uint64_t H[kBins];                 // radix bins
+    uint64_t slot_d[kRowCand];         // tail: the draft row's candidate slots
+    float w[kRowCand];                 // tail: draw weights per slot
+    uint64_t words64[kBins];           // tail: row statistics (4 words each)
+  };
+  float g[2][kMaxChunks];
+  float mcj[2][kMaxChunks];
+  uint32_t n[2][kMaxChunks];
+  uint32_t gbits[kGather];
+  uint64_t gw[kGather];
+  uint32_t gcount;
+  uint64_t statw[8];                   // residual: both rows' statistics
+  float tokp[2 * 64 + 1];              // accept chain: P / Q of the draft tokens
+  int64_t tokd[64 + 1];                // accept chain: the published draws
+};
+
+struct Shared {
+  FinSh f;
+  uint64_t red[kCW];
+  uint64_t u64s[8];
+  uint32_t u32s[8];
+  float f32s[8];
+};
+
+// Physical float index of element v of the chunk in the e-store.
+__device__ __forceinline__ int est_index(int v) {
+  const int s = v >> 2;
+  return ((s ^ ((s >> 3) & 7)) << 2) | (v & 3);
+}
+
+// Exclusive scan in lane order over the workgroup; *total receives the sum.
+__device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t* smem, uint64_t* total) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const uint64_t inc = wave_scan_add_u64(v);
+  __syncthreads();
+  if (lane == kWave - 1) smem[wid] = inc;
+  __syncthreads();
+  uint64_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kCW; ++i) {
+    const uint64_t s = smem[i];
+    base += i < wid ? s : 0;
+    tot += s;
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+__device__ __forceinline__ uint64_t block_sum(uint64_t v, uint64_t* smem) {
+  uint64_t tot;
+  (void)block_excl_scan(v, smem, &tot);
+  return tot;
+}
+
+__device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) {
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+__device__ __forceinline__ uint64_t pack2f(float lo, float hi) { return pack2(__float_as_uint(lo), __float_as_uint(hi)); }
+__device__ __forceinline__ float lo_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+__device__ __forceinline__ float hi_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
+
+__device__ __forceinline__ void put_rec(ChunkRec* dst, const ChunkRec& v) {
+  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+  store_sc64(d + 0, pack2(__float_as_uint(v.mc), static_cast<uint32_t>(v.K)));
+  store_sc64(d + 1, pack2(v.n, v.flags));
+  store_sc64(d + 2, pack2f(v.mass, v.e_tok));
+}
+__device__ __forceinline__ ChunkRec get_rec(const ChunkRec* src) {
+  const uint64_t* s = reinterpret_cast<const uint64_t*>(src);
+  const uint64_t a = load_sc64(s + 0), b = load_sc64(s + 1), c = load_sc64(s + 2);
+  ChunkRec v;
+  v.mc = lo_f(a);
+  v.K = static_cast<int32_t>(a >> 32);
+  v.n = static_cast<uint32_t>(b);
+  v.flags = static_cast<uint32_t>(b >> 32);
+  v.mass = lo_f(c);
+  v.e_tok = hi_f(c);
+  v.pad0 = v.pad1 = 0;
+  return v;
+}
+__device__ __forceinline__ void put_stat(RowStat* dst, const RowStat& v) {
+  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+  store_sc64(d + 0, pack2f(v.mcmax, v.s));
+  store_sc64(d + 1, pack2f(v.cutoff, v.mass));
+  store_sc64(d + 2, pack2(v.flags, __float_as_uint(v.p_tok)));
+  store_sc64(d + 3, v.mass_fx);
+}
+// The four 64-bit words of a published RowStat and the struct they encode.
+__device__ __forceinline__ RowStat stat_of(uint64_t a, uint64_t b, uint64_t c, uint64_t d) {
+  RowStat v;
+  v.mcmax = lo_f(a);
+  v.s = hi_f(a);
+  v.cutoff = lo_f(b);
+  v.mass = hi_f(b);
+  v.flags = static_cast<uint32_t>(c);
+  v.p_tok = hi_f(c);
+  v.mass_fx = d;
+  return v;
 }
 
 // ===========================================================================
@@ -186,24 +339,12 @@ __global__ __launch_bounds__(kBmB) void bitmap_kernel(const SampParams p) {
 }
 
 // ===========================================================================
-// chunk_kernel
+// Chunk phase
 // ===========================================================================
-struct ChunkShared {
-  uint32_t oct[kCW][kOct];             // per-wave octave counts
-  float wmax[kCW];
-  uint64_t wmass[kCW];
-  int wcnt[8][kCW];                    // candidates per (vector slot, wave)
-};
 
-// Inclusive wave scan of a 32-bit value (DPP).
-__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x, int lane) {
-  (void)lane;
-  return wave_scan_add_u32(x);
-}
-
-// Loads of one chunk (clamped: lanes past the chunk end re-read its last
-// vector), plus, with a penalty, the bitmap word of each vector (the EPV bits
-// of a 16-byte vector always sit in one 32-bit word).
+// Loads of one chunk (lanes past the chunk end re-read its last vector), plus,
+// with a penalty, the bitmap word of each vector (the bits of a 16-byte vector
+// always sit in one 32-bit word).
 template <int DT, int NVC>
 __device__ __forceinline__ void load_chunk(const SampParams& p, int item, u32x4 (&d)[NVC], uint32_t (&pw)[NVC]) {
   constexpr int EPV = Elem<DT>::kPerVec;
@@ -227,140 +368,152 @@ __device__ __forceinline__ void load_chunk(const SampParams& p, int item, u32x4 
   }
 }
 
-// One chunk. Three barriers: after the chunk max, after the mass / histogram
-// (every wave then derives K on its own), after the per-(slot, wave)
-// candidate counts (every wave then derives its output offsets on its own).
-// The LDS of the previous chunk is safe to reuse without a barrier: every
-// read of it precedes a barrier that each wave passes before the writes here.
+__device__ __forceinline__ int64_t item_token(const SampParams& p, int item) {
+  if (p.k == 0) return -1;
+  const int r = item / p.nch;
+  const int g = r / p.rpg;
+  return row_token(p, g, r - g * p.rpg);
+}
+
+// One chunk; returns true in every lane when this workgroup is the last to
+// finish a chunk of the row (and so finalises the row).
 template <int DT, int NVC>
-__device__ __forceinline__ void process_chunk(const SampParams& p, ChunkShared& sh, int item, const u32x4 (&d)[NVC],
-                                              const uint32_t (&pw)[NVC]) {
+__device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, int item, const u32x4 (&d)[NVC],
+                                              const uint32_t (&pw)[NVC], int64_t tok) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int NE = NVC * EPV;  // 32 elements per lane
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  constexpr int NE = NVC * EPV;
+  static_assert(NE == kPerLane, "32 elements per lane");
+  // lane-derived values are recomputed per item (not hoisted out of the
+  // persistent loop, where they would stay live through the row phase)
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  const int lane = t & (kWave - 1), wid = t / kWave;
   const int r = item / p.nch;
   const int cj = item - r * p.nch;
-  const int g = r / p.rpg;
-  const int jr = r - g * p.rpg;
   const int c0 = cj * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
-  const Xf xf = make_xf(p);
-  sh.oct[wid][lane] = 0u;
-  // 3. processed logits x (kept as binary32 bit patterns) and the chunk max
-  uint32_t xe[NE];
-  float mx = -__builtin_inff();
-  const bool full = nvc == kCB * NVC;  // only a row's last chunk can be partial
-  if (xf.use_pen | xf.use_t) {
+
+  // 1. penalised logits (-inf past the row end) and the chunk max
+  float x[NE];
 #pragma unroll
-    for (int u = 0; u < NVC; ++u) {
+  for (int u = 0; u < NVC; ++u) {
+    const bool in = u * kCB + t < nvc;
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        const bool seen = xf.use_pen && ((pw[u] >> ((((u * kCB + t) * EPV) & 31) + e)) & 1u);
-        xe[u * EPV + e] = __float_as_uint(xform_seen(xf, vec_elem<DT>(d[u], e), seen));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < NVC; ++u) {
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) xe[u * EPV + e] = __float_as_uint(vec_elem<DT>(d[u], e));
+    for (int e = 0; e < EPV; ++e) {
+      float l = vec_elem<DT>(d[u], e);
+      if (p.use_pen && ((pw[u] >> ((((u * kCB + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+      x[u * EPV + e] = in ? l : -__builtin_inff();
     }
   }
-  if (!full) {
+  float mx = x[0];
 #pragma unroll
-    for (int u = 0; u < NVC; ++u) {
-      if (u * kCB + t >= nvc) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) xe[u * EPV + e] = 0xff800000u;  // -inf
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < NE; i += 2) mx = nmax(mx, nmax(__uint_as_float(xe[i]), __uint_as_float(xe[i + 1])));
+  for (int i = 1; i < NE; ++i) mx = nmax(mx, x[i]);
   mx = wave_max_f32(mx);
-  if (lane == 0) sh.wmax[wid] = mx;
+  if (lane == 0) cs.wmax[wid] = mx;
   __syncthreads();
-  const float m = nmax(nmax(sh.wmax[0], sh.wmax[1]), nmax(sh.wmax[2], sh.wmax[3]));
-  // 4. e in place, exact chunk mass (integer fx46), octave histogram. Every
-  // element is counted (e == 0 in the last bin), which only matters for
-  // K == 64 and keeps the loop branch-free.
-  uint64_t acc = 0;
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const uint32_t b = __float_as_uint(ls_exp(__uint_as_float(xe[i]) - m));  // -inf / NaN give 0
-    xe[i] = b;
-    const uint32_t E = b >> 23;
-    const uint32_t sh_r = 127u - E;
-    const uint64_t mant = static_cast<uint64_t>((b & 0x7fffffu) | 0x800000u) << 23;
-    acc += sh_r > 47u ? 0ull : (mant >> sh_r);  // floor(e * 2^46), exact
-    const uint32_t o = sh_r < static_cast<uint32_t>(kOct - 1) ? sh_r : static_cast<uint32_t>(kOct - 1);
-    __hip_atomic_fetch_add(&sh.oct[wid][o], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  const uint64_t wm = wave_sum_u64(acc);
-  if (lane == 0) sh.wmass[wid] = wm;
-  __syncthreads();
-  // 5. K (every wave): the largest number of leading octaves holding at most
-  // chunk_cap entries.
-  int K;
-  {
-    uint32_t c = 0;
-#pragma unroll
-    for (int w = 0; w < kCW; ++w) c += sh.oct[w][lane];
-    const uint32_t inc = wave_scan_u32(c, lane);
-    K = __builtin_popcountll(__ballot(inc <= static_cast<uint32_t>(p.chunk_cap)));
-  }
-  // e qualifies iff e >= 2^(1-K) (K == 64: every e > 0; K == 0: none)
-  const uint32_t thr_bits = K >= kOct ? 1u : (K == 0 ? 0x7f800000u : static_cast<uint32_t>(128 - K) << 23);
-  // 6. candidate counts per (vector slot, wave); index order is (slot, lane, e)
-  uint32_t cs[NVC];
+  const float m = nmax(nmax(cs.wmax[0], cs.wmax[1]), nmax(cs.wmax[2], cs.wmax[3]));
+  const float mc = m * p.c;
+  const float nmc = -mc;
+
+  // 2. e in place, lane-private exponent bins, e-store
+  const int hbase = t * kHistStride;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    uint32_t c = 0;
+    const bool in = u * kCB + t < nvc;
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) c += xe[u * EPV + e] >= thr_bits ? 1u : 0u;
-    cs[u] = c;
-    int tot = 0;
-    if (__ballot(c != 0)) tot = static_cast<int>(lane_bcast_u32(wave_scan_u32(c, lane), kWave - 1));
-    if (lane == 0) sh.wcnt[u][wid] = tot;
-  }
-  __syncthreads();
-  // 7. this wave's base offset per slot: exclusive prefix over (slot, wave)
-  // in slot-major order, computed by every wave from the shared counts.
-  int flat = 0;
-  if (lane < NVC * kCW) flat = sh.wcnt[lane / kCW][lane % kCW];
-  const int incl = static_cast<int>(wave_scan_u32(static_cast<uint32_t>(flat), lane));
-  const int total = static_cast<int>(lane_bcast_u32(static_cast<uint32_t>(incl), NVC * kCW - 1));
-  uint64_t* out = p.cands + (static_cast<int64_t>(r) * p.nch + cj) * kChunkCand;
-  const int cap = p.chunk_cap;
-#pragma unroll
-  for (int u = 0; u < NVC; ++u) {
-    const uint32_t c = cs[u];
-    if (__ballot(c != 0)) {
-      const int slot = u * kCW + wid;
-      const int base = static_cast<int>(lane_bcast_u32(static_cast<uint32_t>(incl), slot) -
-                                        lane_bcast_u32(static_cast<uint32_t>(flat), slot));
-      int pos = base + static_cast<int>(wave_scan_u32(c, lane) - c);
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        if (xe[u * EPV + e] >= thr_bits) {
-          if (pos < cap) {
-            const uint32_t idx = static_cast<uint32_t>(c0 + (u * kCB + t) * EPV + e);
-            out[pos] = (static_cast<uint64_t>(idx) << 32) | xe[u * EPV + e];
-          }
-          ++pos;
-        }
-      }
+    for (int e = 0; e < EPV; ++e) {
+      const float ev = exp2q(__builtin_fmaf(x[u * EPV + e], p.c, nmc));
+      x[u * EPV + e] = ev;
+      // bin b holds e in [2^-b, 2^(1-b)) (bin 0: e >= 1; the last bin: everything smaller)
+      const int be = static_cast<int>(__float_as_uint(ev) >> 23);
+      const int b = 127 - (be < 127 - (kOctBins - 1) ? 127 - (kOctBins - 1) : (be > 127 ? 127 : be));
+      if (in) __hip_atomic_fetch_add(&cs.hist[hbase + b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+#pragma unroll
+    for (int h = 0; h < EPV / 4; ++h) {
+      const int s = (u * kCB + t) * (EPV / 4) + h;
+      const int ps = s ^ ((s >> 3) & 7);
+      f32x4 v;
+      v.x = x[u * EPV + 4 * h + 0];
+      v.y = x[u * EPV + 4 * h + 1];
+      v.z = x[u * EPV + 4 * h + 2];
+      v.w = x[u * EPV + 4 * h + 3];
+      *reinterpret_cast<f32x4*>(&cs.est[ps * 4]) = v;
+    }
+  }
+  // chunk mass: each lane's 32 e pairwise, then the lanes pairwise
+  const float wm = wave_tree_sum(lane_tree_sum(x));
+  if (lane == 0) cs.wmass[wid] = wm;
+  __syncthreads();
+
+  // 3. bin totals: thread (b, q) sums bin b of lanes 16q..16q+15 and clears it
+  {
+    const int b = t & (kOctBins - 1), q = t >> 4;
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      s += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    if (lane < kOctBins) cs.binw[wid][lane] = s;
+  }
+  // lane-contiguous e: elements [32t, 32t + 32) (index order within the lane)
+  float ec[kPerLane];
+#pragma unroll
+  for (int q = 0; q < kPerLane / 4; ++q) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(&cs.est[(8 * t + (q ^ (t & 7))) * 4]);
+    ec[4 * q + 0] = v.x;
+    ec[4 * q + 1] = v.y;
+    ec[4 * q + 2] = v.z;
+    ec[4 * q + 3] = v.w;
+  }
+  float e_tok = 0.0f;
+  const bool has_tok = tok >= c0 && tok < c0 + nel;
+  if (t == 0 && has_tok) e_tok = cs.est[est_index(static_cast<int>(tok - c0))];
+  __syncthreads();
+
+  // 4. K: the number of leading exponent bins holding at most cap entries
+  uint32_t bc = 0;
+  if (lane < kOctBins) bc = cs.binw[0][lane] + cs.binw[1][lane] + cs.binw[2][lane] + cs.binw[3][lane];
+  const uint32_t binc = wave_scan_add_u32(bc);
+  const int K = __builtin_popcountll(__ballot(lane < kOctBins && binc <= static_cast<uint32_t>(p.cap)));
+  const float th = K >= kOctBins ? __uint_as_float(1u) : (K == 0 ? __builtin_inff() : __builtin_ldexpf(1.0f, 1 - K));
+  // 5. candidate mask (bit 31 - i <-> element 32t + i), counts, offsets
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) mask = (mask << 1) | (ec[i] >= th ? 1u : 0u);
+  const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(mask));
+  const uint32_t incl = wave_scan_add_u32(cnt);
+  if (lane == kWave - 1) cs.wcnt[wid] = incl;
+  __syncthreads();
+  uint32_t pos = incl - cnt, total = 0;
+#pragma unroll
+  for (int w = 0; w < kCW; ++w) {
+    const uint32_t c = cs.wcnt[w];
+    pos += w < wid ? c : 0u;
+    total += c;
+  }
+  // 6. candidates, in index order
+  uint64_t* out = p.cands + (static_cast<int64_t>(r) * p.nch + cj) * kChunkCand;
+  const uint32_t ibase = static_cast<uint32_t>(c0 + kPerLane * t);
+  while (mask) {
+    const int i = __builtin_clz(mask);
+    const uint32_t eb = __float_as_uint(cs.est[(8 * t + ((i >> 2) ^ (t & 7))) * 4 + (i & 3)]);
+    out[pos] = (static_cast<uint64_t>(ibase + static_cast<uint32_t>(i)) << 32) | eb;
+    ++pos;
+    mask &= 0x7fffffffu >> i;
   }
   if (t == 0) {
     ChunkRec rec;
-    rec.m = m;
+    rec.mc = mc;
     rec.K = K;
-    rec.n = static_cast<uint32_t>(total < cap ? total : cap);
-    rec.flags = K >= kOct ? kChunkComplete : 0u;
-    rec.mass = sh.wmass[0] + sh.wmass[1] + sh.wmass[2] + sh.wmass[3];
-    rec.pad = 0;
+    rec.n = total;
+    rec.flags = (K >= kOctBins ? kChunkComplete : 0u) | (has_tok ? kChunkHasTok : 0u);
+    rec.mass = (cs.wmass[0] + cs.wmass[1]) + (cs.wmass[2] + cs.wmass[3]);
+    rec.e_tok = e_tok;
+    rec.pad0 = rec.pad1 = 0;
     p.chunks[static_cast<int64_t>(r) * p.nch + cj] = rec;
   }
 }
@@ -368,109 +521,128 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkShared& 
 // Persistent over (row, chunk) items in row-major order, double-buffered: the
 // next item's loads are in flight while the current one is processed.
 template <int DT>
-__global__ __launch_bounds__(kCB, 3) void chunk_kernel(const SampParams p, int items) {
+__global__ __launch_bounds__(kCB, kChunkWgsPerCu) void chunk_kernel(const SampParams p) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kCB * EPV);  // vectors per lane: 8 (f32) or 4
-  __shared__ ChunkShared sh;
+  __shared__ ChunkSh cs;
+  const int t = threadIdx.x;
+  for (int i = t; i < kCB * kHistStride; i += kCB) cs.hist[i] = 0u;
+  __syncthreads();
   int item = blockIdx.x;
-  if (item >= items) return;
+  if (item >= p.items) return;
   u32x4 cur[NVC], nxt[NVC];
   uint32_t pcur[NVC] = {}, pnxt[NVC] = {};
   load_chunk<DT, NVC>(p, item, cur, pcur);
+  int64_t tcur = item_token(p, item), tnxt = -1;
   while (true) {
     const int next = item + static_cast<int>(gridDim.x);
-    if (next < items) load_chunk<DT, NVC>(p, next, nxt, pnxt);
-    process_chunk<DT, NVC>(p, sh, item, cur, pcur);
-    if (next >= items) break;
+    if (next < p.items) {
+      load_chunk<DT, NVC>(p, next, nxt, pnxt);
+      tnxt = item_token(p, next);
+    }
+    process_chunk<DT, NVC>(p, cs, item, cur, pcur, tcur);
+    if (next >= p.items) break;
+    // register moves (the empty asm keeps the copy from becoming a memcpy of
+    // the arrays, which would put them in scratch)
 #pragma unroll
     for (int u = 0; u < NVC; ++u) {
-      cur[u] = nxt[u];
+      u32x4 v = nxt[u];
+      asm volatile("" : "+v"(v));
+      cur[u] = v;
       pcur[u] = pnxt[u];
     }
+    tcur = tnxt;
     item = next;
   }
 }
 
 // ===========================================================================
-// row_kernel
+// Row phase
 // ===========================================================================
-struct RowShared {
-  uint32_t cidx[kRowCand];       // candidate / support indices
-  float cval[kRowCand];          // candidate / support p
-  uint64_t H[kBins];             // radix histogram
-  float pa[128];                 // tail: P and Q of the draft tokens
-  uint32_t gbits[kWave];         // select: entries of the cutoff's bucket
-  uint64_t gw[kWave];
-  int gcount;
-  float cm[kMaxChunks], cf[kMaxChunks];
-  int cK[kMaxChunks], coff[kMaxChunks + 1];
-  uint32_t cn[kMaxChunks], cfl[kMaxChunks];
-  uint64_t cM[kMaxChunks];
-  uint64_t red[kRW + 2];
-  float redf[kRW + 2];
-  uint32_t u32s[8];
-  uint64_t u64s[8];
-  RowStat st[2 * 64 + 1];        // tail: stats of the element's rows
-  int tail_flag;
+
+// Wave 0: from the chunk records of a row (lane j holds record j) compute the
+// row max, S and g_j (kept in fs.g / fs.mcj / fs.n [slot]), the bound on every
+// p outside the candidates, and p of the draft token.
+struct RowScale {
+  float mcmax, s, p_bound, p_tok;
+  bool has_tok;
 };
 
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t x, int lane) {
-  (void)lane;
-  return wave_scan_add_u64(x);
-}
-
-// Exclusive scan in lane order over the 1024 lanes; *total receives the sum.
-__device__ __forceinline__ uint64_t row_excl_scan(uint64_t v, uint64_t* smem, uint64_t* total) {
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  const uint64_t inc = wave_incl_scan_u64(v, lane);
-  __syncthreads();
-  if (lane == kWave - 1) smem[wid] = inc;
-  __syncthreads();
-  uint64_t base = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < kRW; ++i) {
-    const uint64_t s = smem[i];
-    base += i < wid ? s : 0;
-    tot += s;
+__device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRec& rec, int nch) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool in = lane < nch;
+  RowScale rs;
+  rs.mcmax = wave_max_f32(in ? rec.mc : -__builtin_inff());
+  const float f = in ? exp2q(rec.mc - rs.mcmax) : 0.0f;
+  rs.s = half_tree_sum(in ? f * rec.mass : 0.0f);
+  const float gj = f / rs.s;
+  if (in) {
+    fs.g[slot][lane] = gj;
+    fs.mcj[slot][lane] = rec.mc;
+    fs.n[slot][lane] = rec.n;
   }
-  *total = tot;
-  return base + inc - v;
+  float pb = 0.0f;
+  if (in && !(rec.flags & kChunkComplete)) pb = rec.K > 0 ? __builtin_ldexpf(1.0f, 1 - rec.K) * gj : __builtin_inff();
+  rs.p_bound = wave_max_f32(pb);
+  const bool tk = in && (rec.flags & kChunkHasTok);
+  rs.has_tok = __ballot(tk) != 0;
+  rs.p_tok = wave_max_f32(tk ? rec.e_tok * gj : -1.0f);
+  return rs;
 }
 
-// Exact top-p select: 3 radix rounds (11, 11, 10 bits) over binary32 p bits
-// with fixed-point masses. visit(f) calls f(bits, w) for every element of the
-// set. Returns false if the set's total mass is below thr.
+// Same from published row statistics (mcmax, S): g_j of the chunks only.
+__device__ __forceinline__ void row_g(FinSh& fs, int slot, const ChunkRec& rec, int nch, float mcmax, float s) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (lane < nch) {
+    fs.g[slot][lane] = exp2q(rec.mc - mcmax) / s;
+    fs.mcj[slot][lane] = rec.mc;
+    fs.n[slot][lane] = rec.n;
+  }
+}
+
+__device__ __forceinline__ uint32_t digit_of(uint32_t bits, int shift, uint32_t dmask) {
+  const uint32_t d = (bits >> shift) & dmask;
+  return d < kBins ? d : kBins - 1;
+}
+
+// Exact top-p cutoff over a set whose elements visit(f) passes to f(bits, w)
+// (bits of p > 0, w = fx46(p)): c = max{v : sum_{p >= v} w >= thr}, and the
+// mass kept. Up to three radix rounds on the bits of p (12, 11 and 8 bits
+// from the top; fs.H must be zero on entry); after each round a bucket of at
+// most kGather entries is finished by one wave. Returns false if the set's
+// total mass is below thr.
 template <typename Visit>
-__device__ bool radix_select(RowShared& sh, uint64_t thr, Visit visit, float* cutoff, uint64_t* mass) {
-  uint64_t* H = sh.H;
+__device__ bool radix_select(Shared& sh, uint64_t thr, Visit visit, float* cutoff, uint64_t* mass) {
+  FinSh& fs = sh.f;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
   uint32_t prefix = 0, pmask = 0;
   uint64_t above = 0;
-  const int t = threadIdx.x;
   for (int round = 0; round < 3; ++round) {
-    const int shift = round == 0 ? 21 : (round == 1 ? 10 : 0);
-    const int nbits = round == 2 ? 10 : 11;
-    const uint32_t dmask = (1u << nbits) - 1u;
+    const int shift = round == 0 ? 19 : (round == 1 ? 8 : 0);
+    const uint32_t dmask = round == 0 ? 0xfffu : (round == 1 ? 0x7ffu : 0xffu);
+    if (round > 0) {
 #pragma unroll
-    for (int q = 0; q < kBinsPerLane; ++q) H[kBinsPerLane * t + q] = 0;
-    if (t == 0) sh.u32s[1] = 0xffffffffu;
-    __syncthreads();
+      for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
+      __syncthreads();
+    }
     visit([&](uint32_t bits, uint64_t w) {
-      if ((bits & pmask) == prefix && w) {
-        __hip_atomic_fetch_add(&H[(bits >> shift) & dmask], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
+      if ((bits & pmask) == prefix && w)
+        __hip_atomic_fetch_add(&fs.H[digit_of(bits, shift, dmask)], w, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
     });
     __syncthreads();
-    // Lane t owns digits kBins-1 - (kBinsPerLane*t + q), q = 0.. (descending).
+    // lane t owns digits kBins-1 - (kBinsPerLane*t + q), q = 0.. (descending)
     uint64_t v[kBinsPerLane];
     uint64_t sum = 0;
 #pragma unroll
     for (int q = 0; q < kBinsPerLane; ++q) {
-      const int dg = kBins - 1 - (kBinsPerLane * t + q);
-      v[q] = dg <= static_cast<int>(dmask) ? H[dg] : 0;
+      v[q] = fs.H[kBins - 1 - (kBinsPerLane * t + q)];
       sum += v[q];
     }
     uint64_t total;
-    const uint64_t ex = row_excl_scan(sum, sh.red, &total);
+    const uint64_t ex = block_excl_scan(sum, sh.red, &total);
+    if (t == 0) sh.u32s[1] = kNone;
+    __syncthreads();
     uint64_t before = above + ex;
     if (before < thr && before + sum >= thr) {
 #pragma unroll
@@ -483,157 +655,114 @@ __device__ bool radix_select(RowShared& sh, uint64_t thr, Visit visit, float* cu
         before += v[q];
       }
     }
+    if (t == 0) fs.gcount = 0;
     __syncthreads();
     const uint32_t digit = sh.u32s[1];
-    if (digit == 0xffffffffu) return false;
+    if (digit == kNone) return false;
     prefix |= digit << shift;
     pmask |= dmask << shift;
     above = sh.u64s[1];
-    if (round == 2) {
-      *cutoff = __uint_as_float(prefix);
-      *mass = above + sh.u64s[2];
-    }
-    __syncthreads();
-  }
-  return true;
-}
-
-// Exact cutoff over the n LDS candidates (sh.cval): one 11-bit radix round
-// on the top bits of p picks the bucket holding the cutoff; a bucket of at
-// most 64 entries is finished by one wave (each lane ranks its entry against
-// the others), a larger one by the full 3-round select.
-__device__ bool select_candidates(RowShared& sh, int n, uint64_t thr, float* cutoff, uint64_t* mass) {
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  uint64_t* H = sh.H;
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) H[kBinsPerLane * t + q] = 0;
-  if (t == 0) {
-    sh.u32s[1] = 0xffffffffu;
-    sh.gcount = 0;
-  }
-  __syncthreads();
-  for (int i = t; i < n; i += kRB) {
-    const float pv = sh.cval[i];
-    const uint64_t w = fx46(pv);
-    if (w) __hip_atomic_fetch_add(&H[__float_as_uint(pv) >> 21], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  __syncthreads();
-  {
-    uint64_t v[kBinsPerLane];
-    uint64_t sum = 0;
-#pragma unroll
-    for (int q = 0; q < kBinsPerLane; ++q) {
-      v[q] = H[kBins - 1 - (kBinsPerLane * t + q)];
-      sum += v[q];
-    }
-    uint64_t total;
-    uint64_t before = row_excl_scan(sum, sh.red, &total);
-    if (before < thr && before + sum >= thr) {
-#pragma unroll
-      for (int q = 0; q < kBinsPerLane; ++q) {
-        if (before < thr && before + v[q] >= thr) {
-          sh.u32s[1] = static_cast<uint32_t>(kBins - 1 - (kBinsPerLane * t + q));
-          sh.u64s[1] = before;
+    const uint64_t binmass = sh.u64s[2];
+    visit([&](uint32_t bits, uint64_t w) {
+      if ((bits & pmask) == prefix && w) {
+        const uint32_t k = __hip_atomic_fetch_add(&fs.gcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (k < kGather) {
+          fs.gbits[k] = bits;
+          fs.gw[k] = w;
         }
-        before += v[q];
       }
-    }
-  }
-  __syncthreads();
-  const uint32_t d1 = sh.u32s[1];
-  if (d1 == 0xffffffffu) return false;
-  const uint64_t above = sh.u64s[1];
-  for (int i = t; i < n; i += kRB) {
-    const float pv = sh.cval[i];
-    const uint32_t bits = __float_as_uint(pv);
-    const uint64_t w = fx46(pv);
-    if ((bits >> 21) == d1 && w) {
-      const int k = __hip_atomic_fetch_add(&sh.gcount, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (k < kWave) {
-        sh.gbits[k] = bits;
-        sh.gw[k] = w;
-      }
-    }
-  }
-  __syncthreads();
-  const int cnt = sh.gcount;
-  if (cnt > kWave) {
+    });
     __syncthreads();
-    return radix_select(sh, thr, [&](auto f) {
-      for (int i = t; i < n; i += kRB) {
-        const float pv = sh.cval[i];
-        f(__float_as_uint(pv), fx46(pv));
+    const uint32_t cnt = fs.gcount;
+    if (cnt > kGather && round == 2) {
+      // every entry of the bucket has the same bits
+      *cutoff = __uint_as_float(prefix);
+      *mass = above + binmass;
+      return true;
+    }
+    if (cnt <= kGather) {
+      if (wid == 0) {
+        const uint32_t b = lane < static_cast<int>(cnt) ? fs.gbits[lane] : 0u;
+        const uint64_t w = lane < static_cast<int>(cnt) ? fs.gw[lane] : 0;
+        uint64_t A = above;
+        for (int j = 0; j < static_cast<int>(cnt); ++j) {
+          const uint32_t bj = lane_bcast_u32(b, j);
+          const uint64_t wj = lane_bcast_u64(w, j);
+          A += bj >= b ? wj : 0;
+        }
+        const bool ok = lane < static_cast<int>(cnt) && A >= thr;
+        const uint64_t best = wave_max_u64(ok ? b : 0u);
+        const uint64_t at = wave_max_u64(ok && b == static_cast<uint32_t>(best) ? A : 0);
+        if (lane == 0) {
+          sh.u32s[2] = static_cast<uint32_t>(best);
+          sh.u64s[4] = at;
+        }
       }
-    }, cutoff, mass);
-  }
-  if (wid == 0) {
-    const uint32_t b = lane < cnt ? sh.gbits[lane] : 0u;
-    const uint64_t w = lane < cnt ? sh.gw[lane] : 0;
-    uint64_t A = above;
-    for (int j = 0; j < cnt; ++j) {
-      const uint32_t bj = lane_bcast_u32(b, j);
-      const uint64_t wj = lane_bcast_u64(w, j);
-      A += bj >= b ? wj : 0;
+      __syncthreads();
+      *cutoff = __uint_as_float(sh.u32s[2]);
+      *mass = sh.u64s[4];
+      return true;
     }
-    const bool ok = lane < cnt && A >= thr;
-    const uint64_t best = wave_max_u64(ok ? b : 0u);
-    const uint64_t at = wave_max_u64(ok && b == static_cast<uint32_t>(best) ? A : 0);
-    if (lane == 0) {
-      sh.u32s[2] = static_cast<uint32_t>(best);
-      sh.u64s[4] = at;
-    }
+    __syncthreads();
   }
-  __syncthreads();
-  *cutoff = __uint_as_float(sh.u32s[2]);
-  *mass = sh.u64s[4];
-  return true;
+  return false;  // not reached
 }
 
-// Index-ordered inverse-CDF pick over n LDS entries (cidx, weight w(i)),
-// n <= kRowCand; lane t owns entries [8t, 8t+8). Zero total mass selects
-// zero_index.
+// p of element i of a row recomputed from its logit.
+template <int DT>
+__device__ __forceinline__ float p_elem(const char* rowp, const uint32_t* bm, float c, float pen, float inv_pen,
+                                        const float* mcj, const float* gj, int i) {
+  float l = load_elem<DT>(rowp, i);
+  if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
+  const int j = i >> kChunkShift;
+  return exp2q(__builtin_fmaf(l, c, -mcj[j])) * gj[j];
+}
+
+// Index-ordered inverse-CDF pick over the first n LDS slots; weight(s) is an
+// exact fx46 mass. Lane t owns slots [16t, 16t+16). Returns the winning slot,
+// or -1 at zero total mass.
 template <typename W>
-__device__ int64_t pick_lds(RowShared& sh, int n, float u, W weight, int64_t zero_index) {
-  constexpr int kPer = kRowCand / kRB;
+__device__ int pick_slot(Shared& sh, int n, float u, W weight) {
   const int t = threadIdx.x;
-  const int i0 = kPer * t;
+  const int s0 = kSlotsPerLane * t;
   uint64_t sum = 0;
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) sum += i0 + q < n ? weight(i0 + q) : 0;
+  for (int q = 0; q < kSlotsPerLane; ++q) sum += s0 + q < n ? weight(s0 + q) : 0;
   uint64_t total;
-  const uint64_t ex = row_excl_scan(sum, sh.red, &total);
-  if (t == 0) sh.u64s[3] = static_cast<uint64_t>(zero_index);
+  const uint64_t ex = block_excl_scan(sum, sh.red, &total);
+  if (t == 0) sh.u32s[3] = kNone;
   __syncthreads();
   if (total > 0) {
     const uint64_t target = floor_u_times(u, total);
     if (ex <= target && target < ex + sum) {
       uint64_t run = ex;
-      for (int q = 0; q < kPer; ++q) {
-        if (i0 + q >= n) break;
-        run += weight(i0 + q);
+      for (int q = 0; q < kSlotsPerLane; ++q) {
+        if (s0 + q >= n) break;
+        run += weight(s0 + q);
         if (run > target) {
-          sh.u64s[3] = sh.cidx[i0 + q];
+          sh.u32s[3] = static_cast<uint32_t>(s0 + q);
           break;
         }
       }
     }
   }
   __syncthreads();
-  return static_cast<int64_t>(sh.u64s[3]);
+  const uint32_t s = sh.u32s[3];
+  return s == kNone ? -1 : static_cast<int>(s);
 }
 
-// Dense inverse-CDF pick over a whole row whose masses are computed by
-// weight(idx) (an exact fx46 integer). Lane t owns a contiguous index range.
+// Dense inverse-CDF pick over a whole row whose masses weight(idx) are
+// computed on the fly. Lane t owns a contiguous index range.
 template <typename W>
-__device__ int64_t pick_dense(RowShared& sh, int vocab, float u, W weight) {
+__device__ int64_t pick_dense(Shared& sh, int vocab, float u, W weight) {
   const int t = threadIdx.x;
-  const int per = (vocab + kRB - 1) / kRB;
+  const int per = (vocab + kCB - 1) / kCB;
   const int a = t * per < vocab ? t * per : vocab;
   const int b = a + per < vocab ? a + per : vocab;
   uint64_t sum = 0;
   for (int i = a; i < b; ++i) sum += weight(i);
   uint64_t total;
-  const uint64_t ex = row_excl_scan(sum, sh.red, &total);
+  const uint64_t ex = block_excl_scan(sum, sh.red, &total);
   if (t == 0) sh.u64s[3] = 0;
   __syncthreads();
   if (total > 0) {
@@ -653,426 +782,411 @@ __device__ int64_t pick_dense(RowShared& sh, int vocab, float u, W weight) {
   return static_cast<int64_t>(sh.u64s[3]);
 }
 
-__device__ __forceinline__ void put_stat(RowStat* st, const RowStat& v) {
-  uint32_t* w = reinterpret_cast<uint32_t*>(st);
-  store_sc(w + 0, __float_as_uint(v.m));
-  store_sc(w + 1, __float_as_uint(v.s));
-  store_sc(w + 2, __float_as_uint(v.cutoff));
-  store_sc(w + 3, __float_as_uint(v.mass));
-  store_sc(w + 4, v.n_sup);
-  store_sc(w + 5, v.flags);
-  store_sc64(reinterpret_cast<uint64_t*>(w + 6), v.s_fx);
-  store_sc64(reinterpret_cast<uint64_t*>(w + 8), v.mass_fx);
-}
-__device__ __forceinline__ RowStat get_stat(const RowStat* st) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(st);
-  RowStat v;
-  v.m = __uint_as_float(load_sc(w + 0));
-  v.s = __uint_as_float(load_sc(w + 1));
-  v.cutoff = __uint_as_float(load_sc(w + 2));
-  v.mass = __uint_as_float(load_sc(w + 3));
-  v.n_sup = load_sc(w + 4);
-  v.flags = load_sc(w + 5);
-  v.s_fx = load_sc64(reinterpret_cast<const uint64_t*>(w + 6));
-  v.mass_fx = load_sc64(reinterpret_cast<const uint64_t*>(w + 8));
-  return v;
-}
-
-// Filtered probability of token idx of row r (stats st), recomputed from its
-// logit; bm is the group's penalty bitmap.
+// Exact select over every element of the row (the candidates did not hold the
+// cutoff): p recomputed from the re-read logits, g_j in fs.g[0]. When keep is
+// set, leaves the support {p >= c} in index order in fs.slot (as idx << 32 |
+// bits(p)) and returns its size, or -1 if it does not fit. Out of line, with
+// plain arguments, so the common path's registers are unaffected.
 template <int DT>
-__device__ float prob_at(const SampParams& p, const Xf& f, const uint32_t* bm, int64_t r, const char* rowp,
-                         const RowStat& st, int idx) {
-  const float x = xform_seen(f, load_elem<DT>(rowp, idx), f.use_pen && bit_of(bm, idx));
-  const float mj = p.chunks[r * p.nch + (idx / kChunk)].m;
-  const float pe = chunk_p(x, mj, st.m, st.s);
-  if (st.flags & kFlagUnfiltered) return pe;
-  return pe >= st.cutoff ? pe / st.mass : 0.0f;
-}
-
-// The chain-verify tail for batch element g (whole workgroup, uniform flow).
-template <int DT>
-__device__ void spec_tail(const SampParams& p, RowShared& sh, int64_t g, const uint32_t* bm) {
-  const Xf xf = make_xf(p);
-  const int k = p.k;
-  const int rpg = 2 * k + 1;
+__device__ __noinline__ int slow_select(Shared& sh, const char* rowp, const uint32_t* bm, float c, float pen,
+                                        float inv_pen, int vocab, uint64_t thr, bool keep, float* cutoff,
+                                        uint64_t* mass_fx) {
+  FinSh& fs = sh.f;
   const int t = threadIdx.x;
-  const int64_t r0 = g * rpg;
-  if (t < rpg) sh.st[t] = get_stat(p.stats + r0 + t);
+  const float* mcj = fs.mcj[0];
+  const float* gj = fs.g[0];
+  auto pval = [&](int i) { return p_elem<DT>(rowp, bm, c, pen, inv_pen, mcj, gj, i); };
+#pragma unroll
+  for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
   __syncthreads();
-  // P_i(x_i) (lanes i < k) and Q_i(x_i) (lanes k + i), all in flight together
-  if (t < 2 * k) {
-    const int i = t < k ? t : t - k;
-    const int jr = t < k ? i : k + 1 + i;
-    const int64_t x = p.draft_tokens[g * k + i];
-    float v = 0.0f;
-    if (x >= 0 && x < p.vocab) v = prob_at<DT>(p, xf, bm, r0 + jr, row_of(p, g, jr), sh.st[jr], static_cast<int>(x));
-    sh.pa[t] = v;
-  }
-  __syncthreads();
-  if (t == 0) {
-    int a = 0;
-    while (a < k) {
-      const int64_t x = p.draft_tokens[g * k + a];
-      const bool ok = x >= 0 && x < p.vocab && accept_draw(p.uniforms[g * rpg + a], sh.pa[a], sh.pa[k + a]);
-      if (!ok) break;
-      p.tokens[g * (k + 1) + a] = x;
-      ++a;
-    }
-    sh.tail_flag = a;
-  }
-  __syncthreads();
-  const int a = sh.tail_flag;
-  const RowStat st_t = sh.st[a];
-  const char* trow = row_of(p, g, a);
-  int64_t token;
-  if (a < k) {
-    const RowStat st_d = sh.st[k + 1 + a];
-    const char* drow = row_of(p, g, k + 1 + a);
-    const int64_t rt = r0 + a, rd = r0 + k + 1 + a;
-    const float u = p.uniforms[g * rpg + k + a];
-    if (!(st_t.flags & kFlagDense)) {
-      // Support entries of the target row: P_j = p_j / M; Q_j recomputed from
-      // the draft logits; D_j = max(P_j - Q_j, 0). P_j is kept in H for the
-      // zero-residual fallback.
-      const int n = static_cast<int>(st_t.n_sup);
-      const uint64_t* sup = p.support + rt * static_cast<int64_t>(kSupCap);
-      float* pkeep = reinterpret_cast<float*>(sh.H);
-      for (int i = t; i < n; i += kRB) {
-        const uint64_t en = load_sc64(sup + i);
-        const uint32_t idx = static_cast<uint32_t>(en >> 32);
-        const float pj = __uint_as_float(static_cast<uint32_t>(en)) / st_t.mass;
-        const float qj = prob_at<DT>(p, xf, bm, rd, drow, st_d, static_cast<int>(idx));
-        const float dj = pj - qj;
-        sh.cidx[i] = idx;
-        sh.cval[i] = dj > 0.0f ? dj : 0.0f;
-        pkeep[i] = pj;
-      }
-      __syncthreads();
-      uint64_t dsum = 0, psum = 0;
-      for (int i = t; i < n; i += kRB) {
-        dsum += fx46(sh.cval[i]);
-        psum += fx46(pkeep[i]);
-      }
-      const uint64_t d_fx = block_sum_u64<kRB>(dsum, sh.red);
-      const uint64_t p_fx = block_sum_u64<kRB>(psum, sh.red);
-      const bool use_d = d_fx > 0;
-      const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
-      token = pick_lds(sh, n, u, [&](int i) {
-        const float v = use_d ? sh.cval[i] : pkeep[i];
-        return fx46(v / den);
-      }, 0);
-    } else {
-      uint64_t dsum = 0, psum = 0;
-      {
-        const int per = (p.vocab + kRB - 1) / kRB;
-        const int i0 = t * per < p.vocab ? t * per : p.vocab;
-        const int i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
-        for (int i = i0; i < i1; ++i) {
-          const float pj = prob_at<DT>(p, xf, bm, rt, trow, st_t, i);
-          const float qj = prob_at<DT>(p, xf, bm, rd, drow, st_d, i);
-          const float dj = pj - qj;
-          dsum += fx46(dj > 0.0f ? dj : 0.0f);
-          psum += fx46(pj);
-        }
-      }
-      const uint64_t d_fx = block_sum_u64<kRB>(dsum, sh.red);
-      const uint64_t p_fx = block_sum_u64<kRB>(psum, sh.red);
-      const bool use_d = d_fx > 0;
-      const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
-      token = pick_dense(sh, p.vocab, u, [&](int i) {
-        const float pj = prob_at<DT>(p, xf, bm, rt, trow, st_t, i);
-        float v = pj;
-        if (use_d) {
-          const float dj = pj - prob_at<DT>(p, xf, bm, rd, drow, st_d, i);
-          v = dj > 0.0f ? dj : 0.0f;
-        }
-        return fx46(v / den);
-      });
-    }
-  } else {
-    const float u = p.uniforms[g * rpg + 2 * k];
-    const int64_t rt = r0 + k;
-    if (!(st_t.flags & kFlagDense)) {
-      const int n = static_cast<int>(st_t.n_sup);
-      const uint64_t* sup = p.support + rt * static_cast<int64_t>(kSupCap);
-      for (int i = t; i < n; i += kRB) {
-        const uint64_t en = load_sc64(sup + i);
-        sh.cidx[i] = static_cast<uint32_t>(en >> 32);
-        sh.cval[i] = __uint_as_float(static_cast<uint32_t>(en)) / st_t.mass;
-      }
-      __syncthreads();
-      token = pick_lds(sh, n, u, [&](int i) { return fx46(sh.cval[i]); }, 0);
-    } else {
-      token = pick_dense(sh, p.vocab, u,
-                         [&](int i) { return fx46(prob_at<DT>(p, xf, bm, rt, trow, st_t, i)); });
-    }
-  }
-  if (t == 0) {
-    p.tokens[g * (k + 1) + a] = token;
-    for (int j = a + 1; j <= k; ++j) p.tokens[g * (k + 1) + j] = -1;
-    p.accept_len[g] = a;
-    store_sc(p.counters + g * kCounterStride, 0u);
-  }
-}
-
-// Exact select over every element of the row (the candidates did not hold
-// the cutoff): p recomputed from the re-read logits. Leaves the support
-// {p >= c} in index order in LDS when it fits, else flags the row dense.
-// Kept out of line so the common path's register allocation is unaffected.
-template <int DT>
-__device__ __noinline__ void slow_select(const SampParams& p, RowShared& sh, const char* rowp, const uint32_t* bm,
-                                         float m, float s, uint64_t thr, float* cutoff, uint64_t* mass_fx,
-                                         int* n_sup, uint32_t* flags) {
-  const Xf xf = make_xf(p);
-  const int t = threadIdx.x;
-  const int vocab = p.vocab;
-  auto pval = [&](int i) -> float {
-    const float x = xform_seen(xf, load_elem<DT>(rowp, i), xf.use_pen && bit_of(bm, i));
-    return chunk_p(x, sh.cm[i / kChunk], m, s);
-  };
-  float c;
+  float cc;
   uint64_t mfx;
   const bool ok = radix_select(sh, thr, [&](auto f) {
-    for (int i = t; i < vocab; i += kRB) {
+    for (int i = t; i < vocab; i += kCB) {
       const float pv = pval(i);
       f(__float_as_uint(pv), fx46(pv));
     }
-  }, &c, &mfx);
-  if (ok) {
-    *cutoff = c;
-    *mass_fx = mfx;
-  } else {
+  }, &cc, &mfx);
+  if (!ok) {
     // Total mass below the threshold: keep the whole row (cutoff = min p).
     float mn = __builtin_inff();
     uint64_t tot = 0;
-    for (int i = t; i < vocab; i += kRB) {
+    for (int i = t; i < vocab; i += kCB) {
       const float pv = pval(i);
       mn = fminf(mn, pv);
       tot += fx46(pv);
     }
-    *cutoff = -block_max_f32<kRB>(-mn, sh.redf);
-    *mass_fx = block_sum_u64<kRB>(tot, sh.red);
+    mn = wave_max_f32(-mn);
+    if ((t & (kWave - 1)) == 0) sh.f32s[t / kWave] = mn;
+    tot = block_sum(tot, sh.red);
+    cc = -nmax(nmax(sh.f32s[0], sh.f32s[1]), nmax(sh.f32s[2], sh.f32s[3]));
+    mfx = tot;
+    __syncthreads();
   }
-  const float cc = *cutoff;
-  // support in index order: contiguous lane ranges, counted then written
-  const int per = (vocab + kRB - 1) / kRB;
+  *cutoff = cc;
+  *mass_fx = mfx;
+  if (!keep) return -1;
+  const int per = (vocab + kCB - 1) / kCB;
   const int a = t * per < vocab ? t * per : vocab;
   const int b = a + per < vocab ? a + per : vocab;
   uint64_t cnt = 0;
   for (int i = a; i < b; ++i) cnt += pval(i) >= cc ? 1 : 0;
   uint64_t total;
-  const uint64_t ex = row_excl_scan(cnt, sh.red, &total);
-  if (total <= static_cast<uint64_t>(kSupCap)) {
-    int pos = static_cast<int>(ex);
-    for (int i = a; i < b; ++i) {
-      const float pv = pval(i);
-      if (pv >= cc) {
-        sh.cidx[pos] = static_cast<uint32_t>(i);
-        sh.cval[pos] = pv;
-        ++pos;
-      }
-    }
-    *n_sup = static_cast<int>(total);
-  } else {
-    *flags |= kFlagDense;
+  const uint64_t ex = block_excl_scan(cnt, sh.red, &total);
+  if (total > static_cast<uint64_t>(kRowCand)) return -1;
+  int pos = static_cast<int>(ex);
+  for (int i = a; i < b; ++i) {
+    const float pv = pval(i);
+    if (pv >= cc) fs.slot[pos++] = (static_cast<uint64_t>(i) << 32) | __float_as_uint(pv);
   }
   __syncthreads();
+  return static_cast<int>(total);
 }
 
-template <int DT, int MODE>
-__global__ __launch_bounds__(kRB, 4) void row_kernel(const SampParams p) {
-  __shared__ RowShared sh;
-  const int t = threadIdx.x;
-  const int jr = blockIdx.x;
-  const int64_t g = blockIdx.y;
-  const int64_t r = g * p.rpg + jr;
-  const char* rowp = row_of(p, g, jr);
-  const Xf xf = make_xf(p);
-  const int nch = p.nch;
+// Candidate slot s of row r: (idx << 32 | bits(e)); stale beyond n_j.
+__device__ __forceinline__ uint64_t load_slot(const SampParams& p, int64_t r, int s) {
+  return p.cands[(r * p.nch + (s >> p.cap_log2)) * kChunkCand + (s & (p.cap - 1))];
+}
 
-  // chunk records (wave 0: one lane per chunk): m, f_j, T, candidate offsets
-  const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;  // group's penalty bits
-  if (t < kWave) {
-    const int lane = t;
-    ChunkRec rec{};
-    rec.m = -__builtin_inff();
-    if (lane < nch) rec = p.chunks[r * nch + lane];
-    const float rm = wave_max_f32(rec.m);
-    const float f = lane < nch ? ls_exp(rec.m - rm) : 0.0f;
-    const uint64_t T = wave_sum_u64(lane < nch ? floor_u_times(f, rec.mass) : 0);
-    const uint32_t cnt = lane < nch ? rec.n : 0u;
-    const uint32_t inc = wave_scan_add_u32(cnt);
-    if (lane < nch) {
-      sh.cm[lane] = rec.m;
-      sh.cf[lane] = f;
-      sh.cK[lane] = rec.K;
-      sh.cn[lane] = rec.n;
-      sh.cfl[lane] = rec.flags;
-      sh.coff[lane] = static_cast<int>(inc - cnt);
-    }
-    if (lane == nch - 1) sh.coff[nch] = static_cast<int>(inc);
-    if (lane == 0) {
-      sh.u64s[0] = T;
-      sh.u32s[0] = __float_as_uint(rm);
+__device__ __forceinline__ bool slot_valid(const FinSh& fs, int slot, const SampParams& p, int s) {
+  return (s & (p.cap - 1)) < static_cast<int>(fs.n[slot][s >> p.cap_log2]);
+}
+
+// Inverse-CDF draw over this workgroup's own row (fs.slot holds idx | bits(p)
+// of n slots, fs.g[0] / fs.mcj[0] the row's scales): weights fx46(P), P the
+// filtered, renormalised probability; the whole row when it is dense.
+template <int DT>
+__device__ int64_t own_draw(const SampParams& p, Shared& sh, const RowStat& st, int n, float u, const char* rowp,
+                            const uint32_t* bm) {
+  FinSh& fs = sh.f;
+  const bool unf = st.flags & kFlagUnfiltered;
+  if (!(st.flags & kFlagDense)) {
+    const float cc = st.cutoff, mass = st.mass;
+    const int win = pick_slot(sh, n, u, [&](int s) {
+      const float x = __uint_as_float(static_cast<uint32_t>(fs.slot[s]));
+      return x >= cc && x > 0.0f ? fx46(x / mass) : 0ull;
+    });
+    return win < 0 ? 0 : static_cast<int64_t>(fs.slot[win] >> 32);
+  }
+  const float cc = st.cutoff, mass = st.mass;
+  return pick_dense(sh, p.vocab, u, [&](int i) {
+    const float x = p_elem<DT>(rowp, bm, p.c, p.pen, p.inv_pen, fs.mcj[0], fs.g[0], i);
+    return fx46(unf ? x : (x >= cc ? x / mass : 0.0f));
+  });
+}
+
+// Residual draw for draft position i of group g: normalize(max(P_i - Q_i, 0))
+// (fallback normalize(P_i), rejection.py:60-69) with the uniform u[g, k+i].
+// P_i comes from the target row's candidates (already in fs.slot / fs.g[0]
+// when `own`, i.e. this workgroup finalised the target row); Q_i is
+// recomputed from the draft logits at the support indices.
+template <int DT>
+__device__ int64_t residual_draw(const SampParams& p, Shared& sh, int64_t g, int i, bool own) {
+  FinSh& fs = sh.f;
+  const int k = p.k, rpg = 2 * k + 1, nch = p.nch, nslots = nch * p.cap;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int64_t rt = g * rpg + i, rd = g * rpg + k + 1 + i;
+  // 1. both rows' statistics, chunk records, and the target's candidates
+  if (t < 8) fs.statw[t] = load_sc64(reinterpret_cast<const uint64_t*>(p.stats + (t < 4 ? rt : rd)) + (t & 3));
+  ChunkRec rec_t{}, rec_d{};
+  if (wid == 0 && lane < nch) {
+    rec_d = p.chunks[rd * nch + lane];
+    if (!own) rec_t = p.chunks[rt * nch + lane];
+  }
+  if (!own) {
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int s = t + q * kCB;
+      if (s < nslots) fs.slot[s] = load_slot(p, rt, s);
     }
   }
   __syncthreads();
-  const float m = __uint_as_float(sh.u32s[0]);
-  const uint64_t s_fx = sh.u64s[0];
-  const float s = mass_to_f32(s_fx);
-
-  const float top_p = p.top_p_rows ? p.top_p_rows[r] : p.top_p;
-  const bool unfiltered = !(top_p < 1.0f);
-  float cutoff = 0.0f;
-  uint64_t mass_fx = s_fx;
-  uint32_t flags = unfiltered ? (kFlagUnfiltered | kFlagDense) : 0u;
-  int n_sup = 0;
-
-  if (!unfiltered) {
-    const uint64_t thr = fx46(top_p);
-    // candidates of every chunk, p = RN(RN(e f_j) / S), in index order
-    const int n = sh.coff[nch];
-    for (int i = t; i < n; i += kRB) {
-      int j = 0;
-      while (j + 1 < nch && sh.coff[j + 1] <= i) ++j;
-      const uint64_t en = p.cands[(r * nch + j) * static_cast<int64_t>(kChunkCand) + (i - sh.coff[j])];
-      const float e = __uint_as_float(static_cast<uint32_t>(en));
-      sh.cidx[i] = static_cast<uint32_t>(en >> 32);
-      sh.cval[i] = (e * sh.cf[j]) / s;
-    }
-    // every p outside the candidates is <= p_bound
-    float p_bound = 0.0f;
-    for (int j = 0; j < nch; ++j) {
-      if (!(sh.cfl[j] & kChunkComplete)) {
-        const float eb = __builtin_ldexpf(sh.cf[j], 1 - sh.cK[j]);
-        p_bound = fmaxf(p_bound, eb / s);
+  const RowStat st_t = stat_of(fs.statw[0], fs.statw[1], fs.statw[2], fs.statw[3]);
+  const RowStat st_d = stat_of(fs.statw[4], fs.statw[5], fs.statw[6], fs.statw[7]);
+  if (wid == 0) {
+    if (!own) row_g(fs, 0, rec_t, nch, st_t.mcmax, st_t.s);
+    row_g(fs, 1, rec_d, nch, st_d.mcmax, st_d.s);
+  }
+  __syncthreads();
+  const bool unf_t = st_t.flags & kFlagUnfiltered;
+  const bool unf_d = st_d.flags & kFlagUnfiltered;
+  const float u = p.uniforms[g * rpg + k + i];
+  const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
+  const char* drow = row_of(p, g, k + 1 + i);
+  auto Qof = [&](float l, int j) {
+    const float x = exp2q(__builtin_fmaf(l, p.c, -fs.mcj[1][j])) * fs.g[1][j];
+    return unf_d ? x : (x >= st_d.cutoff ? x / st_d.mass : 0.0f);
+  };
+  if (!(st_t.flags & kFlagDense)) {
+    // P over the target's support, the draft logits there gathered at once
+    float P[kSlotsPerLane], lq[kSlotsPerLane];
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int s = t + q * kCB;
+      P[q] = 0.0f;
+      lq[q] = 0.0f;
+      if (s < nslots && slot_valid(fs, 0, p, s)) {
+        const uint64_t v = fs.slot[s];
+        const float pv = own ? __uint_as_float(static_cast<uint32_t>(v))
+                             : __uint_as_float(static_cast<uint32_t>(v)) * fs.g[0][s >> p.cap_log2];
+        if (pv >= st_t.cutoff && pv > 0.0f) {
+          P[q] = pv / st_t.mass;
+          lq[q] = load_elem<DT>(drow, static_cast<int64_t>(v >> 32));
+        }
       }
     }
+    float D[kSlotsPerLane];
+    uint64_t dsum = 0, psum = 0;
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int s = t + q * kCB;
+      D[q] = 0.0f;
+      if (P[q] > 0.0f) {
+        const int idx = static_cast<int>(fs.slot[s] >> 32);
+        float l = lq[q];
+        if (bm && bit_of(bm, idx)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+        const float dv = P[q] - Qof(l, idx >> kChunkShift);
+        D[q] = dv > 0.0f ? dv : 0.0f;
+        dsum += fx46(D[q]);
+        psum += fx46(P[q]);
+      }
+    }
+    const uint64_t d_fx = block_sum(dsum, sh.red);
+    const uint64_t p_fx = block_sum(psum, sh.red);
+    const bool use_d = d_fx > 0;
+    const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int s = t + q * kCB;
+      if (s < nslots) fs.w[s] = (use_d ? D[q] : P[q]) / den;
+    }
     __syncthreads();
+    const int win = pick_slot(sh, nslots, u, [&](int s) { return fx46(fs.w[s]); });
+    return win < 0 ? 0 : static_cast<int64_t>(fs.slot[win] >> 32);
+  }
+  // dense target row: the whole vocabulary
+  const char* trow = row_of(p, g, i);
+  auto Pof = [&](int x) {
+    const float pv = p_elem<DT>(trow, bm, p.c, p.pen, p.inv_pen, fs.mcj[0], fs.g[0], x);
+    return unf_t ? pv : (pv >= st_t.cutoff ? pv / st_t.mass : 0.0f);
+  };
+  auto Qat = [&](int x) {
+    float l = load_elem<DT>(drow, x);
+    if (bm && bit_of(bm, x)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+    return Qof(l, x >> kChunkShift);
+  };
+  uint64_t dsum = 0, psum = 0;
+  {
+    const int per = (p.vocab + kCB - 1) / kCB;
+    const int i0 = t * per < p.vocab ? t * per : p.vocab;
+    const int i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
+    for (int x = i0; x < i1; ++x) {
+      const float pj = Pof(x);
+      const float dj = pj - Qat(x);
+      dsum += fx46(dj > 0.0f ? dj : 0.0f);
+      psum += fx46(pj);
+    }
+  }
+  const uint64_t d_fx = block_sum(dsum, sh.red);
+  const uint64_t p_fx = block_sum(psum, sh.red);
+  const bool use_d = d_fx > 0;
+  const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
+  return pick_dense(sh, p.vocab, u, [&](int x) {
+    const float pj = Pof(x);
+    float v = pj;
+    if (use_d) {
+      const float dj = pj - Qat(x);
+      v = dj > 0.0f ? dj : 0.0f;
+    }
+    return fx46(v / den);
+  });
+}
+
+// The accept chain of group g once every draw is published: the first
+// rejected position a (u < min(1, P/Q) per position, sampler.py:451-452),
+// then the accepted drafts, the draw of position a, and -1 after it.
+__device__ void accept_chain(const SampParams& p, Shared& sh, int64_t g) {
+  FinSh& fs = sh.f;
+  const int k = p.k, rpg = 2 * k + 1;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int64_t r0 = g * rpg;
+  if (t < rpg) fs.tokp[t] = hi_f(load_sc64(reinterpret_cast<const uint64_t*>(p.stats + r0 + t) + 2));
+  if (t <= k) fs.tokd[t] = static_cast<int64_t>(load_sc64(reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1) + t));
+  int64_t x = -1;
+  float ux = 0.0f;
+  if (wid == 0 && lane < k) {
+    x = p.draft_tokens[g * k + lane];
+    ux = p.uniforms[g * rpg + lane];
+  }
+  __syncthreads();
+  if (wid == 0) {
+    const bool valid = x >= 0 && x < p.vocab;
+    const bool ok = lane < k && valid && accept_draw(ux, fs.tokp[lane], fs.tokp[k + 1 + lane]);
+    const uint64_t bad = __ballot(lane < k && !ok);
+    const int a = bad ? __builtin_ctzll(bad) : k;
+    int64_t* out = p.tokens + g * (k + 1);
+    if (lane < a) out[lane] = x;
+    if (lane == a) out[lane] = fs.tokd[a];
+    if (lane > a && lane <= k) out[lane] = -1;
+    if (k >= kWave && lane == 0) {
+      for (int j = kWave; j <= k; ++j) out[j] = j < a ? p.draft_tokens[g * k + j] : (j == a ? fs.tokd[a] : -1);
+    }
+    if (lane == 0) p.accept_len[g] = a;
+  }
+}
+
+// Row finalisation: one workgroup per row.
+template <int DT, int MODE>
+__global__ __launch_bounds__(kCB) void row_kernel(const SampParams p) {
+  __shared__ Shared sh;
+  FinSh& fs = sh.f;
+  const int r = blockIdx.x;
+  const int t = threadIdx.x, wid = t / kWave;
+  const int nch = p.nch;
+  const int64_t g = r / p.rpg;
+  const int jr = r - static_cast<int>(g) * p.rpg;
+  const int nslots = nch * p.cap;
+  const float top_p = p.top_p_rows ? p.top_p_rows[r] : p.top_p;
+  const bool unfiltered = !(top_p < 1.0f);
+  const char* rowp = row_of(p, g, jr);
+  const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
+
+  // 1. chunk records (wave 0) and candidate slots (strided), in flight together
+  ChunkRec rec{};
+  if (wid == 0 && t < nch) rec = p.chunks[static_cast<int64_t>(r) * nch + t];
+  uint64_t cv[kSlotsPerLane];
+#pragma unroll
+  for (int q = 0; q < kSlotsPerLane; ++q) {
+    const int s = t + q * kCB;
+    cv[q] = (!unfiltered && s < nslots) ? load_slot(p, r, s) : 0;
+  }
+#pragma unroll
+  for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
+  // 2. row scales
+  if (wid == 0) {
+    const RowScale rs = row_scale(fs, 0, rec, nch);
+    if (t == 0) {
+      sh.f32s[4] = rs.mcmax;
+      sh.f32s[5] = rs.s;
+      sh.f32s[6] = rs.p_bound;
+      sh.f32s[7] = rs.has_tok ? rs.p_tok : -1.0f;
+    }
+  }
+  __syncthreads();
+  const float mcmax = sh.f32s[4], s_row = sh.f32s[5], p_bound = sh.f32s[6], p_tok = sh.f32s[7];
+  // 3. p of the candidates, kept in registers and in fs.slot
+  float pv[kSlotsPerLane];
+#pragma unroll
+  for (int q = 0; q < kSlotsPerLane; ++q) {
+    const int s = t + q * kCB;
+    pv[q] = 0.0f;
+    if (!unfiltered && s < nslots && slot_valid(fs, 0, p, s))
+      pv[q] = __uint_as_float(static_cast<uint32_t>(cv[q])) * fs.g[0][s >> p.cap_log2];
+    if (s < nslots) fs.slot[s] = ((cv[q] >> 32) << 32) | __float_as_uint(pv[q]);
+  }
+  float cutoff = 0.0f;
+  uint64_t mass_fx = 0;
+  uint32_t flags = unfiltered ? (kFlagUnfiltered | kFlagDense) : 0u;
+  int n_sup = nslots;
+  if (!unfiltered) {
+    const uint64_t thr = fx46(top_p);
     float c;
     uint64_t mfx;
-    const bool ok = select_candidates(sh, n, thr, &c, &mfx);
+    const bool ok = radix_select(sh, thr, [&](auto f) {
+#pragma unroll
+      for (int q = 0; q < kSlotsPerLane; ++q) {
+        const float x = pv[q];
+        if (x > 0.0f) f(__float_as_uint(x), fx46(x));
+      }
+    }, &c, &mfx);
     if (ok && c > p_bound) {
       cutoff = c;
       mass_fx = mfx;
-      // support = candidates with p >= c, compacted in index order in LDS
-      constexpr int kPer = kRowCand / kRB;
-      const int i0 = kPer * t;
-      uint32_t keep = 0;
-      uint64_t cnt = 0;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        const bool f = i0 + q < n && sh.cval[i0 + q] >= c;
-        keep |= f ? (1u << q) : 0u;
-        cnt += f ? 1 : 0;
-      }
-      uint32_t xi[kPer];
-      float xv[kPer];
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        xi[q] = (keep >> q) & 1u ? sh.cidx[i0 + q] : 0u;
-        xv[q] = (keep >> q) & 1u ? sh.cval[i0 + q] : 0.0f;
-      }
-      uint64_t tot;
-      const uint64_t ex = row_excl_scan(cnt, sh.red, &tot);
-      __syncthreads();
-      int pos = static_cast<int>(ex);
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        if ((keep >> q) & 1u) {
-          sh.cidx[pos] = xi[q];
-          sh.cval[pos] = xv[q];
-          ++pos;
-        }
-      }
-      __syncthreads();
-      n_sup = static_cast<int>(tot);
-      if (MODE == kModeSpec && n_sup > kSupCap) flags |= kFlagDense;
     } else {
       flags |= kFlagSlow;
-      slow_select<DT>(p, sh, rowp, bm, m, s, thr, &cutoff, &mass_fx, &n_sup, &flags);
+      __syncthreads();
+      n_sup = slow_select<DT>(sh, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, thr, MODE == kModeSample, &cutoff,
+                              &mass_fx);
+      if (MODE != kModeSample || n_sup < 0) flags |= kFlagDense;
     }
   }
-  const float mass = unfiltered ? 1.0f : mass_to_f32(mass_fx);
+  RowStat st;
+  st.mcmax = mcmax;
+  st.s = s_row;
+  st.cutoff = cutoff;
+  st.mass = unfiltered ? 1.0f : mass_to_f32(mass_fx);
+  st.flags = flags;
+  st.p_tok = 0.0f;
+  st.mass_fx = mass_fx;
+  if (p_tok >= 0.0f) st.p_tok = unfiltered ? p_tok : (p_tok >= cutoff ? p_tok / st.mass : 0.0f);
 
   if constexpr (MODE == kModeSpec) {
-    RowStat st;
-    st.m = m;
-    st.s = s;
-    st.cutoff = cutoff;
-    st.mass = mass;
-    st.n_sup = static_cast<uint32_t>(n_sup);
-    st.flags = flags;
-    st.s_fx = s_fx;
-    st.mass_fx = mass_fx;
-    if (!(flags & kFlagDense)) {
-      uint64_t* sup = p.support + r * static_cast<int64_t>(kSupCap);
-      for (int i = t; i < n_sup; i += kRB)
-        store_sc64(sup + i, (static_cast<uint64_t>(sh.cidx[i]) << 32) | __float_as_uint(sh.cval[i]));
-    }
-    if (t == 0) put_stat(p.stats + r, st);
-    drain_stores();
-    __syncthreads();
+    const int k = p.k;
     if (t == 0) {
-      const uint32_t prev = atomic_arrive(p.counters + g * kCounterStride);
-      sh.tail_flag = prev == static_cast<uint32_t>(p.rpg - 1);
+      put_stat(p.stats + r, st);
+      drain_stores();
     }
-    __syncthreads();
-    if (sh.tail_flag) spec_tail<DT>(p, sh, g, bm);
+    // Pair (target i, draft i): the second to finish draws position i's
+    // residual; the bonus row draws the bonus token. Each draw arrives on the
+    // group's counter; the last arrival runs the accept chain.
+    bool draw_here = jr == k;
+    const int i = jr < k ? jr : jr - k - 1;
+    if (jr != k) {
+      if (t == 0) {
+        uint32_t* ctr = p.row_cnt + (g * p.rpg + i) * kCounterStride;
+        const uint32_t prev = atomic_arrive(ctr);
+        if (prev == 1u) store_sc(ctr, 0u);
+        sh.u32s[6] = prev == 1u ? 1u : 0u;
+      }
+      __syncthreads();
+      draw_here = sh.u32s[6] != 0u;
+    }
+    if (draw_here) {
+      const int64_t tok = jr == k ? own_draw<DT>(p, sh, st, nslots, p.uniforms[g * p.rpg + 2 * k], rowp, bm)
+                                  : residual_draw<DT>(p, sh, g, i, jr < k);
+      if (t == 0) {
+        store_sc64(reinterpret_cast<uint64_t*>(p.draws) + g * (k + 1) + (jr == k ? k : i), static_cast<uint64_t>(tok));
+        drain_stores();
+        uint32_t* ctr = p.grp_cnt + g * kCounterStride;
+        const uint32_t prev = atomic_arrive(ctr);
+        const bool last = prev == static_cast<uint32_t>(k);
+        if (last) store_sc(ctr, 0u);
+        sh.u32s[7] = last ? 1u : 0u;
+      }
+      __syncthreads();
+      if (sh.u32s[7]) accept_chain(p, sh, g);
+    }
   } else if constexpr (MODE == kModeSample) {
-    const float u = p.row_uniforms[r];
-    int64_t token;
-    if (!(flags & kFlagDense)) {
-      const float mf = mass;
-      token = pick_lds(sh, n_sup, u, [&](int i) { return fx46(sh.cval[i] / mf); }, 0);
-    } else {
-      const float cc = cutoff;
-      const bool unf = unfiltered;
-      token = pick_dense(sh, p.vocab, u, [&](int i) {
-        const float x = xform_seen(xf, load_elem<DT>(rowp, i), xf.use_pen && bit_of(bm, i));
-        const float pe = chunk_p(x, sh.cm[i / kChunk], m, s);
-        return fx46(unf ? pe : (pe >= cc ? pe / mass : 0.0f));
-      });
-    }
+    const int64_t token = own_draw<DT>(p, sh, st, (flags & kFlagSlow) ? n_sup : nslots, p.row_uniforms[r], rowp, bm);
     if (t == 0) p.row_tokens[r] = token;
   } else {
     if (t == 0) {
-      RowStat st;
-      st.m = m;
-      st.s = s;
-      st.cutoff = cutoff;
-      st.mass = mass;
-      st.n_sup = 0;
-      st.flags = flags;
-      st.s_fx = s_fx;
-      st.mass_fx = mass_fx;
       p.stats[r] = st;
       if (p.cutoff_out) p.cutoff_out[r] = unfiltered ? 0.0f : cutoff;
-      if (p.mass_out) p.mass_out[r] = mass;
+      if (p.mass_out) p.mass_out[r] = st.mass;
     }
   }
 }
 
 // ===========================================================================
-// dense_kernel: p and the filtered distribution for one (row, chunk)
+// dense_kernel: p and the filtered distribution for one (row, chunk) item
 // ===========================================================================
 template <int DT>
 __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kCB * EPV);
   const int t = threadIdx.x;
-  const int cj = blockIdx.x;
-  const int64_t r = blockIdx.z;
+  const int item = blockIdx.x;
+  const int64_t r = item / p.nch;
+  const int cj = item - static_cast<int>(r) * p.nch;
   const char* rowp = row_of(p, r, 0);
   const int c0 = cj * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
   const u32x4* src = reinterpret_cast<const u32x4*>(rowp) + c0 / EPV;
   const RowStat st = p.stats[r];
-  const float mj = p.chunks[r * p.nch + cj].m;
-  const float f = ls_exp(mj - st.m);
-  const Xf xf = make_xf(p);
+  const float mc = p.chunks[r * p.nch + cj].mc;
+  const float gj = exp2q(mc - st.mcmax) / st.s;
   const bool unf = st.flags & kFlagUnfiltered;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
@@ -1082,10 +1196,9 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
       float pv[EPV], fv[EPV];
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
-        const float x = xform_seen(xf, vec_elem<DT>(d, e), false);
-        const float pe = (ls_exp(x - mj) * f) / st.s;
-        pv[e] = pe;
-        fv[e] = unf ? pe : (pe >= st.cutoff ? pe / st.mass : 0.0f);
+        const float x = exp2q(__builtin_fmaf(vec_elem<DT>(d, e), p.c, -mc)) * gj;
+        pv[e] = x;
+        fv[e] = unf ? x : (x >= st.cutoff ? x / st.mass : 0.0f);
       }
       const int64_t i = c0 + static_cast<int64_t>(v) * EPV;
 #pragma unroll
@@ -1101,25 +1214,27 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
 // Host side
 // ===========================================================================
 struct Layout {
-  uint64_t cnt, chunks, cands, stats, support, bitmap, total;
+  uint64_t row_cnt, grp_cnt, chunks, cands, stats, draws, bitmap, total;
 };
 
-// Workspace: [spec: arrival counters, one 64-byte line each, for up to
-// kMaxSpecBatch elements at a fixed place] [chunk records] [candidates]
-// [row stats] [spec: supports] [penalty bitmaps, one per group].
-Layout ws_layout(int64_t rows, int64_t groups, int nch, bool spec) {
+// Workspace: [pair arrival counters, one 64-byte line each, for up to
+// kMaxRows rows] [group counters for up to kMaxSpecBatch elements] (both at
+// fixed places, so calls of any shape find them zero) [chunk records]
+// [candidates] [row statistics] [draws] [penalty bitmaps, one per group].
+Layout ws_layout(int64_t rows, int64_t groups, int nch) {
   auto al = [](uint64_t x) { return (x + 255u) & ~255ull; };
   Layout l{};
-  l.cnt = 0;
-  uint64_t off = spec ? al(static_cast<uint64_t>(kMaxSpecBatch) * kCounterStride * 4u) : 0;
+  l.row_cnt = 0;
+  l.grp_cnt = al(static_cast<uint64_t>(kMaxRows) * kCounterStride * 4u);
+  uint64_t off = al(l.grp_cnt + static_cast<uint64_t>(kMaxSpecBatch) * kCounterStride * 4u);
   l.chunks = off;
   off = al(off + static_cast<uint64_t>(rows) * nch * sizeof(ChunkRec));
   l.cands = off;
   off = al(off + static_cast<uint64_t>(rows) * nch * kChunkCand * 8u);
   l.stats = off;
   off = al(off + static_cast<uint64_t>(rows) * sizeof(RowStat));
-  l.support = off;
-  if (spec) off = al(off + static_cast<uint64_t>(rows) * kSupCap * 8u);
+  l.draws = off;
+  off = al(off + static_cast<uint64_t>(rows) * 8u);
   l.bitmap = off;
   off = al(off + static_cast<uint64_t>(groups) * nch * (kChunk / 32) * 4u);
   l.total = off;
@@ -1128,47 +1243,48 @@ Layout ws_layout(int64_t rows, int64_t groups, int nch, bool spec) {
 
 void bind_workspace(SampParams& p, void* ws, const Layout& l) {
   char* b = static_cast<char*>(ws);
-  p.counters = reinterpret_cast<uint32_t*>(b + l.cnt);
+  p.row_cnt = reinterpret_cast<uint32_t*>(b + l.row_cnt);
+  p.grp_cnt = reinterpret_cast<uint32_t*>(b + l.grp_cnt);
   p.chunks = reinterpret_cast<ChunkRec*>(b + l.chunks);
   p.cands = reinterpret_cast<uint64_t*>(b + l.cands);
   p.stats = reinterpret_cast<RowStat*>(b + l.stats);
-  p.support = reinterpret_cast<uint64_t*>(b + l.support);
+  p.draws = reinterpret_cast<int64_t*>(b + l.draws);
   p.bitmap = reinterpret_cast<uint32_t*>(b + l.bitmap);
 }
 
 int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChunk); }
 
 template <int DT, int MODE>
-void launch_dt(const SampParams& p, int64_t groups, hipStream_t st) {
-  const unsigned gz = static_cast<unsigned>(groups);
-  if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(gz), dim3(kBmB), 0, st, p);
-  const int items = static_cast<int>(groups * p.rpg * p.nch);
+void launch_dt(const SampParams& p, int64_t groups, int64_t rows, hipStream_t st) {
+  if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(groups)), dim3(kBmB), 0, st, p);
   const int wgs = static_cast<int>(device_cu_count()) * kChunkWgsPerCu;
-  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(items < wgs ? items : wgs), dim3(kCB), 0, st, p, items);
-  hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(p.rpg, gz), dim3(kRB), 0, st, p);
+  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(p.items < wgs ? p.items : wgs), dim3(kCB), 0, st, p);
+  hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kCB), 0, st, p);
   if constexpr (MODE == kModeDense) {
-    hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.nch, 1, gz), dim3(kCB), 0, st, p);
+    hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.items), dim3(kCB), 0, st, p);
   }
 }
 
 template <int MODE>
-int launch_mode(const SampParams& p, int dtype, int64_t groups, hipStream_t st) {
+int launch_mode(const SampParams& p, int dtype, int64_t groups, int64_t rows, hipStream_t st) {
   switch (dtype) {
-    case LS_DTYPE_F32: launch_dt<F32, MODE>(p, groups, st); break;
-    case LS_DTYPE_BF16: launch_dt<BF16, MODE>(p, groups, st); break;
-    case LS_DTYPE_F16: launch_dt<F16, MODE>(p, groups, st); break;
+    case LS_DTYPE_F32: launch_dt<F32, MODE>(p, groups, rows, st); break;
+    case LS_DTYPE_BF16: launch_dt<BF16, MODE>(p, groups, rows, st); break;
+    case LS_DTYPE_F16: launch_dt<F16, MODE>(p, groups, rows, st); break;
     default: return fail(LS_ERR_VALUE, "unsupported logits dtype");
   }
   return check_launch("sampling kernel launch");
 }
 
 // Shared argument validation / setup for the processing options.
-int setup_common(SampParams& p, int dtype, int64_t vocab, float temperature, float top_p, int64_t top_k,
-                 float penalty, const int32_t* history, int64_t history_stride, const int32_t* history_len) {
+int setup_common(SampParams& p, int dtype, int64_t rows, int64_t vocab, float temperature, float top_p,
+                 int64_t top_k, float penalty, const int32_t* history, int64_t history_stride,
+                 const int32_t* history_len) {
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(LS_ERR_VALUE, "unsupported logits dtype");
   if (vocab <= 0 || vocab > kMaxVocab) return fail(LS_ERR_VALUE, "vocabulary size must be in [1, 262144]");
   if ((vocab * eb) % 16 != 0) return fail(LS_ERR_VALUE, "vocabulary row bytes must be a multiple of 16");
+  if (rows > kMaxRows) return fail(LS_ERR_VALUE, "at most 65536 logit rows per call");
   if (!(temperature > 0.0f)) return fail(LS_ERR_VALUE, "temperature must be > 0");
   if (!(top_p > 0.0f) || top_p > 1.0f) return fail(LS_ERR_VALUE, "top_p must be in (0, 1]");
   if (top_k != 0 && top_k < vocab) return fail(LS_ERR_VALUE, "top_k filtering is not supported by this entry point");
@@ -1177,10 +1293,12 @@ int setup_common(SampParams& p, int dtype, int64_t vocab, float temperature, flo
     return fail(LS_ERR_VALUE, "repetition penalty needs a token history");
   p.vocab = static_cast<int>(vocab);
   p.nch = nch_for(vocab);
-  p.chunk_cap = kRowCand / p.nch < kChunkCand ? kRowCand / p.nch : kChunkCand;
+  p.cap_log2 = p.nch <= kRowCand / kChunkCand ? 8 : (p.nch <= 2 * kRowCand / kChunkCand ? 7 : 6);
+  p.cap = 1 << p.cap_log2;  // nch * cap <= kRowCand
   p.bm_words = p.nch * (kChunk / 32);
-  p.use_t = temperature != 1.0f;
-  p.inv_t = 1.0f / temperature;
+  p.items = static_cast<int>(rows * p.nch);
+  const float inv_t = 1.0f / temperature;
+  p.c = kLog2e * inv_t;
   p.use_pen = penalty != 1.0f;
   p.pen = penalty;
   p.inv_pen = 1.0f / penalty;
@@ -1200,7 +1318,7 @@ extern "C" {
 
 uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab) {
   if (batch <= 0 || k < 1 || vocab <= 0) return 0;
-  return ws_layout(batch * (2 * k + 1), batch, nch_for(vocab), true).total;
+  return ws_layout(batch * (2 * k + 1), batch, nch_for(vocab)).total;
 }
 
 int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64_t target_pos_stride,
@@ -1215,7 +1333,9 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64
   if (!target_logits || !draft_logits || !draft_tokens || !uniforms || !accept_len || !tokens)
     return fail(LS_ERR_VALUE, "spec_verify: NULL pointer");
   SampParams p{};
-  int rc = setup_common(p, dtype, vocab, temperature, top_p, top_k, penalty, history, history_stride, history_len);
+  const int64_t rows = batch * (2 * k + 1);
+  int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, penalty, history, history_stride,
+                        history_len);
   if (rc) return rc;
   const int eb = dtype_bytes(dtype);
   p.base0 = static_cast<const char*>(target_logits);
@@ -1233,26 +1353,27 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64
   p.uniforms = uniforms;
   p.accept_len = accept_len;
   p.tokens = tokens;
-  const Layout l = ws_layout(batch * p.rpg, batch, p.nch, true);
+  const Layout l = ws_layout(rows, batch, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "spec_verify: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeSpec>(p, dtype, batch, static_cast<hipStream_t>(stream));
+  return launch_mode<kModeSpec>(p, dtype, batch, rows, static_cast<hipStream_t>(stream));
 }
 
 uint64_t ls_sample_logits_workspace(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
-  return ws_layout(rows, rows, nch_for(vocab), false).total;
+  return ws_layout(rows, rows, nch_for(vocab)).total;
 }
 
 int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows, int64_t vocab,
                      float temperature, float top_p, int64_t top_k, float penalty, const int32_t* history,
                      int64_t history_stride, const int32_t* history_len, const float* uniforms,
                      int64_t* out_tokens, void* workspace, uint64_t ws_bytes, ls_stream_t stream) {
-  if (rows < 0 || rows > kMaxGridYZ) return fail(LS_ERR_VALUE, "sample_logits: need 0 <= rows <= 65535");
+  if (rows < 0 || rows > kMaxRows) return fail(LS_ERR_VALUE, "sample_logits: need 0 <= rows <= 65536");
   if (rows == 0) return LS_OK;
   if (!logits || !uniforms || !out_tokens) return fail(LS_ERR_VALUE, "sample_logits: NULL pointer");
   SampParams p{};
-  int rc = setup_common(p, dtype, vocab, temperature, top_p, top_k, penalty, history, history_stride, history_len);
+  int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, penalty, history, history_stride,
+                        history_len);
   if (rc) return rc;
   const int eb = dtype_bytes(dtype);
   p.base0 = static_cast<const char*>(logits);
@@ -1262,26 +1383,26 @@ int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   p.k = 0;
   p.row_uniforms = uniforms;
   p.row_tokens = out_tokens;
-  const Layout l = ws_layout(rows, rows, p.nch, false);
+  const Layout l = ws_layout(rows, rows, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "sample_logits: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeSample>(p, dtype, rows, static_cast<hipStream_t>(stream));
+  return launch_mode<kModeSample>(p, dtype, rows, rows, static_cast<hipStream_t>(stream));
 }
 
 uint64_t ls_filter_logits_workspace(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
-  return ws_layout(rows, rows, nch_for(vocab), false).total;
+  return ws_layout(rows, rows, nch_for(vocab)).total;
 }
 
 int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows, int64_t vocab,
                      float temperature, float top_p, const float* top_p_rows, int64_t top_k, float* probs_out,
                      int64_t probs_stride, float* filtered_out, int64_t filtered_stride, float* cutoff_out,
                      float* mass_out, void* workspace, uint64_t ws_bytes, ls_stream_t stream) {
-  if (rows < 0 || rows > kMaxGridYZ) return fail(LS_ERR_VALUE, "filter_logits: need 0 <= rows <= 65535");
+  if (rows < 0 || rows > kMaxRows) return fail(LS_ERR_VALUE, "filter_logits: need 0 <= rows <= 65536");
   if (rows == 0) return LS_OK;
   if (!logits) return fail(LS_ERR_VALUE, "filter_logits: NULL logits");
   SampParams p{};
-  int rc = setup_common(p, dtype, vocab, temperature, top_p, top_k, 1.0f, nullptr, 0, nullptr);
+  int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, 1.0f, nullptr, 0, nullptr);
   if (rc) return rc;
   const int eb = dtype_bytes(dtype);
   p.base0 = static_cast<const char*>(logits);
@@ -1296,10 +1417,10 @@ int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   p.filt_stride = filtered_stride;
   p.cutoff_out = cutoff_out;
   p.mass_out = mass_out;
-  const Layout l = ws_layout(rows, rows, p.nch, false);
+  const Layout l = ws_layout(rows, rows, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "filter_logits: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeDense>(p, dtype, rows, static_cast<hipStream_t>(stream));
+  return launch_mode<kModeDense>(p, dtype, rows, rows, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -5,18 +5,20 @@ torch CUDA cumsum and Triton tl.sum trees, none of which can be reproduced on
 another machine. The kernels and this oracle therefore share one declared
 arithmetic, made of operations that are exactly reproducible on both sides:
 
-* IEEE binary32 +, -, *, / and sqrt with round-to-nearest-even, and fused
-  multiply-add with a single rounding (``fma32`` emulates it exactly here);
-* ``ls_exp``: an exponential built only from those operations (Cody-Waite
-  range reduction, a degree-6 polynomial for e^r, exact scaling by 2^k);
+* IEEE binary32 +, -, *, / with round-to-nearest-even, and fused multiply-add
+  with a single rounding (``fma32`` emulates it exactly here);
+* ``exp2q``: 2^t built only from those operations (rint reduction, a
+  degree-5 polynomial for 2^r on [-1/2, 1/2], exact scaling by 2^k);
+* ``tree_sum_f32``: a binary32 sum in a fixed pairwise order;
 * masses as exact integers: a weight w in [0, 1] contributes
   ``fx46(w) = floor(w * 2^46)``; sums of these are exact, so every reduction
   order gives the same result, and comparisons with u * total are exact;
 * ``u64_to_f32``: round-to-nearest-even conversion of an exact integer mass.
 
 Pinned by: tests/test_oracle_numerics.py (fma32 against exact rationals on
-random and constructed midpoint cases; ls_exp within 2 ulp of math.exp over its
-whole domain; fx46 and u64_to_f32 against Fraction arithmetic).
+random and constructed midpoint cases; exp2q within 4 ulp of 2^t over its
+domain with its special points; tree_sum_f32 against an explicit recursive
+pairwise sum; fx46 and u64_to_f32 against Fraction arithmetic).
 """
 
 from __future__ import annotations
@@ -29,17 +31,18 @@ F64 = np.float64
 FX_BITS = 46
 FX_ONE = 1 << FX_BITS
 
-# ls_exp constants (binary32). LN2_HI has 16 significant bits so k*LN2_HI is
-# exact for |k| <= 256; LN2_LO = ln 2 - LN2_HI rounded to binary32.
+# log2(e) rounded to binary32: the scale of the processed logits is
+# c = RN(LOG2E * RN(1/T)), so that 2^(c * x) = e^(x / T).
 LOG2E = F32(1.44269504)
-LN2_HI = F32(0.693145752)
-LN2_LO = F32(1.42860677e-06)
-EXP_MIN = F32(-87.0)
-# e^r on [-0.35, 0.35], relative-error fit, coefficients rounded to binary32.
-EXP_COEFFS = tuple(F32(c) for c in (
-    1.0, 1.0, 0.4999999403953552, 0.1666642129421234,
-    0.041668057441711426, 0.00837495643645525, 0.0013842721236869693,
+# exp2q: arguments are clamped at EXP2_FLOOR (NaN too), where 2^t is 0 in binary32.
+EXP2_FLOOR = F32(-200.0)
+# 2^r on [-1/2, 1/2], relative-error fit, coefficients rounded to binary32;
+# the constant term is exactly 1, so exp2q(0) == 1.
+EXP2_COEFFS = tuple(F32(float.fromhex(h)) for h in (
+    "0x1.0p+0", "0x1.62e428p-1", "0x1.ebf918p-3", "0x1.c6b6e4p-5", "0x1.3d0c54p-7", "0x1.5c08e4p-10",
 ))
+# Upper bound of the polynomial over [-1/2, 1/2] (attained near r = 1/2).
+EXP2_POLY_MAX = 1.4142136
 
 
 def f32(x) -> np.ndarray:
@@ -72,29 +75,40 @@ def fma32(a, b, c) -> np.ndarray:
     return np.where(move, nb, r).astype(F32)
 
 
-def ls_exp_k(t):
-    """Return (e, k) where e = ls_exp(t) and k the binary exponent used in scaling.
+def exp2q_k(t):
+    """Return (e, k): e = exp2q(t) = P(t - k) * 2^k with k = rint(max(t, -200)).
 
-    t is binary32 (normally t = x - max(x) <= 0). k = rint(t * LOG2E) with the
-    product rounded to binary32 first; r = t - k*ln2 in two fused steps;
-    e = P(r) * 2^k. Inputs below EXP_MIN (and NaN) give exactly 0.
+    t is binary32 (normally t <= 0). NaN and t <= -200 give e = 0 (the scaling
+    underflows); k is returned as int32.
     """
     t = np.asarray(t, dtype=F32)
-    with np.errstate(invalid="ignore", over="ignore"):
-        kf = np.rint((t * LOG2E).astype(F32)).astype(F32)
-        kf_safe = np.where(np.isfinite(kf), kf, F32(0)).astype(F32)
-        r = fma32(kf_safe, -LN2_HI, t)
-        r = fma32(kf_safe, -LN2_LO, r)
-        p = np.full_like(t, EXP_COEFFS[6])
-        for coef in EXP_COEFFS[5::-1]:
+    with np.errstate(invalid="ignore", over="ignore", under="ignore"):
+        tc = np.fmax(t, EXP2_FLOOR).astype(F32)
+        kf = np.rint(tc).astype(F32)
+        r = (tc - kf).astype(F32)  # exact
+        p = np.full_like(tc, EXP2_COEFFS[5])
+        for coef in EXP2_COEFFS[4::-1]:
             p = fma32(p, r, coef)
-        e = np.ldexp(p, kf_safe.astype(np.int32)).astype(F32)
-        keep = t >= EXP_MIN
-    return np.where(keep, e, F32(0)).astype(F32), np.where(keep, kf_safe, F32(0)).astype(F32)
+        k = kf.astype(np.int32)
+        e = np.ldexp(p, k).astype(F32)
+    return e, k
 
 
-def ls_exp(t) -> np.ndarray:
-    return ls_exp_k(t)[0]
+def exp2q(t) -> np.ndarray:
+    return exp2q_k(t)[0]
+
+
+def tree_sum_f32(a) -> np.ndarray:
+    """Binary32 pairwise sum along the last axis (length a power of two):
+    adjacent pairs (0,1), (2,3), ... first, then pairs of those, and so on."""
+    a = np.asarray(a, dtype=F32)
+    n = a.shape[-1]
+    if n & (n - 1):
+        raise ValueError("tree_sum_f32 needs a power-of-two length")
+    with np.errstate(invalid="ignore", over="ignore"):
+        while a.shape[-1] > 1:
+            a = (a[..., 0::2] + a[..., 1::2]).astype(F32)
+    return a[..., 0]
 
 
 def fx46(w) -> np.ndarray:

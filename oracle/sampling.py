@@ -27,7 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from .numerics import (
-    F32, F64, FX_BITS, fx46, floor_u_times, ls_exp, mass_to_f32,
+    F32, F64, FX_BITS, LOG2E, exp2q, exp2q_k, fx46, floor_u_times, mass_to_f32, tree_sum_f32,
 )
 
 
@@ -56,66 +56,119 @@ def apply_penalty(x: np.ndarray, history, penalty: float) -> np.ndarray:
     return x
 
 
-def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float = 1.0, history=None) -> np.ndarray:
-    """x = penalised logits scaled by RN(1/T) (distributions.py:44-48).
+@dataclass
+class Processed:
+    """Processed logits of one row: x = penalised logits, c = the binary32
+    scale RN(LOG2E * RN(1/T)) applied inside the exponential, epv = elements
+    per 16-byte vector of the logits' storage type (4 for float32, 8 for
+    bfloat16 / float16), which fixes the summation order of the chunk masses."""
+    x: np.ndarray
+    c: np.float32
+    epv: int = 4
 
-    The reference divides float32 logits by the Python temperature; on the GPU
-    that is a multiplication by the binary32 reciprocal. T == 1 leaves the
-    logits untouched, as the reference's temperature == 1 branch does.
+
+def scale_of(temperature: float) -> np.float32:
+    """c = RN(LOG2E * RN(1/T)); T == 1 gives LOG2E."""
+    return F32(LOG2E * inv_f32(temperature))
+
+
+def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float = 1.0, history=None,
+                   epv: int = 4) -> Processed:
+    """Penalised logits and the temperature scale (distributions.py:44-48).
+
+    The reference divides float32 logits by the temperature and takes
+    softmax; here the temperature enters as the scale c of the base-2
+    exponent (2^(c x) = e^(x / T)), so T == 1 and T != 1 share one path.
     """
     x = np.asarray(logits, dtype=F32).copy()
     x = apply_penalty(x, history, penalty)
-    if temperature != 1.0:
-        x = (x * inv_f32(temperature)).astype(F32)
-    return x
+    return Processed(x, scale_of(temperature), epv)
 
 
 CHUNK = 8192  # elements per softmax chunk (a constant of the declared arithmetic)
+LANES = 256   # lanes per chunk in the mass summation order
+SCALE_SLOTS = 32  # chunks per row at most; the normaliser sums this many slots
 
 
 @dataclass
 class RowSoftmax:
-    x: np.ndarray      # processed logits
-    m: np.float32      # row max
-    e: np.ndarray      # ls_exp(x - m_chunk), chunk-relative
-    m_chunks: np.ndarray   # per-chunk max
-    f_chunks: np.ndarray   # ls_exp(m_chunk - m)
-    mass_chunks: list      # exact chunk masses sum fx46(e)
-    s_fx: int          # exact normaliser mass T
-    s: np.float32      # binary32 normaliser
-    w: np.ndarray      # RN(e * f_chunk)
-    p: np.ndarray      # probabilities RN(w / s)
+    x: np.ndarray      # penalised logits
+    c: np.float32      # exponent scale
+    m: np.float32      # row max of the scaled chunk maxima, max_j mc_j
+    e: np.ndarray      # exp2q(fma(x, c, -mc_j)), chunk-relative
+    m_chunks: np.ndarray   # per-chunk max of x
+    mc_chunks: np.ndarray  # RN(m_j * c)
+    f_chunks: np.ndarray   # exp2q(RN(mc_j - m))
+    mass_chunks: np.ndarray  # chunk masses M_j (binary32, fixed summation order)
+    s: np.float32      # normaliser S
+    g_chunks: np.ndarray   # RN(f_j / S)
+    p: np.ndarray      # probabilities RN(e_i * g_j)
 
 
-def softmax_row(x: np.ndarray) -> RowSoftmax:
-    """softmax(x) in the declared chunked arithmetic (distributions.py:44-48).
+def chunk_mass(e_chunk: np.ndarray, epv: int) -> np.float32:
+    """M_j of one chunk of CHUNK e-values (zero padded past the vocabulary).
 
-    The row is cut into chunks of CHUNK elements. Chunk j: m_j = max x,
-    e_i = ls_exp(x_i - m_j), M_j = sum fx46(e_i) (exact). Row: m = max m_j,
-    f_j = ls_exp(m_j - m), T = sum_j floor(f_j * M_j) (exact), S = RN32(T) 2^-46,
-    w_i = RN(e_i * f_j), p_i = RN(w_i / S). For rows of at most CHUNK elements
-    this is e_i = ls_exp(x_i - m), p_i = RN(e_i / S). Every chunk can be
-    processed on its own before the row-wide values are known, which is what
-    lets the kernels read the logits once with many workgroups per row.
+    Summation order: the chunk is read as 16-byte vectors of epv elements;
+    lane t of LANES owns vectors u * LANES + t (u = 0, 1, ...); each lane sums
+    its 32 elements pairwise in (u, element) order, then the lane sums are
+    summed pairwise in lane order.
     """
+    nvc = CHUNK // (LANES * epv)
+    lanes = np.asarray(e_chunk, dtype=F32).reshape(nvc, LANES, epv).transpose(1, 0, 2).reshape(LANES, nvc * epv)
+    return F32(tree_sum_f32(tree_sum_f32(lanes)))
+
+
+def softmax_row(x, c=None, epv: int = 4) -> RowSoftmax:
+    """softmax(x / T) in the declared chunked arithmetic (distributions.py:44-48).
+
+    x is a Processed row (or raw logits with T = 1). The row is cut into chunks
+    of CHUNK elements. Chunk j: m_j = max x, mc_j = RN(m_j c),
+    e_i = exp2q(fma(x_i, c, -mc_j)), M_j = chunk_mass(e). Row: m = max mc_j,
+    f_j = exp2q(RN(mc_j - m)), S = pairwise sum over SCALE_SLOTS slots of
+    RN(f_j M_j) (zero past the last chunk), g_j = RN(f_j / S),
+    p_i = RN(e_i g_j). Every chunk can be processed on its own before the
+    row-wide values are known, which is what lets the kernels read the logits
+    once with many workgroups per row.
+    """
+    if isinstance(x, Processed):
+        x, c, epv = x.x, x.c, x.epv
+    c = LOG2E if c is None else F32(c)
     x = np.asarray(x, dtype=F32)
     v = len(x)
     nch = -(-v // CHUNK)
-    with np.errstate(invalid="ignore"):
-        m_chunks = np.array([np.max(x[j * CHUNK:(j + 1) * CHUNK]) for j in range(nch)], dtype=F32)
-    m = F32(np.max(m_chunks))
-    cidx = np.arange(v) // CHUNK
-    with np.errstate(invalid="ignore"):
-        t = (x - m_chunks[cidx]).astype(F32)
-    e = ls_exp(t)
-    mass_chunks = [int(fx46(e[j * CHUNK:(j + 1) * CHUNK]).sum(dtype=np.uint64)) for j in range(nch)]
-    with np.errstate(invalid="ignore"):
-        f_chunks = ls_exp((m_chunks - m).astype(F32))
-    s_fx = sum(floor_u_times(f_chunks[j], mass_chunks[j]) for j in range(nch))
-    s = mass_to_f32(s_fx)
-    w = (e * f_chunks[cidx]).astype(F32)
-    p = (w / s).astype(F32)
-    return RowSoftmax(x, m, e, m_chunks, f_chunks, mass_chunks, s_fx, s, w, p)
+    if nch > SCALE_SLOTS:
+        raise ValueError("vocabulary larger than SCALE_SLOTS chunks")
+    xp = np.full(nch * CHUNK, -np.inf, dtype=F32)
+    xp[:v] = x
+    xc = xp.reshape(nch, CHUNK)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m_chunks = np.max(xc, axis=1).astype(F32)
+        mc = (m_chunks * c).astype(F32)
+        t = _fma_rows(xc, c, (-mc).astype(F32))
+        e = exp2q(t)
+        mass = np.array([chunk_mass(e[j], epv) for j in range(nch)], dtype=F32)
+        m = F32(np.max(mc))
+        f = exp2q((mc - m).astype(F32))
+        fm = np.zeros(SCALE_SLOTS, dtype=F32)
+        fm[:nch] = (f * mass).astype(F32)
+        s = F32(tree_sum_f32(fm))
+        g = (f / s).astype(F32)
+        p = (e * g[:, None]).astype(F32).reshape(-1)[:v]
+    return RowSoftmax(x, c, m, e.reshape(-1)[:v], m_chunks, mc, f, mass, s, g, p)
+
+
+def _fma_rows(xc: np.ndarray, c: np.float32, nmc: np.ndarray) -> np.ndarray:
+    from .numerics import fma32
+    return fma32(xc, np.full_like(xc, c), np.broadcast_to(nmc[:, None], xc.shape))
+
+
+def p_at(soft: RowSoftmax, idx: int) -> np.float32:
+    """p of one element recomputed from its logit (what the kernels do for a
+    single token): RN(exp2q(fma(x, c, -mc_j)) * g_j)."""
+    from .numerics import fma32
+    j = idx // CHUNK
+    t = fma32(soft.x[idx], soft.c, -soft.mc_chunks[j])
+    return F32(exp2q(t) * soft.g_chunks[j])
 
 
 def threshold_fx(top_p: float) -> int:
@@ -172,18 +225,19 @@ class FilteredRow:
     filtered: bool
 
 
-def filter_row(x: np.ndarray, top_p: float, top_k: int = 0) -> FilteredRow:
+def filter_row(x, top_p: float, top_k: int = 0) -> FilteredRow:
     """filtered_probabilities for one processed-logit row (distributions.py:14-86).
 
     top_k == 0 (or >= V) and top_p == 1: the unfiltered softmax, returned as is.
     top-p only: cutoff from top_p_cutoff. Both: cutoff = max(k-th value, top-p
     cutoff), renormalised once. top-k only: p >= k-th value (parity unpinned).
+    x is a Processed row or raw logits (T = 1).
     """
     soft = softmax_row(x)
     v = len(soft.p)
     eff_k = 0 if top_k >= v else top_k
     if eff_k == 0 and top_p >= 1.0:
-        return FilteredRow(soft, F32(np.min(soft.p)), soft.s_fx, soft.p, False)
+        return FilteredRow(soft, F32(np.min(soft.p)), int(fx46(soft.p).sum(dtype=np.uint64)), soft.p, False)
     if eff_k == 0:
         c, mass = top_p_cutoff(soft.p, top_p)
     elif top_p >= 1.0:
@@ -250,12 +304,12 @@ class SpecResult:
     tokens: np.ndarray       # int64 [B, k+1], -1 padded
     cutoffs: np.ndarray      # float32 [B, 2k+1] per-row cutoff (target rows then draft rows)
     masses: np.ndarray       # uint64 [B, 2k+1] retained masses
-    maxes: np.ndarray        # float32 [B, 2k+1]
-    norms: np.ndarray        # uint64 [B, 2k+1] exact softmax masses
+    maxes: np.ndarray        # float32 [B, 2k+1] row max of the scaled chunk maxima
+    norms: np.ndarray        # float32 [B, 2k+1] normalisers S
 
 
 def speculative_verify(target_logits, draft_logits, draft_tokens, uniforms, temperature=1.0,
-                       top_p=1.0, penalty=1.0, histories=None, top_k=0) -> SpecResult:
+                       top_p=1.0, penalty=1.0, histories=None, top_k=0, epv=4) -> SpecResult:
     """Lossless speculative verification over a chain of k draft positions.
 
     Per position i the reference's q1 rule (sampler.py:428-460): accept the
@@ -268,7 +322,8 @@ def speculative_verify(target_logits, draft_logits, draft_tokens, uniforms, temp
     Positions after a rejection are discarded (pipeline.py:379-412).
 
     target_logits [B, k+1, V], draft_logits [B, k, V] (any float dtype, taken
-    as binary32), draft_tokens int64 [B, k], uniforms float32 [B, 2k+1].
+    as binary32), draft_tokens int64 [B, k], uniforms float32 [B, 2k+1];
+    epv = 4 for float32 logits, 8 for bfloat16 / float16 (see Processed).
     """
     t = np.asarray(target_logits, dtype=F32)
     d = np.asarray(draft_logits, dtype=F32)
@@ -281,13 +336,15 @@ def speculative_verify(target_logits, draft_logits, draft_tokens, uniforms, temp
     cut = np.zeros((b_n, 2 * k + 1), dtype=F32)
     mas = np.zeros((b_n, 2 * k + 1), dtype=np.uint64)
     mx = np.zeros((b_n, 2 * k + 1), dtype=F32)
-    nrm = np.zeros((b_n, 2 * k + 1), dtype=np.uint64)
+    nrm = np.zeros((b_n, 2 * k + 1), dtype=F32)
     for b in range(b_n):
         hist = None if histories is None else histories[b]
-        rows_t = [filter_row(process_logits(t[b, i], temperature, penalty, hist), top_p, top_k) for i in range(kp1)]
-        rows_d = [filter_row(process_logits(d[b, i], temperature, penalty, hist), top_p, top_k) for i in range(k)]
+        rows_t = [filter_row(process_logits(t[b, i], temperature, penalty, hist, epv), top_p, top_k)
+                  for i in range(kp1)]
+        rows_d = [filter_row(process_logits(d[b, i], temperature, penalty, hist, epv), top_p, top_k)
+                  for i in range(k)]
         for j, r in enumerate(rows_t + rows_d):
-            cut[b, j], mas[b, j], mx[b, j], nrm[b, j] = r.cutoff, r.mass_fx, r.soft.m, r.soft.s_fx
+            cut[b, j], mas[b, j], mx[b, j], nrm[b, j] = r.cutoff, r.mass_fx, r.soft.m, r.soft.s
         a = 0
         while a < k:
             x = int(xs[b, a])
@@ -308,13 +365,14 @@ def speculative_verify(target_logits, draft_logits, draft_tokens, uniforms, temp
 # Drop-in level restatements (dense rows), used by the sampler API tests.
 # ---------------------------------------------------------------------------
 
-def filtered_probabilities(logits: np.ndarray, temperature: float, top_k: int, top_p, top_p_thresholds=None):
+def filtered_probabilities(logits: np.ndarray, temperature: float, top_k: int, top_p, top_p_thresholds=None,
+                           epv: int = 4):
     """distributions.py:14-86 over [B, V]; per-row thresholds optional."""
     logits = np.asarray(logits, dtype=F32)
     out = np.zeros_like(logits)
     for b in range(logits.shape[0]):
         tp = float(top_p_thresholds[b]) if top_p_thresholds is not None and top_p < 1 else top_p
-        out[b] = filter_row(process_logits(logits[b], temperature), tp, top_k).P
+        out[b] = filter_row(process_logits(logits[b], temperature, epv=epv), tp, top_k).P
     return out
 
 
@@ -392,4 +450,4 @@ def rejection_run(first, target, second, token: int, has_second: bool, u0: float
     return (int(token) if a else sampled, int(a), int(has_second and not a))
 
 
-__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "ls_exp", "CHUNK"]
+__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "exp2q", "CHUNK"]

@@ -107,7 +107,7 @@ def test_prepare_and_sample_top_p(gpu, indirect):
     probs = ctx[0].cpu().numpy()
     cut = ctx[1].cpu().numpy()[:, 0]
     for r in range(rows):
-        want = osmp.filter_row(logits[r].float().numpy(), float(thr[r, 0]))
+        want = osmp.filter_row(osmp.process_logits(logits[r].float().numpy(), epv=8), float(thr[r, 0]))
         assert np.array_equal(probs[r], want.soft.p)
         assert cut[r] == want.cutoff
         assert np.array_equal(normalized[r].cpu().numpy(), want.P)
@@ -215,7 +215,7 @@ def test_filtered_probabilities_plain(gpu, temperature, top_p):
     logits = (torch.randn(rows, vocab, generator=torch.Generator().manual_seed(2)) * 4).to(torch.bfloat16)
     out = dist.filtered_probabilities(logits.to(gpu), temperature, 0, top_p).cpu().numpy()
     for r in range(rows):
-        want = osmp.filter_row(osmp.process_logits(logits[r].float().numpy(), temperature), top_p)
+        want = osmp.filter_row(osmp.process_logits(logits[r].float().numpy(), temperature, epv=8), top_p)
         assert np.array_equal(out[r], want.P)
 
 

@@ -52,21 +52,51 @@ def test_fma32_midpoint_cases():
     assert naive != np.float32(1 + 2 ** -11 + 2 ** -23)
 
 
-def test_exp_accuracy_and_special_points():
+def test_exp2_accuracy_and_special_points():
     rng = np.random.default_rng(1)
     t = np.concatenate([
-        -rng.random(200000).astype(np.float32) * 87,
-        -rng.random(20000).astype(np.float32) * 0.5,
-        np.float32([0.0, -0.0, -1e-30, -0.3466, -0.34657359, -86.999, -87.0]),
+        -rng.random(200000).astype(np.float32) * 126,
+        -rng.random(50000).astype(np.float32) * 2,
+        np.float32([0.0, -0.0, -1e-30, -0.5, -1.5, -2.5, -0.49999997, -125.5, -126.0]),
     ]).astype(np.float32)
-    e = nm.ls_exp(t)
-    ref = np.exp(t.astype(np.float64))
+    e, k = nm.exp2q_k(t)
+    ref = np.exp2(t.astype(np.float64))
     ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
     err = np.abs(e.astype(np.float64) - ref) / ulp
-    assert err.max() <= 2.0, err.max()
-    assert nm.ls_exp(np.float32([0.0]))[0] == np.float32(1.0)
-    assert (nm.ls_exp(np.float32([-87.01, -1e30, -np.inf, np.nan])) == 0).all()
-    assert (nm.ls_exp(t) > 0).all()  # every result in the domain is a normal number
+    assert err.max() <= 4.0, err.max()
+    # k is the rounded argument (half to even) and e / 2^k is the polynomial's range
+    assert np.array_equal(k, np.rint(t).astype(np.int32))
+    scaled = np.ldexp(e.astype(np.float64), -k)
+    assert scaled.min() >= 2 ** -0.5 * (1 - 1e-6) and scaled.max() <= nm.EXP2_POLY_MAX
+    # integers are exact powers of two; the floor, -inf and NaN give 0
+    ints = -np.arange(0, 127, dtype=np.float32)
+    assert np.array_equal(nm.exp2q(ints), np.ldexp(np.float32(1), ints.astype(np.int32)).astype(np.float32))
+    assert (nm.exp2q(np.float32([-200.0, -1e30, -np.inf, np.nan])) == 0).all()
+    assert nm.exp2q(np.float32([-149.0]))[0] == np.float32(2.0 ** -149)  # denormals keep their exact value
+    # e^(x/T) = 2^(c x): the temperature scale agrees with the natural exponential
+    x = (rng.standard_normal(10000) * 3).astype(np.float32)
+    c = np.float32(nm.LOG2E * (np.float32(1) / np.float32(0.7)))
+    got = nm.exp2q(nm.fma32(x, c, np.float32(0)))
+    want = np.exp(x.astype(np.float64) / 0.7)
+    assert np.max(np.abs(got / want - 1)) < 3e-6
+
+
+def test_tree_sum_order():
+    rng = np.random.default_rng(5)
+
+    def pairwise(v):
+        if len(v) == 1:
+            return np.float32(v[0])
+        h = len(v) // 2
+        return np.float32(pairwise(v[:h]) + pairwise(v[h:]))
+
+    for n in (1, 2, 8, 32, 256):
+        a = (rng.random(n) * 10.0 ** rng.integers(-8, 3, n)).astype(np.float32)
+        assert nm.tree_sum_f32(a) == pairwise(list(a))
+    # the order is observable: 1 + 2^-24 + 2^-24 depends on the grouping
+    tiny = np.float32(2.0 ** -24)
+    assert nm.tree_sum_f32(np.float32([1, tiny, tiny, 0])) == np.float32(1)
+    assert nm.tree_sum_f32(np.float32([1, 0, tiny, tiny])) == np.float32(1 + 2.0 ** -23)
 
 
 def test_fixed_point_and_conversions():

@@ -26,18 +26,41 @@ def test_softmax_matches_torch():
         assert np.max(np.abs(soft.p[big] - ref32[big]) / ref32[big]) < 1e-5  # the contract tolerance
 
 
+def test_chunk_mass_order():
+    # M_j sums each lane's 32 elements pairwise, lane t owning 16-byte vectors
+    # u * 256 + t; placing two 2^-24 next to a 1 in one pairwise group loses
+    # them (ties to even), placing them in a group of their own keeps 2^-23.
+    tiny = np.float32(2.0 ** -24)
+    for epv in (4, 8):
+        e = np.zeros(os_.CHUNK, np.float32)
+        e[0], e[1], e[2] = 1, tiny, tiny          # lane 0: (1 + t) + (t + 0) -> 1
+        assert os_.chunk_mass(e, epv) == np.float32(1)
+        e = np.zeros(os_.CHUNK, np.float32)
+        e[0], e[epv], e[epv + 1] = 1, tiny, tiny  # the tiny pair is lane 1's first vector
+        assert os_.chunk_mass(e, epv) == np.float32(1 + 2.0 ** -23)
+    # Elements 1024 and 1028: with epv = 4 they are the second vectors of
+    # lanes 0 and 1 (each tiny meets the 1 on its own and is lost); with epv = 8
+    # both sit in lane 128's first vector and add up first.
+    e = np.zeros(os_.CHUNK, np.float32)
+    e[0], e[1024], e[1028] = 1, tiny, tiny
+    assert os_.chunk_mass(e, 4) == np.float32(1)
+    assert os_.chunk_mass(e, 8) == np.float32(1 + 2.0 ** -23)
+
+
 def test_chunked_softmax_closed_forms():
     c = os_.CHUNK
-    # A row no longer than one chunk is the plain formula e = ls_exp(x - m), p = RN(e / S).
-    x = (np.random.default_rng(1).standard_normal(c) * 3).astype(np.float32)
-    soft = os_.softmax_row(x)
-    e = nm.ls_exp((x - x.max()).astype(np.float32))
-    s = nm.mass_to_f32(int(nm.fx46(e).sum(dtype=np.uint64)))
-    assert np.array_equal(soft.p, (e / s).astype(np.float32))
-    # A constant row of n chunks: every e = 1, every f = 1, p = RN(1 / RN32(V)).
+    # A zero row of 3 chunks + 5: every e = 1, M = (8192, 8192, 8192, 5),
+    # S = V exactly, p = RN(1 / V).
     v = 3 * c + 5
-    soft = os_.softmax_row(np.full(v, 2.5, np.float32))
-    assert soft.s_fx == v << 46 and np.all(soft.p == np.float32(1) / np.float32(v))
+    soft = os_.softmax_row(np.zeros(v, np.float32))
+    assert np.array_equal(soft.mass_chunks, np.float32([c, c, c, 5])) and soft.s == np.float32(v)
+    assert np.all(soft.p == np.float32(1) / np.float32(v))
+    # Zeros next to a maximum whose scaled value rounds to 1: t = -1 exactly,
+    # so their e is exactly 1/2.
+    x = np.zeros(c, np.float32)
+    x[0] = np.float32(1.0) / nm.LOG2E
+    soft = os_.softmax_row(x)
+    assert soft.mc_chunks[0] == 1 and soft.e[0] == 1 and np.all(soft.e[1:] == np.float32(0.5))
     # A chunk of -inf contributes nothing and the others are unaffected; the
     # maximum may sit in any chunk.
     x = (np.random.default_rng(2).standard_normal(3 * c) * 2).astype(np.float32)
@@ -49,19 +72,34 @@ def test_chunked_softmax_closed_forms():
     ref = torch.softmax(torch.from_numpy(x).double(), -1).numpy()
     big = ref > 1e-30
     assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 3e-6
-    # The normaliser is the exact sum of the chunk masses scaled by f_j.
-    assert soft.s_fx == sum(nm.floor_u_times(soft.f_chunks[j], soft.mass_chunks[j]) for j in range(3))
+    # The normaliser is sum_j f_j M_j to binary32 accuracy, and p sums to 1.
+    s64 = sum(float(soft.f_chunks[j]) * float(soft.mass_chunks[j]) for j in range(3))
+    assert abs(float(soft.s) / s64 - 1) < 1e-6
     assert abs(float(soft.p.astype(np.float64).sum()) - 1.0) < 1e-5
+    # p of a single element recomputed from its logit is the row's value.
+    for i in (0, 5, c + 3, 2 * c + 7, 3 * c - 1):
+        assert os_.p_at(soft, i) == soft.p[i]
+
+
+def test_softmax_layouts_and_temperature_agree_with_torch():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 128256, generator=g) * 4
+    for r in range(2):
+        for epv, temp in ((4, 1.0), (8, 0.7)):
+            soft = os_.softmax_row(os_.process_logits(x[r].numpy(), temp, epv=epv))
+            ref = torch.softmax(x[r].double() / temp, -1).numpy()
+            big = ref > 1e-30
+            assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 1e-5
 
 
 def test_temperature_and_penalty_closed_form():
     x = np.float32([-2.0, -0.5, 0.0, 0.5, 3.0])
     y = os_.process_logits(x, temperature=0.7, penalty=1.1, history=[0, 3, 3, 4])
-    inv_t = np.float32(1) / np.float32(0.7)
     inv_r = np.float32(1) / np.float32(1.1)
     want = np.float32([np.float32(-2.0 * np.float32(1.1)), -0.5, 0.0, np.float32(0.5 * inv_r), np.float32(3.0 * inv_r)])
-    assert np.array_equal(y, (want * inv_t).astype(np.float32))
-    assert np.array_equal(os_.process_logits(x, 1.0), x)
+    assert np.array_equal(y.x, want)
+    assert y.c == np.float32(nm.LOG2E * (np.float32(1) / np.float32(0.7)))
+    assert np.array_equal(os_.process_logits(x, 1.0).x, x) and os_.process_logits(x, 1.0).c == nm.LOG2E
 
 
 def brute_cutoff(p, top_p):

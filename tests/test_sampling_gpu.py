@@ -18,8 +18,14 @@ from tests.conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def oracle_filter(logits, temperature, top_p, penalty=1.0, history=None):
-    x = osmp.process_logits(np.asarray(logits, dtype=np.float32), temperature, penalty, history)
+def epv_of(dtype):
+    """Elements per 16-byte vector of the logits' storage type (fixes the
+    summation order of the chunk masses in the declared arithmetic)."""
+    return 4 if dtype == torch.float32 else 8
+
+
+def oracle_filter(logits, temperature, top_p, penalty=1.0, history=None, epv=4):
+    x = osmp.process_logits(np.asarray(logits, dtype=np.float32), temperature, penalty, history, epv)
     return osmp.filter_row(x, top_p)
 
 
@@ -33,7 +39,7 @@ def draft_tokens_from(inp, cfg):
         if cfg.penalty != 1.0:
             hist = inp["history"][b, : int(inp["history_len"][b])].numpy()
         for i in range(cfg.k):
-            q = oracle_filter(d[b, i], cfg.temperature, cfg.top_p, cfg.penalty, hist).P
+            q = oracle_filter(d[b, i], cfg.temperature, cfg.top_p, cfg.penalty, hist, epv_of(cfg.dtype)).P
             out[b, i] = osmp.categorical_pick(q, du[b, i])
     return torch.from_numpy(out)
 
@@ -53,7 +59,8 @@ def oracle_spec(cfg, inp, drafts):
     if cfg.penalty != 1.0:
         hists = [inp["history"][b, : int(inp["history_len"][b])].numpy() for b in range(cfg.batch)]
     return osmp.speculative_verify(inp["target"].float().numpy(), inp["draft"].float().numpy(), drafts.numpy(),
-                                   inp["uniforms"].numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hists)
+                                   inp["uniforms"].numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hists,
+                                   epv=epv_of(cfg.dtype))
 
 
 @pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 49152), (torch.float16, 4096),
@@ -66,7 +73,7 @@ def test_filter_logits_bitexact(gpu, dtype, vocab, temperature, top_p):
     res = verify.filter_logits(logits.to(gpu), temperature, top_p, want_probs=True)
     torch.cuda.synchronize()
     for r in range(6):
-        want = oracle_filter(logits[r].float().numpy(), temperature, top_p)
+        want = oracle_filter(logits[r].float().numpy(), temperature, top_p, epv=epv_of(dtype))
         assert np.array_equal(res["probs"][r].cpu().numpy(), want.soft.p), r
         assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
         if top_p < 1:
@@ -120,7 +127,8 @@ def test_sample_logits_bitexact(gpu, dtype, vocab, temperature, top_p):
     announce(f"sample dtype={dtype} V={vocab}")
     got = verify.sample_logits(logits.to(gpu), u.to(gpu), temperature, top_p)
     torch.cuda.synchronize()
-    want = [osmp.categorical_pick(oracle_filter(logits[r].float().numpy(), temperature, top_p).P, u[r].item())
+    want = [osmp.categorical_pick(oracle_filter(logits[r].float().numpy(), temperature, top_p,
+                                                epv=epv_of(dtype)).P, u[r].item())
             for r in range(rows)]
     assert got.cpu().tolist() == want
 
@@ -138,7 +146,7 @@ def test_sample_logits_with_penalty(gpu):
     want = []
     for r in range(cfg.batch):
         hist = inp["history"][r, : int(inp["history_len"][r])].numpy()
-        q = oracle_filter(logits[r].float().numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hist).P
+        q = oracle_filter(logits[r].float().numpy(), cfg.temperature, cfg.top_p, cfg.penalty, hist, 8).P
         want.append(osmp.categorical_pick(q, u[r].item()))
     assert got.cpu().tolist() == want
 
