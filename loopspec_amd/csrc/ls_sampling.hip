@@ -35,23 +35,23 @@
 namespace ls {
 namespace {
 
-constexpr int kChunk = 8192;                 // softmax chunk (declared arithmetic)
-constexpr int kChunkShift = 13;
-constexpr int kCB = 256;                     // lanes per workgroup
+constexpr int kChunk = 2048;                 // softmax chunk (declared arithmetic)
+constexpr int kChunkShift = 11;
+constexpr int kCB = 256;                     // row kernel lanes
 constexpr int kCW = kCB / kWave;
-constexpr int kPerLane = kChunk / kCB;       // 32 elements per lane and chunk
-constexpr int kChunkCand = 256;              // candidate slots per chunk in the workspace
+constexpr int kPerLane = kChunk / kWave;     // 32 elements per lane: one wave per chunk
+constexpr int kChunkCand = 64;               // candidate slots per chunk in the workspace
 constexpr int kOctBins = 16;                 // exponent bins of e
 constexpr int kHistStride = kOctBins + 1;    // lane-private bins, padded against bank conflicts
 constexpr int kRowCand = 2048;               // candidate slots of a row
 constexpr int kSlotsPerLane = kRowCand / kCB;
-constexpr int kMaxChunks = 32;               // vocab <= 262144
+constexpr int kMaxChunks = 128;              // vocab <= 262144
 constexpr int kMaxVocab = kMaxChunks * kChunk;
 constexpr int kBins = 2048;                  // radix digits per round
 constexpr int kBinsPerLane = kBins / kCB;
 constexpr int kGather = kWave;               // bucket size finished by one wave
 constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
-constexpr int kChunkWgsPerCu = 3;
+constexpr int kChunkWavesPerCu = 12;         // resident chunk waves per CU (LDS-bound)
 constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
 constexpr uint32_t kNone = 0xffffffffu;
@@ -204,11 +204,7 @@ __device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
 // ---------------------------------------------------------------------------
 struct ChunkSh {
   float est[kChunk];                   // e of the chunk, 16-byte slots XOR-swizzled
-  uint32_t hist[kCB * kHistStride];    // lane-private exponent bins
-  float wmax[kCW];
-  float wmass[kCW];
-  uint32_t binw[kCW][kOctBins];
-  uint32_t wcnt[kCW];
+  uint32_t hist[kWave * kHistStride];  // lane-private exponent bins
 };
 
 struct FinSh {
@@ -358,13 +354,13 @@ __device__ __forceinline__ void load_chunk(const SampParams& p, int item, u32x4 
   const u32x4* src = reinterpret_cast<const u32x4*>(row_of(p, g, jr)) + c0 / EPV;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    const int v = u * kCB + static_cast<int>(threadIdx.x);
+    const int v = u * kWave + static_cast<int>(threadIdx.x);
     d[u] = __builtin_nontemporal_load(src + (v < nvc ? v : nvc - 1));
   }
   if (p.use_pen) {
     const uint32_t* bm = p.bitmap + static_cast<int64_t>(g) * p.bm_words + c0 / 32;
 #pragma unroll
-    for (int u = 0; u < NVC; ++u) pw[u] = bm[((u * kCB + static_cast<int>(threadIdx.x)) * EPV) >> 5];
+    for (int u = 0; u < NVC; ++u) pw[u] = bm[((u * kWave + static_cast<int>(threadIdx.x)) * EPV) >> 5];
   }
 }
 
@@ -375,8 +371,8 @@ __device__ __forceinline__ int64_t item_token(const SampParams& p, int item) {
   return row_token(p, g, r - g * p.rpg);
 }
 
-// One chunk; returns true in every lane when this workgroup is the last to
-// finish a chunk of the row (and so finalises the row).
+// One chunk, processed by one wave: no workgroup barriers (the wave's LDS
+// accesses are ordered; s_barrier of a one-wave workgroup only fences).
 template <int DT, int NVC>
 __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, int item, const u32x4 (&d)[NVC],
                                               const uint32_t (&pw)[NVC], int64_t tok) {
@@ -384,55 +380,61 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
   constexpr int NE = NVC * EPV;
   static_assert(NE == kPerLane, "32 elements per lane");
   // lane-derived values are recomputed per item (not hoisted out of the
-  // persistent loop, where they would stay live through the row phase)
+  // persistent loop)
   int t = threadIdx.x;
   asm volatile("" : "+v"(t));
-  const int lane = t & (kWave - 1), wid = t / kWave;
   const int r = item / p.nch;
   const int cj = item - r * p.nch;
   const int c0 = cj * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
+  const bool full = nvc == NVC * kWave;  // only a row's last chunk can be partial
 
   // 1. penalised logits (-inf past the row end) and the chunk max
   float x[NE];
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    const bool in = u * kCB + t < nvc;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       float l = vec_elem<DT>(d[u], e);
-      if (p.use_pen && ((pw[u] >> ((((u * kCB + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
-      x[u * EPV + e] = in ? l : -__builtin_inff();
+      if (p.use_pen && ((pw[u] >> ((((u * kWave + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+      x[u * EPV + e] = l;
+    }
+  }
+  if (!full) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      if (u * kWave + t >= nvc) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) x[u * EPV + e] = -__builtin_inff();
+      }
     }
   }
   float mx = x[0];
 #pragma unroll
   for (int i = 1; i < NE; ++i) mx = nmax(mx, x[i]);
-  mx = wave_max_f32(mx);
-  if (lane == 0) cs.wmax[wid] = mx;
-  __syncthreads();
-  const float m = nmax(nmax(cs.wmax[0], cs.wmax[1]), nmax(cs.wmax[2], cs.wmax[3]));
+  const float m = wave_max_f32(mx);
   const float mc = m * p.c;
   const float nmc = -mc;
 
-  // 2. e in place, lane-private exponent bins, e-store
-  const int hbase = t * kHistStride;
+  // 2. e in place, lane-private exponent bins, e-store. Bin b holds e in
+  // [2^-b, 2^(1-b)) (bin 0: e >= 1; the last bin: everything smaller); lanes
+  // past the row end are not counted.
+  const int hbase = t * kHistStride + 127;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    const bool in = u * kCB + t < nvc;
+    const bool in = full || u * kWave + t < nvc;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       const float ev = exp2q(__builtin_fmaf(x[u * EPV + e], p.c, nmc));
       x[u * EPV + e] = ev;
-      // bin b holds e in [2^-b, 2^(1-b)) (bin 0: e >= 1; the last bin: everything smaller)
       const int be = static_cast<int>(__float_as_uint(ev) >> 23);
-      const int b = 127 - (be < 127 - (kOctBins - 1) ? 127 - (kOctBins - 1) : (be > 127 ? 127 : be));
-      if (in) __hip_atomic_fetch_add(&cs.hist[hbase + b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int bc = __builtin_elementwise_min(__builtin_elementwise_max(be, 127 - (kOctBins - 1)), 127);
+      if (in) __hip_atomic_fetch_add(&cs.hist[hbase - bc], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 #pragma unroll
     for (int h = 0; h < EPV / 4; ++h) {
-      const int s = (u * kCB + t) * (EPV / 4) + h;
+      const int s = (u * kWave + t) * (EPV / 4) + h;
       const int ps = s ^ ((s >> 3) & 7);
       f32x4 v;
       v.x = x[u * EPV + 4 * h + 0];
@@ -443,21 +445,21 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
     }
   }
   // chunk mass: each lane's 32 e pairwise, then the lanes pairwise
-  const float wm = wave_tree_sum(lane_tree_sum(x));
-  if (lane == 0) cs.wmass[wid] = wm;
+  const float mass = wave_tree_sum(lane_tree_sum(x));
   __syncthreads();
 
-  // 3. bin totals: thread (b, q) sums bin b of lanes 16q..16q+15 and clears it
+  // 3. bin totals: lane (b, q) sums bin b of lanes 16q..16q+15 and clears it
+  uint32_t bc;
   {
     const int b = t & (kOctBins - 1), q = t >> 4;
-    uint32_t s = 0;
+    uint32_t sb = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-      s += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
-    if (lane < kOctBins) cs.binw[wid][lane] = s;
+      sb += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+    sb += __shfl_xor(sb, 16);
+    sb += __shfl_xor(sb, 32);
+    bc = t < kOctBins ? sb : 0u;
   }
   // lane-contiguous e: elements [32t, 32t + 32) (index order within the lane)
   float ec[kPerLane];
@@ -469,32 +471,22 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
     ec[4 * q + 2] = v.z;
     ec[4 * q + 3] = v.w;
   }
-  float e_tok = 0.0f;
   const bool has_tok = tok >= c0 && tok < c0 + nel;
-  if (t == 0 && has_tok) e_tok = cs.est[est_index(static_cast<int>(tok - c0))];
-  __syncthreads();
+  float e_tok = 0.0f;
+  if (has_tok) e_tok = cs.est[est_index(static_cast<int>(tok - c0))];
 
   // 4. K: the number of leading exponent bins holding at most cap entries
-  uint32_t bc = 0;
-  if (lane < kOctBins) bc = cs.binw[0][lane] + cs.binw[1][lane] + cs.binw[2][lane] + cs.binw[3][lane];
   const uint32_t binc = wave_scan_add_u32(bc);
-  const int K = __builtin_popcountll(__ballot(lane < kOctBins && binc <= static_cast<uint32_t>(p.cap)));
+  const int K = __builtin_popcountll(__ballot(t < kOctBins && binc <= static_cast<uint32_t>(p.cap)));
   const float th = K >= kOctBins ? __uint_as_float(1u) : (K == 0 ? __builtin_inff() : __builtin_ldexpf(1.0f, 1 - K));
-  // 5. candidate mask (bit 31 - i <-> element 32t + i), counts, offsets
+  // 5. candidate mask (bit 31 - i <-> element 32t + i), offsets
   uint32_t mask = 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) mask = (mask << 1) | (ec[i] >= th ? 1u : 0u);
   const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(mask));
   const uint32_t incl = wave_scan_add_u32(cnt);
-  if (lane == kWave - 1) cs.wcnt[wid] = incl;
-  __syncthreads();
-  uint32_t pos = incl - cnt, total = 0;
-#pragma unroll
-  for (int w = 0; w < kCW; ++w) {
-    const uint32_t c = cs.wcnt[w];
-    pos += w < wid ? c : 0u;
-    total += c;
-  }
+  const uint32_t total = lane_bcast_u32(incl, kWave - 1);
+  uint32_t pos = incl - cnt;
   // 6. candidates, in index order
   uint64_t* out = p.cands + (static_cast<int64_t>(r) * p.nch + cj) * kChunkCand;
   const uint32_t ibase = static_cast<uint32_t>(c0 + kPerLane * t);
@@ -511,22 +503,23 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
     rec.K = K;
     rec.n = total;
     rec.flags = (K >= kOctBins ? kChunkComplete : 0u) | (has_tok ? kChunkHasTok : 0u);
-    rec.mass = (cs.wmass[0] + cs.wmass[1]) + (cs.wmass[2] + cs.wmass[3]);
+    rec.mass = mass;
     rec.e_tok = e_tok;
     rec.pad0 = rec.pad1 = 0;
     p.chunks[static_cast<int64_t>(r) * p.nch + cj] = rec;
   }
+  __syncthreads();  // the e-store and bins are rewritten by the next item
 }
 
 // Persistent over (row, chunk) items in row-major order, double-buffered: the
 // next item's loads are in flight while the current one is processed.
 template <int DT>
-__global__ __launch_bounds__(kCB, kChunkWgsPerCu) void chunk_kernel(const SampParams p) {
+__global__ __launch_bounds__(kWave, kChunkWavesPerCu) void chunk_kernel(const SampParams p) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int NVC = kChunk / (kCB * EPV);  // vectors per lane: 8 (f32) or 4
+  constexpr int NVC = kChunk / (kWave * EPV);  // vectors per lane: 8 (f32) or 4
   __shared__ ChunkSh cs;
   const int t = threadIdx.x;
-  for (int i = t; i < kCB * kHistStride; i += kCB) cs.hist[i] = 0u;
+  for (int i = t; i < kWave * kHistStride; i += kWave) cs.hist[i] = 0u;
   __syncthreads();
   int item = blockIdx.x;
   if (item >= p.items) return;
@@ -560,44 +553,70 @@ __global__ __launch_bounds__(kCB, kChunkWgsPerCu) void chunk_kernel(const SampPa
 // Row phase
 // ===========================================================================
 
-// Wave 0: from the chunk records of a row (lane j holds record j) compute the
-// row max, S and g_j (kept in fs.g / fs.mcj / fs.n [slot]), the bound on every
-// p outside the candidates, and p of the draft token.
+// Wave 0: from the chunk records of a row (lane l holds records 2l and
+// 2l+1) compute the row max, S and g_j (kept in fs.g / fs.mcj / fs.n [slot]),
+// the bound on every p outside the candidates, and p of the draft token.
 struct RowScale {
   float mcmax, s, p_bound, p_tok;
   bool has_tok;
 };
 
-__device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRec& rec, int nch) {
+__device__ __forceinline__ float chunk_bound(const ChunkRec& rec, float gj) {
+  if (rec.flags & kChunkComplete) return 0.0f;
+  return rec.K > 0 ? __builtin_ldexpf(1.0f, 1 - rec.K) * gj : __builtin_inff();
+}
+
+__device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRec& ra, const ChunkRec& rb, int nch) {
   const int lane = threadIdx.x & (kWave - 1);
-  const bool in = lane < nch;
+  const int ja = 2 * lane, jb = ja + 1;
+  const bool ia = ja < nch, ib = jb < nch;
   RowScale rs;
-  rs.mcmax = wave_max_f32(in ? rec.mc : -__builtin_inff());
-  const float f = in ? exp2q(rec.mc - rs.mcmax) : 0.0f;
-  rs.s = half_tree_sum(in ? f * rec.mass : 0.0f);
-  const float gj = f / rs.s;
-  if (in) {
-    fs.g[slot][lane] = gj;
-    fs.mcj[slot][lane] = rec.mc;
-    fs.n[slot][lane] = rec.n;
+  rs.mcmax = wave_max_f32(nmax(ia ? ra.mc : -__builtin_inff(), ib ? rb.mc : -__builtin_inff()));
+  const float fa = ia ? exp2q(ra.mc - rs.mcmax) : 0.0f;
+  const float fb = ib ? exp2q(rb.mc - rs.mcmax) : 0.0f;
+  // slots 2l and 2l+1 are the first pairwise level of the normaliser's sum
+  rs.s = wave_tree_sum((ia ? fa * ra.mass : 0.0f) + (ib ? fb * rb.mass : 0.0f));
+  const float ga = fa / rs.s, gb = fb / rs.s;
+  if (ia) {
+    fs.g[slot][ja] = ga;
+    fs.mcj[slot][ja] = ra.mc;
+    fs.n[slot][ja] = ra.n;
   }
-  float pb = 0.0f;
-  if (in && !(rec.flags & kChunkComplete)) pb = rec.K > 0 ? __builtin_ldexpf(1.0f, 1 - rec.K) * gj : __builtin_inff();
-  rs.p_bound = wave_max_f32(pb);
-  const bool tk = in && (rec.flags & kChunkHasTok);
-  rs.has_tok = __ballot(tk) != 0;
-  rs.p_tok = wave_max_f32(tk ? rec.e_tok * gj : -1.0f);
+  if (ib) {
+    fs.g[slot][jb] = gb;
+    fs.mcj[slot][jb] = rb.mc;
+    fs.n[slot][jb] = rb.n;
+  }
+  rs.p_bound = wave_max_f32(__builtin_fmaxf(ia ? chunk_bound(ra, ga) : 0.0f, ib ? chunk_bound(rb, gb) : 0.0f));
+  const bool ta = ia && (ra.flags & kChunkHasTok), tb = ib && (rb.flags & kChunkHasTok);
+  rs.has_tok = __ballot(ta || tb) != 0;
+  rs.p_tok = wave_max_f32(ta ? ra.e_tok * ga : (tb ? rb.e_tok * gb : -1.0f));
   return rs;
 }
 
-// Same from published row statistics (mcmax, S): g_j of the chunks only.
-__device__ __forceinline__ void row_g(FinSh& fs, int slot, const ChunkRec& rec, int nch, float mcmax, float s) {
+// g_j from published row statistics (mcmax, S), two chunks per lane.
+__device__ __forceinline__ void row_g(FinSh& fs, int slot, const ChunkRec& ra, const ChunkRec& rb, int nch,
+                                      float mcmax, float s) {
   const int lane = threadIdx.x & (kWave - 1);
-  if (lane < nch) {
-    fs.g[slot][lane] = exp2q(rec.mc - mcmax) / s;
-    fs.mcj[slot][lane] = rec.mc;
-    fs.n[slot][lane] = rec.n;
+  const int ja = 2 * lane, jb = ja + 1;
+  if (ja < nch) {
+    fs.g[slot][ja] = exp2q(ra.mc - mcmax) / s;
+    fs.mcj[slot][ja] = ra.mc;
+    fs.n[slot][ja] = ra.n;
   }
+  if (jb < nch) {
+    fs.g[slot][jb] = exp2q(rb.mc - mcmax) / s;
+    fs.mcj[slot][jb] = rb.mc;
+    fs.n[slot][jb] = rb.n;
+  }
+}
+
+// Chunk records 2l and 2l+1 of row r for lane l of wave 0.
+__device__ __forceinline__ void load_recs(const SampParams& p, int64_t r, ChunkRec* ra, ChunkRec* rb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ja = 2 * lane, jb = ja + 1;
+  if (ja < p.nch) *ra = p.chunks[r * p.nch + ja];
+  if (jb < p.nch) *rb = p.chunks[r * p.nch + jb];
 }
 
 __device__ __forceinline__ uint32_t digit_of(uint32_t bits, int shift, uint32_t dmask) {
@@ -884,14 +903,14 @@ template <int DT>
 __device__ int64_t residual_draw(const SampParams& p, Shared& sh, int64_t g, int i, bool own) {
   FinSh& fs = sh.f;
   const int k = p.k, rpg = 2 * k + 1, nch = p.nch, nslots = nch * p.cap;
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int t = threadIdx.x, wid = t / kWave;
   const int64_t rt = g * rpg + i, rd = g * rpg + k + 1 + i;
   // 1. both rows' statistics, chunk records, and the target's candidates
   if (t < 8) fs.statw[t] = load_sc64(reinterpret_cast<const uint64_t*>(p.stats + (t < 4 ? rt : rd)) + (t & 3));
-  ChunkRec rec_t{}, rec_d{};
-  if (wid == 0 && lane < nch) {
-    rec_d = p.chunks[rd * nch + lane];
-    if (!own) rec_t = p.chunks[rt * nch + lane];
+  ChunkRec rt_a{}, rt_b{}, rd_a{}, rd_b{};
+  if (wid == 0) {
+    load_recs(p, rd, &rd_a, &rd_b);
+    if (!own) load_recs(p, rt, &rt_a, &rt_b);
   }
   if (!own) {
 #pragma unroll
@@ -904,8 +923,8 @@ __device__ int64_t residual_draw(const SampParams& p, Shared& sh, int64_t g, int
   const RowStat st_t = stat_of(fs.statw[0], fs.statw[1], fs.statw[2], fs.statw[3]);
   const RowStat st_d = stat_of(fs.statw[4], fs.statw[5], fs.statw[6], fs.statw[7]);
   if (wid == 0) {
-    if (!own) row_g(fs, 0, rec_t, nch, st_t.mcmax, st_t.s);
-    row_g(fs, 1, rec_d, nch, st_d.mcmax, st_d.s);
+    if (!own) row_g(fs, 0, rt_a, rt_b, nch, st_t.mcmax, st_t.s);
+    row_g(fs, 1, rd_a, rd_b, nch, st_d.mcmax, st_d.s);
   }
   __syncthreads();
   const bool unf_t = st_t.flags & kFlagUnfiltered;
@@ -1052,8 +1071,8 @@ __global__ __launch_bounds__(kCB) void row_kernel(const SampParams p) {
   const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
 
   // 1. chunk records (wave 0) and candidate slots (strided), in flight together
-  ChunkRec rec{};
-  if (wid == 0 && t < nch) rec = p.chunks[static_cast<int64_t>(r) * nch + t];
+  ChunkRec ra{}, rb{};
+  if (wid == 0) load_recs(p, r, &ra, &rb);
   uint64_t cv[kSlotsPerLane];
 #pragma unroll
   for (int q = 0; q < kSlotsPerLane; ++q) {
@@ -1064,7 +1083,7 @@ __global__ __launch_bounds__(kCB) void row_kernel(const SampParams p) {
   for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
   // 2. row scales
   if (wid == 0) {
-    const RowScale rs = row_scale(fs, 0, rec, nch);
+    const RowScale rs = row_scale(fs, 0, ra, rb, nch);
     if (t == 0) {
       sh.f32s[4] = rs.mcmax;
       sh.f32s[5] = rs.s;
@@ -1257,8 +1276,8 @@ int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChu
 template <int DT, int MODE>
 void launch_dt(const SampParams& p, int64_t groups, int64_t rows, hipStream_t st) {
   if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(groups)), dim3(kBmB), 0, st, p);
-  const int wgs = static_cast<int>(device_cu_count()) * kChunkWgsPerCu;
-  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(p.items < wgs ? p.items : wgs), dim3(kCB), 0, st, p);
+  const int wgs = static_cast<int>(device_cu_count()) * kChunkWavesPerCu;
+  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(p.items < wgs ? p.items : wgs), dim3(kWave), 0, st, p);
   hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kCB), 0, st, p);
   if constexpr (MODE == kModeDense) {
     hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.items), dim3(kCB), 0, st, p);
@@ -1293,7 +1312,7 @@ int setup_common(SampParams& p, int dtype, int64_t rows, int64_t vocab, float te
     return fail(LS_ERR_VALUE, "repetition penalty needs a token history");
   p.vocab = static_cast<int>(vocab);
   p.nch = nch_for(vocab);
-  p.cap_log2 = p.nch <= kRowCand / kChunkCand ? 8 : (p.nch <= 2 * kRowCand / kChunkCand ? 7 : 6);
+  p.cap_log2 = p.nch <= kRowCand / kChunkCand ? 6 : (p.nch <= 2 * kRowCand / kChunkCand ? 5 : 4);
   p.cap = 1 << p.cap_log2;  // nch * cap <= kRowCand
   p.bm_words = p.nch * (kChunk / 32);
   p.items = static_cast<int>(rows * p.nch);

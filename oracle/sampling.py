@@ -85,9 +85,9 @@ def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float 
     return Processed(x, scale_of(temperature), epv)
 
 
-CHUNK = 8192  # elements per softmax chunk (a constant of the declared arithmetic)
-LANES = 256   # lanes per chunk in the mass summation order
-SCALE_SLOTS = 32  # chunks per row at most; the normaliser sums this many slots
+CHUNK = 2048  # elements per softmax chunk (a constant of the declared arithmetic)
+LANES = 64    # lanes per chunk in the mass summation order
+SCALE_SLOTS = 128  # chunks per row at most; the normaliser sums this many slots
 
 
 @dataclass

@@ -28,7 +28,7 @@ def test_softmax_matches_torch():
 
 def test_chunk_mass_order():
     # M_j sums each lane's 32 elements pairwise, lane t owning 16-byte vectors
-    # u * 256 + t; placing two 2^-24 next to a 1 in one pairwise group loses
+    # u * 64 + t; placing two 2^-24 next to a 1 in one pairwise group loses
     # them (ties to even), placing them in a group of their own keeps 2^-23.
     tiny = np.float32(2.0 ** -24)
     for epv in (4, 8):
@@ -38,9 +38,9 @@ def test_chunk_mass_order():
         e = np.zeros(os_.CHUNK, np.float32)
         e[0], e[epv], e[epv + 1] = 1, tiny, tiny  # the tiny pair is lane 1's first vector
         assert os_.chunk_mass(e, epv) == np.float32(1 + 2.0 ** -23)
-    # Elements 1024 and 1028: with epv = 4 they are the second vectors of
-    # lanes 0 and 1 (each tiny meets the 1 on its own and is lost); with epv = 8
-    # both sit in lane 128's first vector and add up first.
+    # Elements 1024 and 1028: with epv = 4 they open lane 0's and lane 1's
+    # fifth vectors (each tiny meets the 1 on its own and is lost); with epv = 8
+    # both sit in lane 0's third vector and add up first.
     e = np.zeros(os_.CHUNK, np.float32)
     e[0], e[1024], e[1028] = 1, tiny, tiny
     assert os_.chunk_mass(e, 4) == np.float32(1)
@@ -49,7 +49,7 @@ def test_chunk_mass_order():
 
 def test_chunked_softmax_closed_forms():
     c = os_.CHUNK
-    # A zero row of 3 chunks + 5: every e = 1, M = (8192, 8192, 8192, 5),
+    # A zero row of 3 chunks + 5: every e = 1, M = (2048, 2048, 2048, 5),
     # S = V exactly, p = RN(1 / V).
     v = 3 * c + 5
     soft = os_.softmax_row(np.zeros(v, np.float32))
