@@ -37,18 +37,19 @@ namespace {
 
 constexpr int kChunk = 2048;                 // softmax chunk (declared arithmetic)
 constexpr int kChunkShift = 11;
-constexpr int kCB = 256;                     // row kernel lanes
-constexpr int kCW = kCB / kWave;
+constexpr int kCB = 256;                     // dense kernel lanes
+constexpr int kRB = 512;                     // row kernel lanes
+constexpr int kRW = kRB / kWave;
 constexpr int kPerLane = kChunk / kWave;     // 32 elements per lane: one wave per chunk
 constexpr int kChunkCand = 64;               // candidate slots per chunk in the workspace
 constexpr int kOctBins = 16;                 // exponent bins of e
 constexpr int kHistStride = kOctBins + 1;    // lane-private bins, padded against bank conflicts
 constexpr int kRowCand = 2048;               // candidate slots of a row
-constexpr int kSlotsPerLane = kRowCand / kCB;
+constexpr int kSlotsPerLane = kRowCand / kRB;
 constexpr int kMaxChunks = 128;              // vocab <= 262144
 constexpr int kMaxVocab = kMaxChunks * kChunk;
 constexpr int kBins = 2048;                  // radix digits per round
-constexpr int kBinsPerLane = kBins / kCB;
+constexpr int kBinsPerLane = kBins / kRB;
 constexpr int kGather = kWave;               // bucket size finished by one wave
 constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
 constexpr int kChunkWavesPerCu = 12;         // resident chunk waves per CU (LDS-bound)
@@ -207,61 +208,10 @@ struct ChunkSh {
   uint32_t hist[kWave * kHistStride];  // lane-private exponent bins
 };
 
-struct FinSh {
-  uint64_t slot[kRowCand];             // the row's candidate slots (idx << 32 | bits)
-  union {
-    uint64_t H[kBins];                 // radix bins
-    uint64_t slot_d[kRowCand];         // tail: the draft row's candidate slots
-    float w[kRowCand];                 // tail: draw weights per slot
-    uint64_t words64[kBins];           // tail: row statistics (4 words each)
-  };
-  float g[2][kMaxChunks];
-  float mcj[2][kMaxChunks];
-  uint32_t n[2][kMaxChunks];
-  uint32_t gbits[kGather];
-  uint64_t gw[kGather];
-  uint32_t gcount;
-  uint64_t statw[8];                   // residual: both rows' statistics
-  float tokp[2 * 64 + 1];              // accept chain: P / Q of the draft tokens
-  int64_t tokd[64 + 1];                // accept chain: the published draws
-};
-
-struct Shared {
-  FinSh f;
-  uint64_t red[kCW];
-  uint64_t u64s[8];
-  uint32_t u32s[8];
-  float f32s[8];
-};
-
 // Physical float index of element v of the chunk in the e-store.
 __device__ __forceinline__ int est_index(int v) {
   const int s = v >> 2;
   return ((s ^ ((s >> 3) & 7)) << 2) | (v & 3);
-}
-
-// Exclusive scan in lane order over the workgroup; *total receives the sum.
-__device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t* smem, uint64_t* total) {
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  const uint64_t inc = wave_scan_add_u64(v);
-  __syncthreads();
-  if (lane == kWave - 1) smem[wid] = inc;
-  __syncthreads();
-  uint64_t base = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < kCW; ++i) {
-    const uint64_t s = smem[i];
-    base += i < wid ? s : 0;
-    tot += s;
-  }
-  *total = tot;
-  return base + inc - v;
-}
-
-__device__ __forceinline__ uint64_t block_sum(uint64_t v, uint64_t* smem) {
-  uint64_t tot;
-  (void)block_excl_scan(v, smem, &tot);
-  return tot;
 }
 
 __device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) {
@@ -270,45 +220,6 @@ __device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) {
 __device__ __forceinline__ uint64_t pack2f(float lo, float hi) { return pack2(__float_as_uint(lo), __float_as_uint(hi)); }
 __device__ __forceinline__ float lo_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 __device__ __forceinline__ float hi_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
-
-__device__ __forceinline__ void put_rec(ChunkRec* dst, const ChunkRec& v) {
-  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
-  store_sc64(d + 0, pack2(__float_as_uint(v.mc), static_cast<uint32_t>(v.K)));
-  store_sc64(d + 1, pack2(v.n, v.flags));
-  store_sc64(d + 2, pack2f(v.mass, v.e_tok));
-}
-__device__ __forceinline__ ChunkRec get_rec(const ChunkRec* src) {
-  const uint64_t* s = reinterpret_cast<const uint64_t*>(src);
-  const uint64_t a = load_sc64(s + 0), b = load_sc64(s + 1), c = load_sc64(s + 2);
-  ChunkRec v;
-  v.mc = lo_f(a);
-  v.K = static_cast<int32_t>(a >> 32);
-  v.n = static_cast<uint32_t>(b);
-  v.flags = static_cast<uint32_t>(b >> 32);
-  v.mass = lo_f(c);
-  v.e_tok = hi_f(c);
-  v.pad0 = v.pad1 = 0;
-  return v;
-}
-__device__ __forceinline__ void put_stat(RowStat* dst, const RowStat& v) {
-  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
-  store_sc64(d + 0, pack2f(v.mcmax, v.s));
-  store_sc64(d + 1, pack2f(v.cutoff, v.mass));
-  store_sc64(d + 2, pack2(v.flags, __float_as_uint(v.p_tok)));
-  store_sc64(d + 3, v.mass_fx);
-}
-// The four 64-bit words of a published RowStat and the struct they encode.
-__device__ __forceinline__ RowStat stat_of(uint64_t a, uint64_t b, uint64_t c, uint64_t d) {
-  RowStat v;
-  v.mcmax = lo_f(a);
-  v.s = hi_f(a);
-  v.cutoff = lo_f(b);
-  v.mass = hi_f(b);
-  v.flags = static_cast<uint32_t>(c);
-  v.p_tok = hi_f(c);
-  v.mass_fx = d;
-  return v;
-}
 
 // ===========================================================================
 // bitmap_kernel: the penalty bitmap of each group's token history
@@ -371,9 +282,51 @@ __device__ __forceinline__ int64_t item_token(const SampParams& p, int item) {
   return row_token(p, g, r - g * p.rpg);
 }
 
+// Bins and candidates: bin b = min(-k, 15) counts the elements whose
+// exponent scaling in exp2q is 2^k = 2^-b (e in [2^-b / sqrt2, 2^-b * sqrt2)),
+// the last bin also everything smaller; lanes past the row end are not
+// counted. With K the number of leading bins holding at most cap entries,
+// the candidates are the e >= kCandScale * 2^-K, all inside those bins since
+// e <= kCandScale * 2^k for every k (K == kOctBins: every e > 0; K == 0: none).
+constexpr float kCandScale = 1.41422f;  // > max of exp2q's polynomial over [-1/2, 1/2]
+
+template <bool IN_ALL, int DT, int NVC>
+__device__ __forceinline__ void exp_bins(const SampParams& p, ChunkSh& cs, float (&x)[NVC * Elem<DT>::kPerVec],
+                                         int t, int nvc, float nmc) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  // byte offset of this lane's bin 0 in the histogram
+  const int hbase4 = static_cast<int>(reinterpret_cast<uintptr_t>(&cs.hist[t * kHistStride]) -
+                                      reinterpret_cast<uintptr_t>(&cs.hist[0]));
+  char* hist0 = reinterpret_cast<char*>(&cs.hist[0]);
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) {
+    const bool in = IN_ALL || u * kWave + t < nvc;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      int ki;
+      x[u * EPV + e] = exp2q_k(__builtin_fmaf(x[u * EPV + e], p.c, nmc), &ki);
+      const int b = __builtin_elementwise_min(__builtin_elementwise_max(ki, -(kOctBins - 1)), 0);  // -bin
+      if (in)
+        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(hist0 + (hbase4 - 4 * b)), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+#pragma unroll
+    for (int h = 0; h < EPV / 4; ++h) {
+      const int s = (u * kWave + t) * (EPV / 4) + h;
+      const int ps = s ^ ((s >> 3) & 7);
+      f32x4 v;
+      v.x = x[u * EPV + 4 * h + 0];
+      v.y = x[u * EPV + 4 * h + 1];
+      v.z = x[u * EPV + 4 * h + 2];
+      v.w = x[u * EPV + 4 * h + 3];
+      *reinterpret_cast<f32x4*>(&cs.est[ps * 4]) = v;
+    }
+  }
+}
+
 // One chunk, processed by one wave: no workgroup barriers (the wave's LDS
 // accesses are ordered; s_barrier of a one-wave workgroup only fences).
-template <int DT, int NVC>
+template <int DT, int NVC, bool PEN>
 __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, int item, const u32x4 (&d)[NVC],
                                               const uint32_t (&pw)[NVC], int64_t tok) {
   constexpr int EPV = Elem<DT>::kPerVec;
@@ -397,7 +350,7 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       float l = vec_elem<DT>(d[u], e);
-      if (p.use_pen && ((pw[u] >> ((((u * kWave + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+      if (PEN && ((pw[u] >> ((((u * kWave + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
       x[u * EPV + e] = l;
     }
   }
@@ -417,32 +370,11 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
   const float mc = m * p.c;
   const float nmc = -mc;
 
-  // 2. e in place, lane-private exponent bins, e-store. Bin b holds e in
-  // [2^-b, 2^(1-b)) (bin 0: e >= 1; the last bin: everything smaller); lanes
-  // past the row end are not counted.
-  const int hbase = t * kHistStride + 127;
-#pragma unroll
-  for (int u = 0; u < NVC; ++u) {
-    const bool in = full || u * kWave + t < nvc;
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      const float ev = exp2q(__builtin_fmaf(x[u * EPV + e], p.c, nmc));
-      x[u * EPV + e] = ev;
-      const int be = static_cast<int>(__float_as_uint(ev) >> 23);
-      const int bc = __builtin_elementwise_min(__builtin_elementwise_max(be, 127 - (kOctBins - 1)), 127);
-      if (in) __hip_atomic_fetch_add(&cs.hist[hbase - bc], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-#pragma unroll
-    for (int h = 0; h < EPV / 4; ++h) {
-      const int s = (u * kWave + t) * (EPV / 4) + h;
-      const int ps = s ^ ((s >> 3) & 7);
-      f32x4 v;
-      v.x = x[u * EPV + 4 * h + 0];
-      v.y = x[u * EPV + 4 * h + 1];
-      v.z = x[u * EPV + 4 * h + 2];
-      v.w = x[u * EPV + 4 * h + 3];
-      *reinterpret_cast<f32x4*>(&cs.est[ps * 4]) = v;
-    }
+  // 2. e in place, exponent bins, e-store
+  if (full) {
+    exp_bins<true, DT, NVC>(p, cs, x, t, nvc, nmc);
+  } else {
+    exp_bins<false, DT, NVC>(p, cs, x, t, nvc, nmc);
   }
   // chunk mass: each lane's 32 e pairwise, then the lanes pairwise
   const float mass = wave_tree_sum(lane_tree_sum(x));
@@ -478,11 +410,14 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
   // 4. K: the number of leading exponent bins holding at most cap entries
   const uint32_t binc = wave_scan_add_u32(bc);
   const int K = __builtin_popcountll(__ballot(t < kOctBins && binc <= static_cast<uint32_t>(p.cap)));
-  const float th = K >= kOctBins ? __uint_as_float(1u) : (K == 0 ? __builtin_inff() : __builtin_ldexpf(1.0f, 1 - K));
+  const float th = K >= kOctBins ? __uint_as_float(1u) : (K == 0 ? __builtin_inff() : __builtin_ldexpf(kCandScale, -K));
   // 5. candidate mask (bit 31 - i <-> element 32t + i), offsets
   uint32_t mask = 0;
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) mask = (mask << 1) | (ec[i] >= th ? 1u : 0u);
+  for (int i = 0; i < kPerLane; ++i) {
+    // mask = 2 mask + (ec[i] >= th): a compare into VCC and one add with carry
+    asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc" : "+v"(mask) : "v"(ec[i]), "v"(th) : "vcc");
+  }
   const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(mask));
   const uint32_t incl = wave_scan_add_u32(cnt);
   const uint32_t total = lane_bcast_u32(incl, kWave - 1);
@@ -513,8 +448,9 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
 
 // Persistent over (row, chunk) items in row-major order, double-buffered: the
 // next item's loads are in flight while the current one is processed.
-template <int DT>
-__global__ __launch_bounds__(kWave, kChunkWavesPerCu) void chunk_kernel(const SampParams p) {
+template <int DT, bool PEN>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(kChunkWavesPerCu / 4)))
+void chunk_kernel(const SampParams p) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kWave * EPV);  // vectors per lane: 8 (f32) or 4
   __shared__ ChunkSh cs;
@@ -533,7 +469,7 @@ __global__ __launch_bounds__(kWave, kChunkWavesPerCu) void chunk_kernel(const Sa
       load_chunk<DT, NVC>(p, next, nxt, pnxt);
       tnxt = item_token(p, next);
     }
-    process_chunk<DT, NVC>(p, cs, item, cur, pcur, tcur);
+    process_chunk<DT, NVC, PEN>(p, cs, item, cur, pcur, tcur);
     if (next >= p.items) break;
     // register moves (the empty asm keeps the copy from becoming a memcpy of
     // the arrays, which would put them in scratch)
@@ -553,8 +489,68 @@ __global__ __launch_bounds__(kWave, kChunkWavesPerCu) void chunk_kernel(const Sa
 // Row phase
 // ===========================================================================
 
-// Wave 0: from the chunk records of a row (lane l holds records 2l and
-// 2l+1) compute the row max, S and g_j (kept in fs.g / fs.mcj / fs.n [slot]),
+// Shared memory of the row kernels: up to two rows (spec: the target and the
+// draft row of one draft position) finalised side by side.
+struct RowSh {
+  uint64_t slot[2][kRowCand];          // candidate slots (idx << 32 | bits(p))
+  union {
+    uint64_t H[2][kBins];              // radix bins of each row
+    float w[kRowCand];                 // draw weights per slot
+  };
+  float g[2][kMaxChunks];
+  float mcj[2][kMaxChunks];
+  uint32_t n[2][kMaxChunks];
+  uint32_t gbits[2][kGather];
+  uint64_t gw[2][kGather];
+  uint32_t gcount[2];
+  uint32_t sel32[2][2];
+  uint64_t sel64[2][3];
+  uint64_t red[2 * kRW];
+  uint64_t u64s[8];
+  uint32_t u32s[8];
+  float f32s[2][4];
+  uint64_t draws[64 + 1];
+};
+
+// Exclusive scans in lane order over the workgroup of NS values at once;
+// tot receives the sums. smem holds NS * kRW words.
+template <int NS>
+__device__ __forceinline__ void block_excl_scan_n(const uint64_t (&v)[NS], uint64_t* smem, uint64_t (&ex)[NS],
+                                                  uint64_t (&tot)[NS]) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  uint64_t inc[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) inc[s] = wave_scan_add_u64(v[s]);
+  __syncthreads();
+  if (lane == kWave - 1) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) smem[s * kRW + wid] = inc[s];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint64_t base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < kRW; ++i) {
+      const uint64_t x = smem[s * kRW + i];
+      base += i < wid ? x : 0;
+      t += x;
+    }
+    ex[s] = base + inc[s] - v[s];
+    tot[s] = t;
+  }
+}
+
+__device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t* smem, uint64_t* total) {
+  const uint64_t vv[1] = {v};
+  uint64_t ex[1], tot[1];
+  block_excl_scan_n<1>(vv, smem, ex, tot);
+  *total = tot[0];
+  return ex[0];
+}
+
+// Wave w: from the chunk records of row-set `set` (lane l holds records 2l
+// and 2l+1) compute the row max, S and g_j (kept in sh.g / sh.mcj / sh.n),
 // the bound on every p outside the candidates, and p of the draft token.
 struct RowScale {
   float mcmax, s, p_bound, p_tok;
@@ -563,10 +559,10 @@ struct RowScale {
 
 __device__ __forceinline__ float chunk_bound(const ChunkRec& rec, float gj) {
   if (rec.flags & kChunkComplete) return 0.0f;
-  return rec.K > 0 ? __builtin_ldexpf(1.0f, 1 - rec.K) * gj : __builtin_inff();
+  return rec.K > 0 ? __builtin_ldexpf(kCandScale, -rec.K) * gj : __builtin_inff();
 }
 
-__device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRec& ra, const ChunkRec& rb, int nch) {
+__device__ __forceinline__ RowScale row_scale(RowSh& sh, int set, const ChunkRec& ra, const ChunkRec& rb, int nch) {
   const int lane = threadIdx.x & (kWave - 1);
   const int ja = 2 * lane, jb = ja + 1;
   const bool ia = ja < nch, ib = jb < nch;
@@ -578,14 +574,14 @@ __device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRe
   rs.s = wave_tree_sum((ia ? fa * ra.mass : 0.0f) + (ib ? fb * rb.mass : 0.0f));
   const float ga = fa / rs.s, gb = fb / rs.s;
   if (ia) {
-    fs.g[slot][ja] = ga;
-    fs.mcj[slot][ja] = ra.mc;
-    fs.n[slot][ja] = ra.n;
+    sh.g[set][ja] = ga;
+    sh.mcj[set][ja] = ra.mc;
+    sh.n[set][ja] = ra.n;
   }
   if (ib) {
-    fs.g[slot][jb] = gb;
-    fs.mcj[slot][jb] = rb.mc;
-    fs.n[slot][jb] = rb.n;
+    sh.g[set][jb] = gb;
+    sh.mcj[set][jb] = rb.mc;
+    sh.n[set][jb] = rb.n;
   }
   rs.p_bound = wave_max_f32(__builtin_fmaxf(ia ? chunk_bound(ra, ga) : 0.0f, ib ? chunk_bound(rb, gb) : 0.0f));
   const bool ta = ia && (ra.flags & kChunkHasTok), tb = ib && (rb.flags & kChunkHasTok);
@@ -594,24 +590,7 @@ __device__ __forceinline__ RowScale row_scale(FinSh& fs, int slot, const ChunkRe
   return rs;
 }
 
-// g_j from published row statistics (mcmax, S), two chunks per lane.
-__device__ __forceinline__ void row_g(FinSh& fs, int slot, const ChunkRec& ra, const ChunkRec& rb, int nch,
-                                      float mcmax, float s) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int ja = 2 * lane, jb = ja + 1;
-  if (ja < nch) {
-    fs.g[slot][ja] = exp2q(ra.mc - mcmax) / s;
-    fs.mcj[slot][ja] = ra.mc;
-    fs.n[slot][ja] = ra.n;
-  }
-  if (jb < nch) {
-    fs.g[slot][jb] = exp2q(rb.mc - mcmax) / s;
-    fs.mcj[slot][jb] = rb.mc;
-    fs.n[slot][jb] = rb.n;
-  }
-}
-
-// Chunk records 2l and 2l+1 of row r for lane l of wave 0.
+// Chunk records 2l and 2l+1 of row r for lane l.
 __device__ __forceinline__ void load_recs(const SampParams& p, int64_t r, ChunkRec* ra, ChunkRec* rb) {
   const int lane = threadIdx.x & (kWave - 1);
   const int ja = 2 * lane, jb = ja + 1;
@@ -624,107 +603,166 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t bits, int shift, uint32_t 
   return d < kBins ? d : kBins - 1;
 }
 
-// Exact top-p cutoff over a set whose elements visit(f) passes to f(bits, w)
-// (bits of p > 0, w = fx46(p)): c = max{v : sum_{p >= v} w >= thr}, and the
-// mass kept. Up to three radix rounds on the bits of p (12, 11 and 8 bits
-// from the top; fs.H must be zero on entry); after each round a bucket of at
-// most kGather entries is finished by one wave. Returns false if the set's
-// total mass is below thr.
-template <typename Visit>
-__device__ bool radix_select(Shared& sh, uint64_t thr, Visit visit, float* cutoff, uint64_t* mass) {
-  FinSh& fs = sh.f;
+// Exact top-p cutoffs of NS sets at once (sets s0 .. s0+NS-1 of sh), each
+// visited by visit(s, f), which passes f(bits, w) for its elements (bits of
+// p > 0, w = fx46(p)): c = max{v : sum_{p >= v} w >= thr}, and the mass
+// kept. Up to three radix rounds on the bits of p (12, 11 and 8 bits from the
+// top; sh.H[s] zero on entry); after each round a bucket of at most kGather
+// entries is finished by one wave (wave s for set s). found[s] is false when
+// the set's total mass is below thr. The sets advance in lockstep, so NS rows
+// cost the barriers of one.
+template <int NS, typename Visit>
+__device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Visit visit, bool (&found)[NS],
+                               float (&cut)[NS], uint64_t (&mass)[NS]) {
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  uint32_t prefix = 0, pmask = 0;
-  uint64_t above = 0;
+  uint32_t prefix[NS], pmask[NS];
+  uint64_t above[NS];
+  bool done[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    prefix[s] = pmask[s] = 0;
+    above[s] = 0;
+    done[s] = false;
+    found[s] = false;
+  }
   for (int round = 0; round < 3; ++round) {
     const int shift = round == 0 ? 19 : (round == 1 ? 8 : 0);
     const uint32_t dmask = round == 0 ? 0xfffu : (round == 1 ? 0x7ffu : 0xffu);
     if (round > 0) {
 #pragma unroll
-      for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
+      for (int s = 0; s < NS; ++s) {
+        if (!done[s]) {
+#pragma unroll
+          for (int q = 0; q < kBinsPerLane; ++q) sh.H[s0 + s][kBinsPerLane * t + q] = 0;
+        }
+      }
       __syncthreads();
     }
-    visit([&](uint32_t bits, uint64_t w) {
-      if ((bits & pmask) == prefix && w)
-        __hip_atomic_fetch_add(&fs.H[digit_of(bits, shift, dmask)], w, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-    });
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (!done[s]) {
+        uint64_t* H = sh.H[s0 + s];
+        const uint32_t pm = pmask[s], pf = prefix[s];
+        visit(s, [&](uint32_t bits, uint64_t w) {
+          if ((bits & pm) == pf && w)
+            __hip_atomic_fetch_add(&H[digit_of(bits, shift, dmask)], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        });
+      }
+    }
     __syncthreads();
     // lane t owns digits kBins-1 - (kBinsPerLane*t + q), q = 0.. (descending)
-    uint64_t v[kBinsPerLane];
-    uint64_t sum = 0;
+    uint64_t v[NS][kBinsPerLane], sum[NS], ex[NS], tot[NS];
 #pragma unroll
-    for (int q = 0; q < kBinsPerLane; ++q) {
-      v[q] = fs.H[kBins - 1 - (kBinsPerLane * t + q)];
-      sum += v[q];
-    }
-    uint64_t total;
-    const uint64_t ex = block_excl_scan(sum, sh.red, &total);
-    if (t == 0) sh.u32s[1] = kNone;
-    __syncthreads();
-    uint64_t before = above + ex;
-    if (before < thr && before + sum >= thr) {
+    for (int s = 0; s < NS; ++s) {
+      sum[s] = 0;
 #pragma unroll
       for (int q = 0; q < kBinsPerLane; ++q) {
-        if (before < thr && before + v[q] >= thr) {
-          sh.u32s[1] = static_cast<uint32_t>(kBins - 1 - (kBinsPerLane * t + q));
-          sh.u64s[1] = before;
-          sh.u64s[2] = v[q];
-        }
-        before += v[q];
+        v[s][q] = done[s] ? 0 : sh.H[s0 + s][kBins - 1 - (kBinsPerLane * t + q)];
+        sum[s] += v[s][q];
       }
     }
-    if (t == 0) fs.gcount = 0;
+    block_excl_scan_n<NS>(sum, sh.red, ex, tot);
+    if (t < NS) sh.sel32[t][0] = kNone;
     __syncthreads();
-    const uint32_t digit = sh.u32s[1];
-    if (digit == kNone) return false;
-    prefix |= digit << shift;
-    pmask |= dmask << shift;
-    above = sh.u64s[1];
-    const uint64_t binmass = sh.u64s[2];
-    visit([&](uint32_t bits, uint64_t w) {
-      if ((bits & pmask) == prefix && w) {
-        const uint32_t k = __hip_atomic_fetch_add(&fs.gcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (k < kGather) {
-          fs.gbits[k] = bits;
-          fs.gw[k] = w;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint64_t before = above[s] + ex[s];
+      if (!done[s] && before < thr[s] && before + sum[s] >= thr[s]) {
+#pragma unroll
+        for (int q = 0; q < kBinsPerLane; ++q) {
+          if (before < thr[s] && before + v[s][q] >= thr[s]) {
+            sh.sel32[s][0] = static_cast<uint32_t>(kBins - 1 - (kBinsPerLane * t + q));
+            sh.sel64[s][0] = before;
+            sh.sel64[s][1] = v[s][q];
+          }
+          before += v[s][q];
         }
       }
-    });
-    __syncthreads();
-    const uint32_t cnt = fs.gcount;
-    if (cnt > kGather && round == 2) {
-      // every entry of the bucket has the same bits
-      *cutoff = __uint_as_float(prefix);
-      *mass = above + binmass;
-      return true;
     }
-    if (cnt <= kGather) {
-      if (wid == 0) {
-        const uint32_t b = lane < static_cast<int>(cnt) ? fs.gbits[lane] : 0u;
-        const uint64_t w = lane < static_cast<int>(cnt) ? fs.gw[lane] : 0;
-        uint64_t A = above;
-        for (int j = 0; j < static_cast<int>(cnt); ++j) {
-          const uint32_t bj = lane_bcast_u32(b, j);
-          const uint64_t wj = lane_bcast_u64(w, j);
-          A += bj >= b ? wj : 0;
-        }
-        const bool ok = lane < static_cast<int>(cnt) && A >= thr;
-        const uint64_t best = wave_max_u64(ok ? b : 0u);
-        const uint64_t at = wave_max_u64(ok && b == static_cast<uint32_t>(best) ? A : 0);
-        if (lane == 0) {
-          sh.u32s[2] = static_cast<uint32_t>(best);
-          sh.u64s[4] = at;
+    if (t < NS) sh.gcount[t] = 0;
+    __syncthreads();
+    uint64_t binmass[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      binmass[s] = 0;
+      if (!done[s]) {
+        const uint32_t digit = sh.sel32[s][0];
+        if (digit == kNone) {
+          done[s] = true;
+        } else {
+          prefix[s] |= digit << shift;
+          pmask[s] |= dmask << shift;
+          above[s] = sh.sel64[s][0];
+          binmass[s] = sh.sel64[s][1];
         }
       }
-      __syncthreads();
-      *cutoff = __uint_as_float(sh.u32s[2]);
-      *mass = sh.u64s[4];
-      return true;
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (!done[s]) {
+        const uint32_t pm = pmask[s], pf = prefix[s];
+        uint32_t* gb = sh.gbits[s];
+        uint64_t* gw = sh.gw[s];
+        uint32_t* gc = &sh.gcount[s];
+        visit(s, [&](uint32_t bits, uint64_t w) {
+          if ((bits & pm) == pf && w) {
+            const uint32_t k = __hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (k < kGather) {
+              gb[k] = bits;
+              gw[k] = w;
+            }
+          }
+        });
+      }
     }
     __syncthreads();
+    bool finish[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      finish[s] = false;
+      if (!done[s]) {
+        const uint32_t cnt = sh.gcount[s];
+        if (cnt > kGather && round == 2) {
+          // every entry of the bucket has the same bits
+          cut[s] = __uint_as_float(prefix[s]);
+          mass[s] = above[s] + binmass[s];
+          found[s] = true;
+          done[s] = true;
+        } else if (cnt <= kGather) {
+          finish[s] = true;
+          if (wid == s) {
+            const uint32_t b = lane < static_cast<int>(cnt) ? sh.gbits[s][lane] : 0u;
+            uint64_t A = above[s];
+            for (int j = 0; j < static_cast<int>(cnt); ++j) {
+              const uint32_t bj = sh.gbits[s][j];
+              const uint64_t wj = sh.gw[s][j];
+              A += bj >= b ? wj : 0;
+            }
+            const bool ok = lane < static_cast<int>(cnt) && A >= thr[s];
+            const uint64_t best = wave_max_u64(ok ? b : 0u);
+            const uint64_t at = wave_max_u64(ok && b == static_cast<uint32_t>(best) ? A : 0);
+            if (lane == 0) {
+              sh.sel32[s][1] = static_cast<uint32_t>(best);
+              sh.sel64[s][2] = at;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    bool all = true;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (finish[s]) {
+        cut[s] = __uint_as_float(sh.sel32[s][1]);
+        mass[s] = sh.sel64[s][2];
+        found[s] = true;
+        done[s] = true;
+      }
+      all = all && done[s];
+    }
+    if (all) break;
   }
-  return false;  // not reached
 }
 
 // p of element i of a row recomputed from its logit.
@@ -737,11 +775,11 @@ __device__ __forceinline__ float p_elem(const char* rowp, const uint32_t* bm, fl
   return exp2q(__builtin_fmaf(l, c, -mcj[j])) * gj[j];
 }
 
-// Index-ordered inverse-CDF pick over the first n LDS slots; weight(s) is an
-// exact fx46 mass. Lane t owns slots [16t, 16t+16). Returns the winning slot,
-// or -1 at zero total mass.
+// Index-ordered inverse-CDF pick over the first n slots; weight(s) is an
+// exact fx46 mass. Lane t owns slots [8t, 8t+8). Returns the winning slot, or
+// -1 at zero total mass.
 template <typename W>
-__device__ int pick_slot(Shared& sh, int n, float u, W weight) {
+__device__ int pick_slot(RowSh& sh, int n, float u, W weight) {
   const int t = threadIdx.x;
   const int s0 = kSlotsPerLane * t;
   uint64_t sum = 0;
@@ -773,9 +811,9 @@ __device__ int pick_slot(Shared& sh, int n, float u, W weight) {
 // Dense inverse-CDF pick over a whole row whose masses weight(idx) are
 // computed on the fly. Lane t owns a contiguous index range.
 template <typename W>
-__device__ int64_t pick_dense(Shared& sh, int vocab, float u, W weight) {
+__device__ int64_t pick_dense(RowSh& sh, int vocab, float u, W weight) {
   const int t = threadIdx.x;
-  const int per = (vocab + kCB - 1) / kCB;
+  const int per = (vocab + kRB - 1) / kRB;
   const int a = t * per < vocab ? t * per : vocab;
   const int b = a + per < vocab ? a + per : vocab;
   uint64_t sum = 0;
@@ -801,51 +839,57 @@ __device__ int64_t pick_dense(Shared& sh, int vocab, float u, W weight) {
   return static_cast<int64_t>(sh.u64s[3]);
 }
 
-// Exact select over every element of the row (the candidates did not hold the
-// cutoff): p recomputed from the re-read logits, g_j in fs.g[0]. When keep is
-// set, leaves the support {p >= c} in index order in fs.slot (as idx << 32 |
-// bits(p)) and returns its size, or -1 if it does not fit. Out of line, with
-// plain arguments, so the common path's registers are unaffected.
+// Exact select over every element of the row of set `set` (its candidates
+// did not hold the cutoff): p recomputed from the re-read logits with the
+// set's g_j. When keep is set, leaves the support {p >= c} in index order in
+// sh.slot[set] (as idx << 32 | bits(p)) and returns its size, or -1 if it does
+// not fit. Out of line, with plain arguments, so the common path's registers
+// are unaffected.
 template <int DT>
-__device__ __noinline__ int slow_select(Shared& sh, const char* rowp, const uint32_t* bm, float c, float pen,
+__device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
                                         float inv_pen, int vocab, uint64_t thr, bool keep, float* cutoff,
                                         uint64_t* mass_fx) {
-  FinSh& fs = sh.f;
-  const int t = threadIdx.x;
-  const float* mcj = fs.mcj[0];
-  const float* gj = fs.g[0];
+  const int t = threadIdx.x, wid = t / kWave;
+  const float* mcj = sh.mcj[set];
+  const float* gj = sh.g[set];
   auto pval = [&](int i) { return p_elem<DT>(rowp, bm, c, pen, inv_pen, mcj, gj, i); };
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
   __syncthreads();
-  float cc;
-  uint64_t mfx;
-  const bool ok = radix_select(sh, thr, [&](auto f) {
-    for (int i = t; i < vocab; i += kCB) {
+#pragma unroll
+  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
+  __syncthreads();
+  const uint64_t thr1[1] = {thr};
+  bool found[1];
+  float cc1[1];
+  uint64_t mfx1[1];
+  radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
+    for (int i = t; i < vocab; i += kRB) {
       const float pv = pval(i);
       f(__float_as_uint(pv), fx46(pv));
     }
-  }, &cc, &mfx);
-  if (!ok) {
+  }, found, cc1, mfx1);
+  float cc = cc1[0];
+  uint64_t mfx = mfx1[0];
+  if (!found[0]) {
     // Total mass below the threshold: keep the whole row (cutoff = min p).
     float mn = __builtin_inff();
     uint64_t tot = 0;
-    for (int i = t; i < vocab; i += kCB) {
+    for (int i = t; i < vocab; i += kRB) {
       const float pv = pval(i);
       mn = fminf(mn, pv);
       tot += fx46(pv);
     }
     mn = wave_max_f32(-mn);
-    if ((t & (kWave - 1)) == 0) sh.f32s[t / kWave] = mn;
-    tot = block_sum(tot, sh.red);
-    cc = -nmax(nmax(sh.f32s[0], sh.f32s[1]), nmax(sh.f32s[2], sh.f32s[3]));
-    mfx = tot;
+    if ((t & (kWave - 1)) == 0) sh.f32s[set][wid] = mn;
+    uint64_t all;
+    (void)block_excl_scan(tot, sh.red, &all);
+    cc = -nmax(nmax(sh.f32s[set][0], sh.f32s[set][1]), nmax(sh.f32s[set][2], sh.f32s[set][3]));
+    mfx = all;
     __syncthreads();
   }
   *cutoff = cc;
   *mass_fx = mfx;
   if (!keep) return -1;
-  const int per = (vocab + kCB - 1) / kCB;
+  const int per = (vocab + kRB - 1) / kRB;
   const int a = t * per < vocab ? t * per : vocab;
   const int b = a + per < vocab ? a + per : vocab;
   uint64_t cnt = 0;
@@ -856,7 +900,7 @@ __device__ __noinline__ int slow_select(Shared& sh, const char* rowp, const uint
   int pos = static_cast<int>(ex);
   for (int i = a; i < b; ++i) {
     const float pv = pval(i);
-    if (pv >= cc) fs.slot[pos++] = (static_cast<uint64_t>(i) << 32) | __float_as_uint(pv);
+    if (pv >= cc) sh.slot[set][pos++] = (static_cast<uint64_t>(i) << 32) | __float_as_uint(pv);
   }
   __syncthreads();
   return static_cast<int>(total);
@@ -867,322 +911,320 @@ __device__ __forceinline__ uint64_t load_slot(const SampParams& p, int64_t r, in
   return p.cands[(r * p.nch + (s >> p.cap_log2)) * kChunkCand + (s & (p.cap - 1))];
 }
 
-__device__ __forceinline__ bool slot_valid(const FinSh& fs, int slot, const SampParams& p, int s) {
-  return (s & (p.cap - 1)) < static_cast<int>(fs.n[slot][s >> p.cap_log2]);
+__device__ __forceinline__ bool slot_valid(const RowSh& sh, int set, const SampParams& p, int s) {
+  return (s & (p.cap - 1)) < static_cast<int>(sh.n[set][s >> p.cap_log2]);
 }
 
-// Inverse-CDF draw over this workgroup's own row (fs.slot holds idx | bits(p)
-// of n slots, fs.g[0] / fs.mcj[0] the row's scales): weights fx46(P), P the
-// filtered, renormalised probability; the whole row when it is dense.
+// Finalisation of NS rows side by side (set s = row r[s]): scales, p of the
+// candidates into sh.slot[s] (idx << 32 | bits(p), 0 for empty slots), the
+// exact top-p cutoff (candidates, or the re-streamed row when they do not hold
+// it). after_p() runs once the slots are written, before the selects, so
+// loads issued there overlap them. Outputs the row statistics, the filtered
+// probability of each row's draft token (-1 if the row has none) and, for a
+// row that took the slow path with keep_support, the size of its support.
+template <int DT, int NS, typename After>
+__device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)[NS], bool keep_support,
+                              RowStat (&st)[NS], float (&P_tok)[NS], int (&n_sup)[NS], After after_p) {
+  const int t = threadIdx.x, wid = t / kWave;
+  const int nch = p.nch;
+  const int nslots = nch * p.cap;
+  float top_p[NS];
+  bool unf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    top_p[s] = p.top_p_rows ? p.top_p_rows[r[s]] : p.top_p;
+    unf[s] = !(top_p[s] < 1.0f);
+  }
+  // 1. chunk records (wave s: row s) and candidate slots (strided), in flight together
+  ChunkRec ra{}, rb{};
+  if (wid < NS) load_recs(p, wid == 0 ? r[0] : r[NS - 1], &ra, &rb);
+  uint64_t cv[NS][kSlotsPerLane];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      cv[s][q] = (!unf[s] && sl < nslots) ? load_slot(p, r[s], sl) : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kBinsPerLane; ++q) sh.H[s][kBinsPerLane * t + q] = 0;
+  }
+  // 2. row scales (wave s: row s)
+  if (wid < NS) {
+    const RowScale rs = row_scale(sh, wid, ra, rb, nch);
+    if ((t & (kWave - 1)) == 0) {
+      sh.f32s[wid][0] = rs.mcmax;
+      sh.f32s[wid][1] = rs.s;
+      sh.f32s[wid][2] = rs.p_bound;
+      sh.f32s[wid][3] = rs.has_tok ? rs.p_tok : -1.0f;
+    }
+  }
+  __syncthreads();
+  // 3. p of the candidates, kept in registers and in sh.slot
+  float pv[NS][kSlotsPerLane];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      pv[s][q] = 0.0f;
+      if (!unf[s] && sl < nslots && slot_valid(sh, s, p, sl))
+        pv[s][q] = __uint_as_float(static_cast<uint32_t>(cv[s][q])) * sh.g[s][sl >> p.cap_log2];
+      if (sl < nslots) sh.slot[s][sl] = ((cv[s][q] >> 32) << 32) | __float_as_uint(pv[s][q]);
+    }
+  }
+  after_p();
+  // 4. cutoffs
+  uint64_t thr[NS];
+  bool found[NS];
+  float cut[NS];
+  uint64_t mfx[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) thr[s] = unf[s] ? 0 : fx46(top_p[s]);
+  bool any = false;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) any = any || !unf[s];
+  if (any) {
+    radix_select_n<NS>(sh, 0, thr, [&](int s, auto f) {
+#pragma unroll
+      for (int q = 0; q < kSlotsPerLane; ++q) {
+        const float x = pv[s][q];
+        if (x > 0.0f) f(__float_as_uint(x), fx46(x));
+      }
+    }, found, cut, mfx);
+  }
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    st[s].mcmax = sh.f32s[s][0];
+    st[s].s = sh.f32s[s][1];
+    st[s].flags = unf[s] ? (kFlagUnfiltered | kFlagDense) : 0u;
+    st[s].cutoff = 0.0f;
+    st[s].mass_fx = 0;
+    n_sup[s] = nslots;
+    const float p_bound = sh.f32s[s][2];
+    if (!unf[s]) {
+      if (found[s] && cut[s] > p_bound) {
+        st[s].cutoff = cut[s];
+        st[s].mass_fx = mfx[s];
+      } else {
+        st[s].flags |= kFlagSlow;
+        const int64_t g = r[s] / p.rpg;
+        const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
+        n_sup[s] = slow_select<DT>(sh, s, row_of(p, g, static_cast<int>(r[s] - g * p.rpg)), bm, p.c, p.pen, p.inv_pen,
+                                   p.vocab, thr[s], keep_support, &st[s].cutoff, &st[s].mass_fx);
+        if (!keep_support || n_sup[s] < 0) st[s].flags |= kFlagDense;
+      }
+    }
+    st[s].mass = unf[s] ? 1.0f : mass_to_f32(st[s].mass_fx);
+    const float pt = sh.f32s[s][3];
+    P_tok[s] = pt < 0.0f ? -1.0f : (unf[s] ? pt : (pt >= st[s].cutoff ? pt / st[s].mass : 0.0f));
+    st[s].p_tok = P_tok[s] < 0.0f ? 0.0f : P_tok[s];
+  }
+}
+
+// Inverse-CDF draw over the row of set `set` (its slots hold idx | bits(p),
+// n of them, sh.g / sh.mcj its scales): weights fx46(P), P the filtered,
+// renormalised probability; the whole row when it is dense.
 template <int DT>
-__device__ int64_t own_draw(const SampParams& p, Shared& sh, const RowStat& st, int n, float u, const char* rowp,
-                            const uint32_t* bm) {
-  FinSh& fs = sh.f;
+__device__ int64_t own_draw(const SampParams& p, RowSh& sh, int set, const RowStat& st, int n, float u,
+                            const char* rowp, const uint32_t* bm) {
   const bool unf = st.flags & kFlagUnfiltered;
+  const float cc = st.cutoff, mass = st.mass;
   if (!(st.flags & kFlagDense)) {
-    const float cc = st.cutoff, mass = st.mass;
     const int win = pick_slot(sh, n, u, [&](int s) {
-      const float x = __uint_as_float(static_cast<uint32_t>(fs.slot[s]));
+      const float x = __uint_as_float(static_cast<uint32_t>(sh.slot[set][s]));
       return x >= cc && x > 0.0f ? fx46(x / mass) : 0ull;
     });
-    return win < 0 ? 0 : static_cast<int64_t>(fs.slot[win] >> 32);
+    return win < 0 ? 0 : static_cast<int64_t>(sh.slot[set][win] >> 32);
   }
-  const float cc = st.cutoff, mass = st.mass;
   return pick_dense(sh, p.vocab, u, [&](int i) {
-    const float x = p_elem<DT>(rowp, bm, p.c, p.pen, p.inv_pen, fs.mcj[0], fs.g[0], i);
+    const float x = p_elem<DT>(rowp, bm, p.c, p.pen, p.inv_pen, sh.mcj[set], sh.g[set], i);
     return fx46(unf ? x : (x >= cc ? x / mass : 0.0f));
   });
 }
 
-// Residual draw for draft position i of group g: normalize(max(P_i - Q_i, 0))
-// (fallback normalize(P_i), rejection.py:60-69) with the uniform u[g, k+i].
-// P_i comes from the target row's candidates (already in fs.slot / fs.g[0]
-// when `own`, i.e. this workgroup finalised the target row); Q_i is
-// recomputed from the draft logits at the support indices.
-template <int DT>
-__device__ int64_t residual_draw(const SampParams& p, Shared& sh, int64_t g, int i, bool own) {
-  FinSh& fs = sh.f;
-  const int k = p.k, rpg = 2 * k + 1, nch = p.nch, nslots = nch * p.cap;
-  const int t = threadIdx.x, wid = t / kWave;
-  const int64_t rt = g * rpg + i, rd = g * rpg + k + 1 + i;
-  // 1. both rows' statistics, chunk records, and the target's candidates
-  if (t < 8) fs.statw[t] = load_sc64(reinterpret_cast<const uint64_t*>(p.stats + (t < 4 ? rt : rd)) + (t & 3));
-  ChunkRec rt_a{}, rt_b{}, rd_a{}, rd_b{};
-  if (wid == 0) {
-    load_recs(p, rd, &rd_a, &rd_b);
-    if (!own) load_recs(p, rt, &rt_a, &rt_b);
-  }
-  if (!own) {
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int s = t + q * kCB;
-      if (s < nslots) fs.slot[s] = load_slot(p, rt, s);
-    }
-  }
-  __syncthreads();
-  const RowStat st_t = stat_of(fs.statw[0], fs.statw[1], fs.statw[2], fs.statw[3]);
-  const RowStat st_d = stat_of(fs.statw[4], fs.statw[5], fs.statw[6], fs.statw[7]);
-  if (wid == 0) {
-    if (!own) row_g(fs, 0, rt_a, rt_b, nch, st_t.mcmax, st_t.s);
-    row_g(fs, 1, rd_a, rd_b, nch, st_d.mcmax, st_d.s);
-  }
-  __syncthreads();
-  const bool unf_t = st_t.flags & kFlagUnfiltered;
-  const bool unf_d = st_d.flags & kFlagUnfiltered;
-  const float u = p.uniforms[g * rpg + k + i];
-  const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
-  const char* drow = row_of(p, g, k + 1 + i);
-  auto Qof = [&](float l, int j) {
-    const float x = exp2q(__builtin_fmaf(l, p.c, -fs.mcj[1][j])) * fs.g[1][j];
-    return unf_d ? x : (x >= st_d.cutoff ? x / st_d.mass : 0.0f);
-  };
-  if (!(st_t.flags & kFlagDense)) {
-    // P over the target's support, the draft logits there gathered at once
-    float P[kSlotsPerLane], lq[kSlotsPerLane];
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int s = t + q * kCB;
-      P[q] = 0.0f;
-      lq[q] = 0.0f;
-      if (s < nslots && slot_valid(fs, 0, p, s)) {
-        const uint64_t v = fs.slot[s];
-        const float pv = own ? __uint_as_float(static_cast<uint32_t>(v))
-                             : __uint_as_float(static_cast<uint32_t>(v)) * fs.g[0][s >> p.cap_log2];
-        if (pv >= st_t.cutoff && pv > 0.0f) {
-          P[q] = pv / st_t.mass;
-          lq[q] = load_elem<DT>(drow, static_cast<int64_t>(v >> 32));
-        }
-      }
-    }
-    float D[kSlotsPerLane];
-    uint64_t dsum = 0, psum = 0;
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int s = t + q * kCB;
-      D[q] = 0.0f;
-      if (P[q] > 0.0f) {
-        const int idx = static_cast<int>(fs.slot[s] >> 32);
-        float l = lq[q];
-        if (bm && bit_of(bm, idx)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
-        const float dv = P[q] - Qof(l, idx >> kChunkShift);
-        D[q] = dv > 0.0f ? dv : 0.0f;
-        dsum += fx46(D[q]);
-        psum += fx46(P[q]);
-      }
-    }
-    const uint64_t d_fx = block_sum(dsum, sh.red);
-    const uint64_t p_fx = block_sum(psum, sh.red);
-    const bool use_d = d_fx > 0;
-    const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int s = t + q * kCB;
-      if (s < nslots) fs.w[s] = (use_d ? D[q] : P[q]) / den;
-    }
-    __syncthreads();
-    const int win = pick_slot(sh, nslots, u, [&](int s) { return fx46(fs.w[s]); });
-    return win < 0 ? 0 : static_cast<int64_t>(fs.slot[win] >> 32);
-  }
-  // dense target row: the whole vocabulary
-  const char* trow = row_of(p, g, i);
-  auto Pof = [&](int x) {
-    const float pv = p_elem<DT>(trow, bm, p.c, p.pen, p.inv_pen, fs.mcj[0], fs.g[0], x);
-    return unf_t ? pv : (pv >= st_t.cutoff ? pv / st_t.mass : 0.0f);
-  };
-  auto Qat = [&](int x) {
-    float l = load_elem<DT>(drow, x);
-    if (bm && bit_of(bm, x)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
-    return Qof(l, x >> kChunkShift);
-  };
-  uint64_t dsum = 0, psum = 0;
-  {
-    const int per = (p.vocab + kCB - 1) / kCB;
-    const int i0 = t * per < p.vocab ? t * per : p.vocab;
-    const int i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
-    for (int x = i0; x < i1; ++x) {
-      const float pj = Pof(x);
-      const float dj = pj - Qat(x);
-      dsum += fx46(dj > 0.0f ? dj : 0.0f);
-      psum += fx46(pj);
-    }
-  }
-  const uint64_t d_fx = block_sum(dsum, sh.red);
-  const uint64_t p_fx = block_sum(psum, sh.red);
-  const bool use_d = d_fx > 0;
-  const float den = use_d ? mass_to_f32(d_fx) : (p_fx > 0 ? mass_to_f32(p_fx) : 1.0f);
-  return pick_dense(sh, p.vocab, u, [&](int x) {
-    const float pj = Pof(x);
-    float v = pj;
-    if (use_d) {
-      const float dj = pj - Qat(x);
-      v = dj > 0.0f ? dj : 0.0f;
-    }
-    return fx46(v / den);
-  });
-}
-
-// The accept chain of group g once every draw is published: the first
-// rejected position a (u < min(1, P/Q) per position, sampler.py:451-452),
-// then the accepted drafts, the draw of position a, and -1 after it.
-__device__ void accept_chain(const SampParams& p, Shared& sh, int64_t g) {
-  FinSh& fs = sh.f;
-  const int k = p.k, rpg = 2 * k + 1;
+// Publish draw word w of group g and arrive on its counter; the last of the
+// k+1 arrivals runs the accept chain: a = the first position whose accept
+// bit (bit 63) is clear, tokens = the accepted drafts, draw a, then -1.
+__device__ void publish_draw(const SampParams& p, RowSh& sh, int64_t g, int i, uint64_t word) {
+  const int k = p.k;
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  const int64_t r0 = g * rpg;
-  if (t < rpg) fs.tokp[t] = hi_f(load_sc64(reinterpret_cast<const uint64_t*>(p.stats + r0 + t) + 2));
-  if (t <= k) fs.tokd[t] = static_cast<int64_t>(load_sc64(reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1) + t));
-  int64_t x = -1;
-  float ux = 0.0f;
-  if (wid == 0 && lane < k) {
-    x = p.draft_tokens[g * k + lane];
-    ux = p.uniforms[g * rpg + lane];
+  if (t == 0) {
+    store_sc64(reinterpret_cast<uint64_t*>(p.draws) + g * (k + 1) + i, word);
+    drain_stores();
+    uint32_t* ctr = p.grp_cnt + g * kCounterStride;
+    const uint32_t prev = atomic_arrive(ctr);
+    const bool last = prev == static_cast<uint32_t>(k);
+    if (last) store_sc(ctr, 0u);
+    sh.u32s[7] = last ? 1u : 0u;
   }
   __syncthreads();
+  if (!sh.u32s[7]) return;
+  if (t <= k) sh.draws[t] = load_sc64(reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1) + t);
+  int64_t x = -1;
+  if (wid == 0 && lane < k) x = p.draft_tokens[g * k + lane];
+  __syncthreads();
   if (wid == 0) {
-    const bool valid = x >= 0 && x < p.vocab;
-    const bool ok = lane < k && valid && accept_draw(ux, fs.tokp[lane], fs.tokp[k + 1 + lane]);
-    const uint64_t bad = __ballot(lane < k && !ok);
+    const uint64_t bad = __ballot(lane < k && !(sh.draws[lane] >> 63));
     const int a = bad ? __builtin_ctzll(bad) : k;
+    const int64_t da = static_cast<int64_t>(sh.draws[a] & ~(1ull << 63));
     int64_t* out = p.tokens + g * (k + 1);
     if (lane < a) out[lane] = x;
-    if (lane == a) out[lane] = fs.tokd[a];
+    if (lane == a) out[lane] = da;
     if (lane > a && lane <= k) out[lane] = -1;
-    if (k >= kWave && lane == 0) {
-      for (int j = kWave; j <= k; ++j) out[j] = j < a ? p.draft_tokens[g * k + j] : (j == a ? fs.tokd[a] : -1);
-    }
+    if (k >= kWave && lane == 0) out[k] = a == k ? da : -1;
     if (lane == 0) p.accept_len[g] = a;
   }
 }
 
-// Row finalisation: one workgroup per row.
-template <int DT, int MODE>
-__global__ __launch_bounds__(kCB) void row_kernel(const SampParams p) {
-  __shared__ Shared sh;
-  FinSh& fs = sh.f;
-  const int r = blockIdx.x;
-  const int t = threadIdx.x, wid = t / kWave;
-  const int nch = p.nch;
-  const int64_t g = r / p.rpg;
-  const int jr = r - static_cast<int>(g) * p.rpg;
-  const int nslots = nch * p.cap;
-  const float top_p = p.top_p_rows ? p.top_p_rows[r] : p.top_p;
-  const bool unfiltered = !(top_p < 1.0f);
-  const char* rowp = row_of(p, g, jr);
+// Spec mode: one workgroup per (batch element g, position i). i < k: the
+// target row i and the draft row i, finalised side by side; the accept bit
+// of draft token x_i (u < min(1, P/Q), sampler.py:451-452) and the residual
+// draw normalize(max(P - Q, 0)) (fallback normalize(P), rejection.py:60-69)
+// with u[g, k+i]. i == k: the bonus row's draw with u[g, 2k].
+template <int DT>
+__global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
+  __shared__ RowSh sh;
+  const int k = p.k, rpg = 2 * k + 1;
+  const int64_t g = blockIdx.x / (k + 1);
+  const int i = static_cast<int>(blockIdx.x - g * (k + 1));
+  const int t = threadIdx.x;
+  const int nslots = p.nch * p.cap;
   const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
+  if (i == k) {
+    const int64_t r[1] = {g * rpg + k};
+    RowStat st[1];
+    float P_tok[1];
+    int n_sup[1];
+    finalize_rows<DT, 1>(p, sh, r, false, st, P_tok, n_sup, [] {});
+    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, p.uniforms[g * rpg + 2 * k], row_of(p, g, k), bm);
+    publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
+    return;
+  }
+  const int64_t r[2] = {g * rpg + i, g * rpg + k + 1 + i};
+  const char* trow = row_of(p, g, i);
+  const char* drow = row_of(p, g, k + 1 + i);
+  // the draft logits at the target's candidates, gathered during the selects
+  float lq[kSlotsPerLane];
+  auto gather = [&] {
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      lq[q] = 0.0f;
+      if (sl < nslots && slot_valid(sh, 0, p, sl)) {
+        const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
+        lq[q] = load_elem<DT>(drow, idx < p.vocab ? idx : 0);
+      }
+    }
+  };
+  RowStat st[2];
+  float P_tok[2];
+  int n_sup[2];
+  finalize_rows<DT, 2>(p, sh, r, false, st, P_tok, n_sup, gather);
+  const RowStat& st_t = st[0];
+  const RowStat& st_d = st[1];
+  // accept bit of x_i
+  const int64_t x = p.draft_tokens[g * k + i];
+  const bool acc = x >= 0 && x < p.vocab && accept_draw(p.uniforms[g * rpg + i], P_tok[0] < 0.0f ? 0.0f : P_tok[0],
+                                                        P_tok[1] < 0.0f ? 0.0f : P_tok[1]);
+  const float u = p.uniforms[g * rpg + k + i];
+  const bool unf_t = st_t.flags & kFlagUnfiltered;
+  const bool unf_d = st_d.flags & kFlagUnfiltered;
+  auto Qof = [&](float l, int idx) {
+    if (bm && bit_of(bm, idx)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
+    const int j = idx >> kChunkShift;
+    const float q = exp2q(__builtin_fmaf(l, p.c, -sh.mcj[1][j])) * sh.g[1][j];
+    return unf_d ? q : (q >= st_d.cutoff ? q / st_d.mass : 0.0f);
+  };
+  int64_t token;
+  if (!(st_t.flags & kFlagDense)) {
+    float P[kSlotsPerLane], D[kSlotsPerLane];
+    uint64_t sums[2] = {0, 0};  // fx46 masses of D and of P
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      P[q] = D[q] = 0.0f;
+      if (sl < nslots) {
+        const uint64_t v = sh.slot[0][sl];
+        const float pv = __uint_as_float(static_cast<uint32_t>(v));
+        if (pv > 0.0f && pv >= st_t.cutoff) {
+          P[q] = pv / st_t.mass;
+          const float dv = P[q] - Qof(lq[q], static_cast<int>(v >> 32));
+          D[q] = dv > 0.0f ? dv : 0.0f;
+          sums[0] += fx46(D[q]);
+          sums[1] += fx46(P[q]);
+        }
+      }
+    }
+    uint64_t ex[2], tot[2];
+    block_excl_scan_n<2>(sums, sh.red, ex, tot);
+    const bool use_d = tot[0] > 0;
+    const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      if (sl < nslots) sh.w[sl] = (use_d ? D[q] : P[q]) / den;
+    }
+    __syncthreads();
+    const int win = pick_slot(sh, nslots, u, [&](int s) { return fx46(sh.w[s]); });
+    token = win < 0 ? 0 : static_cast<int64_t>(sh.slot[0][win] >> 32);
+  } else {
+    // dense target row: the whole vocabulary
+    auto Pof = [&](int y) {
+      const float pv = p_elem<DT>(trow, bm, p.c, p.pen, p.inv_pen, sh.mcj[0], sh.g[0], y);
+      return unf_t ? pv : (pv >= st_t.cutoff ? pv / st_t.mass : 0.0f);
+    };
+    auto Qat = [&](int y) { return Qof(load_elem<DT>(drow, y), y); };
+    uint64_t sums[2] = {0, 0};
+    {
+      const int per = (p.vocab + kRB - 1) / kRB;
+      const int i0 = t * per < p.vocab ? t * per : p.vocab;
+      const int i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
+      for (int y = i0; y < i1; ++y) {
+        const float pj = Pof(y);
+        const float dj = pj - Qat(y);
+        sums[0] += fx46(dj > 0.0f ? dj : 0.0f);
+        sums[1] += fx46(pj);
+      }
+    }
+    uint64_t ex[2], tot[2];
+    block_excl_scan_n<2>(sums, sh.red, ex, tot);
+    const bool use_d = tot[0] > 0;
+    const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
+    token = pick_dense(sh, p.vocab, u, [&](int y) {
+      const float pj = Pof(y);
+      float v = pj;
+      if (use_d) {
+        const float dj = pj - Qat(y);
+        v = dj > 0.0f ? dj : 0.0f;
+      }
+      return fx46(v / den);
+    });
+  }
+  publish_draw(p, sh, g, i, static_cast<uint64_t>(token) | (acc ? 1ull << 63 : 0ull));
+}
 
-  // 1. chunk records (wave 0) and candidate slots (strided), in flight together
-  ChunkRec ra{}, rb{};
-  if (wid == 0) load_recs(p, r, &ra, &rb);
-  uint64_t cv[kSlotsPerLane];
-#pragma unroll
-  for (int q = 0; q < kSlotsPerLane; ++q) {
-    const int s = t + q * kCB;
-    cv[q] = (!unfiltered && s < nslots) ? load_slot(p, r, s) : 0;
-  }
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) fs.H[kBinsPerLane * t + q] = 0;
-  // 2. row scales
-  if (wid == 0) {
-    const RowScale rs = row_scale(fs, 0, ra, rb, nch);
-    if (t == 0) {
-      sh.f32s[4] = rs.mcmax;
-      sh.f32s[5] = rs.s;
-      sh.f32s[6] = rs.p_bound;
-      sh.f32s[7] = rs.has_tok ? rs.p_tok : -1.0f;
-    }
-  }
-  __syncthreads();
-  const float mcmax = sh.f32s[4], s_row = sh.f32s[5], p_bound = sh.f32s[6], p_tok = sh.f32s[7];
-  // 3. p of the candidates, kept in registers and in fs.slot
-  float pv[kSlotsPerLane];
-#pragma unroll
-  for (int q = 0; q < kSlotsPerLane; ++q) {
-    const int s = t + q * kCB;
-    pv[q] = 0.0f;
-    if (!unfiltered && s < nslots && slot_valid(fs, 0, p, s))
-      pv[q] = __uint_as_float(static_cast<uint32_t>(cv[q])) * fs.g[0][s >> p.cap_log2];
-    if (s < nslots) fs.slot[s] = ((cv[q] >> 32) << 32) | __float_as_uint(pv[q]);
-  }
-  float cutoff = 0.0f;
-  uint64_t mass_fx = 0;
-  uint32_t flags = unfiltered ? (kFlagUnfiltered | kFlagDense) : 0u;
-  int n_sup = nslots;
-  if (!unfiltered) {
-    const uint64_t thr = fx46(top_p);
-    float c;
-    uint64_t mfx;
-    const bool ok = radix_select(sh, thr, [&](auto f) {
-#pragma unroll
-      for (int q = 0; q < kSlotsPerLane; ++q) {
-        const float x = pv[q];
-        if (x > 0.0f) f(__float_as_uint(x), fx46(x));
-      }
-    }, &c, &mfx);
-    if (ok && c > p_bound) {
-      cutoff = c;
-      mass_fx = mfx;
-    } else {
-      flags |= kFlagSlow;
-      __syncthreads();
-      n_sup = slow_select<DT>(sh, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, thr, MODE == kModeSample, &cutoff,
-                              &mass_fx);
-      if (MODE != kModeSample || n_sup < 0) flags |= kFlagDense;
-    }
-  }
-  RowStat st;
-  st.mcmax = mcmax;
-  st.s = s_row;
-  st.cutoff = cutoff;
-  st.mass = unfiltered ? 1.0f : mass_to_f32(mass_fx);
-  st.flags = flags;
-  st.p_tok = 0.0f;
-  st.mass_fx = mass_fx;
-  if (p_tok >= 0.0f) st.p_tok = unfiltered ? p_tok : (p_tok >= cutoff ? p_tok / st.mass : 0.0f);
-
-  if constexpr (MODE == kModeSpec) {
-    const int k = p.k;
-    if (t == 0) {
-      put_stat(p.stats + r, st);
-      drain_stores();
-    }
-    // Pair (target i, draft i): the second to finish draws position i's
-    // residual; the bonus row draws the bonus token. Each draw arrives on the
-    // group's counter; the last arrival runs the accept chain.
-    bool draw_here = jr == k;
-    const int i = jr < k ? jr : jr - k - 1;
-    if (jr != k) {
-      if (t == 0) {
-        uint32_t* ctr = p.row_cnt + (g * p.rpg + i) * kCounterStride;
-        const uint32_t prev = atomic_arrive(ctr);
-        if (prev == 1u) store_sc(ctr, 0u);
-        sh.u32s[6] = prev == 1u ? 1u : 0u;
-      }
-      __syncthreads();
-      draw_here = sh.u32s[6] != 0u;
-    }
-    if (draw_here) {
-      const int64_t tok = jr == k ? own_draw<DT>(p, sh, st, nslots, p.uniforms[g * p.rpg + 2 * k], rowp, bm)
-                                  : residual_draw<DT>(p, sh, g, i, jr < k);
-      if (t == 0) {
-        store_sc64(reinterpret_cast<uint64_t*>(p.draws) + g * (k + 1) + (jr == k ? k : i), static_cast<uint64_t>(tok));
-        drain_stores();
-        uint32_t* ctr = p.grp_cnt + g * kCounterStride;
-        const uint32_t prev = atomic_arrive(ctr);
-        const bool last = prev == static_cast<uint32_t>(k);
-        if (last) store_sc(ctr, 0u);
-        sh.u32s[7] = last ? 1u : 0u;
-      }
-      __syncthreads();
-      if (sh.u32s[7]) accept_chain(p, sh, g);
-    }
-  } else if constexpr (MODE == kModeSample) {
-    const int64_t token = own_draw<DT>(p, sh, st, (flags & kFlagSlow) ? n_sup : nslots, p.row_uniforms[r], rowp, bm);
-    if (t == 0) p.row_tokens[r] = token;
+// Sample and dense modes: one workgroup per row.
+template <int DT, int MODE>
+__global__ __launch_bounds__(kRB) void row_kernel(const SampParams p) {
+  __shared__ RowSh sh;
+  const int64_t r[1] = {blockIdx.x};
+  const int t = threadIdx.x;
+  RowStat st[1];
+  float P_tok[1];
+  int n_sup[1];
+  finalize_rows<DT, 1>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [] {});
+  if constexpr (MODE == kModeSample) {
+    const uint32_t* bm = p.use_pen ? p.bitmap + r[0] * p.bm_words : nullptr;
+    const int64_t token = own_draw<DT>(p, sh, 0, st[0], (st[0].flags & kFlagSlow) ? n_sup[0] : p.nch * p.cap,
+                                       p.row_uniforms[r[0]], row_of(p, r[0], 0), bm);
+    if (t == 0) p.row_tokens[r[0]] = token;
   } else {
     if (t == 0) {
-      p.stats[r] = st;
-      if (p.cutoff_out) p.cutoff_out[r] = unfiltered ? 0.0f : cutoff;
-      if (p.mass_out) p.mass_out[r] = st.mass;
+      p.stats[r[0]] = st[0];
+      const bool unf = st[0].flags & kFlagUnfiltered;
+      if (p.cutoff_out) p.cutoff_out[r[0]] = unf ? 0.0f : st[0].cutoff;
+      if (p.mass_out) p.mass_out[r[0]] = st[0].mass;
     }
   }
 }
@@ -1277,8 +1319,17 @@ template <int DT, int MODE>
 void launch_dt(const SampParams& p, int64_t groups, int64_t rows, hipStream_t st) {
   if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(groups)), dim3(kBmB), 0, st, p);
   const int wgs = static_cast<int>(device_cu_count()) * kChunkWavesPerCu;
-  hipLaunchKernelGGL((chunk_kernel<DT>), dim3(p.items < wgs ? p.items : wgs), dim3(kWave), 0, st, p);
-  hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kCB), 0, st, p);
+  const dim3 grid(p.items < wgs ? p.items : wgs);
+  if (p.use_pen) {
+    hipLaunchKernelGGL((chunk_kernel<DT, true>), grid, dim3(kWave), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((chunk_kernel<DT, false>), grid, dim3(kWave), 0, st, p);
+  }
+  if constexpr (MODE == kModeSpec) {
+    hipLaunchKernelGGL((spec_row_kernel<DT>), dim3(static_cast<unsigned>(groups * (p.k + 1))), dim3(kRB), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kRB), 0, st, p);
+  }
   if constexpr (MODE == kModeDense) {
     hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.items), dim3(kCB), 0, st, p);
   }

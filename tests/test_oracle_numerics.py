@@ -126,3 +126,18 @@ def test_philox_known_answers():
     u = philox.uniforms((1000,), seed=5)
     assert u.dtype == np.float32 and (u >= 0).all() and (u < 1).all()
     assert np.array_equal(philox.uniforms((10,), seed=5, offset=3), u[3:13])
+
+
+def test_exp2_polynomial_bound_for_candidate_scale():
+    """The chunk kernel keeps every e >= 1.41422 * 2^-K as a candidate and
+    relies on e < 1.41422 * 2^k whenever exp2q scaled by 2^k: the polynomial
+    must stay below 1.41422 on [-1/2, 1/2]. Exhaustive over the binary32
+    arguments of [1/4, 1/2] (where the maximum lies), sampled below."""
+    top = np.arange(np.float32(0.25).view(np.uint32), np.float32(0.5).view(np.uint32) + 1,
+                    dtype=np.uint32).view(np.float32)
+    low = np.linspace(-0.5, 0.25, 200001, dtype=np.float64).astype(np.float32)
+    for r in (top, low):
+        p = np.full_like(r, nm.EXP2_COEFFS[5])
+        for coef in nm.EXP2_COEFFS[4::-1]:
+            p = nm.fma32(p, r, coef)
+        assert float(p.max()) < 1.41422
