@@ -174,7 +174,10 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
         "config": {"workload": cfg.name, "batch": cfg.batch, "k": cfg.k, "vocab": cfg.vocab,
                    "temperature": cfg.temperature, "top_p": cfg.top_p, "penalty": cfg.penalty,
                    "input_sets": nsets, "input_set_bytes": nbytes,
-                   "kernel": "ls::sample_kernel<DT, spec>", "submission": "hipGraph of one launch per step"},
+                   "kernels": ("ls::bitmap_kernel + " if cfg.penalty != 1.0 else "")
+                   + "ls::chunk_kernel<DT, PEN> + ls::spec_row_kernel<DT>",
+                   "submission": "hipGraph of one ls_spec_verify call (%d launches) per step"
+                   % (3 if cfg.penalty != 1.0 else 2)},
         "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
         "acceptance_rate": accepted / (cfg.batch * cfg.k),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -236,8 +239,8 @@ def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
                    "vocab": cfg.vocab, "temperature": cfg.temperature, "top_p": cfg.top_p,
                    "kv_planes": kvc.planes, "kv_token_bytes": kvc.token_bytes, "page_size": kvc.page_size,
                    "input_sets": nsets, "logit_bytes": logit_bytes, "kv_commit_bytes": kv_bytes,
-                   "kernels": "ls::sample_kernel<DT, spec> + kv_plan_kernel + kv_copy_kernel",
-                   "submission": "hipGraph of three launches per step"},
+                   "kernels": "ls::chunk_kernel<DT, PEN> + ls::spec_row_kernel<DT> + kv_plan_kernel + kv_copy_kernel",
+                   "submission": "hipGraph of four launches per step"},
         "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
         "acceptance_rate": accepted / (cfg.batch * cfg.k),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -376,7 +379,9 @@ def main() -> int:
         return 2
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                    "data": "synthetic (seeded N(0,3^2) logits, draft = target + N(0,1), 1% planted ties)"})
-    kernel_name = {"C2": "greedy_kernel", "C3": "sample_kernel", "C4": "sample_kernel"}.get(args.config)
+    # Traffic summaries are per launch unit: the greedy kernel (C2), or the
+    # kernels of one ls_spec_verify call together (C3, C4).
+    kernel_name = {"C2": "greedy_kernel", "C3": "spec_verify", "C4": "spec_verify"}.get(args.config)
     if kernel_name:
         result["roofline"]["traffic"] = traffic_from_profile(kernel_name, args.config)
     if args.copy_calibration:

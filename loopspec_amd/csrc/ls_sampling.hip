@@ -509,6 +509,8 @@ struct RowSh {
   uint64_t u64s[8];
   uint32_t u32s[8];
   float f32s[2][4];
+  float slow_cut[2];
+  uint64_t slow_mass[2];
   uint64_t draws[64 + 1];
 };
 
@@ -843,12 +845,12 @@ __device__ int64_t pick_dense(RowSh& sh, int vocab, float u, W weight) {
 // did not hold the cutoff): p recomputed from the re-read logits with the
 // set's g_j. When keep is set, leaves the support {p >= c} in index order in
 // sh.slot[set] (as idx << 32 | bits(p)) and returns its size, or -1 if it does
-// not fit. Out of line, with plain arguments, so the common path's registers
-// are unaffected.
+// not fit. The cutoff and its fx46 mass go to sh.slow_cut / sh.slow_mass.
+// Out of line, with plain arguments and no pointers into the caller's frame,
+// so the common path's registers are unaffected.
 template <int DT>
 __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
-                                        float inv_pen, int vocab, uint64_t thr, bool keep, float* cutoff,
-                                        uint64_t* mass_fx) {
+                                        float inv_pen, int vocab, uint64_t thr, bool keep) {
   const int t = threadIdx.x, wid = t / kWave;
   const float* mcj = sh.mcj[set];
   const float* gj = sh.g[set];
@@ -886,8 +888,11 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
     mfx = all;
     __syncthreads();
   }
-  *cutoff = cc;
-  *mass_fx = mfx;
+  if (t == 0) {
+    sh.slow_cut[set] = cc;
+    sh.slow_mass[set] = mfx;
+  }
+  __syncthreads();
   if (!keep) return -1;
   const int per = (vocab + kRB - 1) / kRB;
   const int a = t * per < vocab ? t * per : vocab;
@@ -1011,7 +1016,9 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
         const int64_t g = r[s] / p.rpg;
         const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
         n_sup[s] = slow_select<DT>(sh, s, row_of(p, g, static_cast<int>(r[s] - g * p.rpg)), bm, p.c, p.pen, p.inv_pen,
-                                   p.vocab, thr[s], keep_support, &st[s].cutoff, &st[s].mass_fx);
+                                   p.vocab, thr[s], keep_support);
+        st[s].cutoff = sh.slow_cut[s];
+        st[s].mass_fx = sh.slow_mass[s];
         if (!keep_support || n_sup[s] < 0) st[s].flags |= kFlagDense;
       }
     }
@@ -1162,8 +1169,12 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
     const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
 #pragma unroll
     for (int q = 0; q < kSlotsPerLane; ++q) {
+      // both values in registers first: a select of the two arrays would
+      // otherwise become a select of their addresses, on the stack
+      float dq = D[q], pq = P[q];
+      asm volatile("" : "+v"(dq), "+v"(pq));
       const int sl = t + q * kRB;
-      if (sl < nslots) sh.w[sl] = (use_d ? D[q] : P[q]) / den;
+      if (sl < nslots) sh.w[sl] = (use_d ? dq : pq) / den;
     }
     __syncthreads();
     const int win = pick_slot(sh, nslots, u, [&](int s) { return fx46(sh.w[s]); });
