@@ -9,7 +9,7 @@
 // the maximum inside the winning vector, and the block reduces packed
 // (value, -index) keys. Segments meet in the fused epilogue without
 // same-address contention: each workgroup writes its key to its own slot with
-// a device-coherent store, drains it, and arrives on its batch element's
+// a device-coherent store and arrives on its batch element's
 // counter; the last arriver loads the element's keys, takes the per-row
 // maximum over segments and runs the accept-prefix scan.
 //
@@ -86,6 +86,10 @@ __device__ __forceinline__ uint64_t thread_argmax_vec(const u32x4* __restrict__ 
       const int j = J > 0 ? u : (j0 + u < n ? j0 + u : n - 1);
       d[u] = __builtin_nontemporal_load(p + static_cast<int64_t>(j) * BLOCK);
     }
+    // Every load of the batch is issued before any of them is consumed: the
+    // scheduler would otherwise interleave the first vectors' decoding with
+    // the issue and wait on them before the last loads leave.
+    __builtin_amdgcn_sched_barrier(0);
     // Seeding with the lane's first vector makes an all -inf share resolve to
     // its first element without a sentinel.
     if (j0 == 0) bestd = d[0];
@@ -132,47 +136,93 @@ __device__ __forceinline__ uint64_t thread_argmax_scalar(const char* row, int64_
   return besti < 0 ? 0 : argmax_key(best, static_cast<uint32_t>(besti));
 }
 
+// A published key is never zero (its low word is ~index with index < 2^31),
+// so an empty slot reads as 0. Keys are stored without waiting for the store
+// to complete before the arrival: the last arriver polls each slot until its
+// key is visible (every store it waits for was issued before the matching
+// arrival, so the wait ends; the poll count is bounded regardless) and clears
+// it for the next call.
+constexpr int kPollLimit = 1 << 22;
+
+__device__ __forceinline__ uint64_t take_key(uint64_t* slot) {
+  uint64_t v = load_sc64(slot);
+  for (int n = 0; v == 0 && n < kPollLimit; ++n) {
+    __builtin_amdgcn_s_sleep(1);
+    v = load_sc64(slot);
+  }
+  store_sc64(slot, 0);
+  return v;
+}
+
 // Runs on every lane of the last workgroup of group g (a block-uniform
-// branch). Lane i loads key i of the group's rows_per_group * splits keys with
-// a device-coherent load; row j's key is the maximum over its splits; lane 0
-// runs the scan and re-arms the group's counter.
+// branch). Row j's key is the maximum over its splits' keys. The
+// accept-prefix scan is lane-parallel: lane i compares draft position i, the
+// first mismatch comes from one ballot, and lane i writes output position i,
+// so no store waits on another. When the group has at most 64 keys, wave 0
+// alone does all of it in registers (no workgroup barrier).
 template <int BLOCK>
-__device__ void finalize_group(const GreedyParams& p, int64_t g, int64_t* ids, uint64_t* keys) {
-  const int lane = threadIdx.x;
-  const int nkeys = p.rows_per_group * p.splits;
-  const uint64_t* slots = p.slots + g * nkeys;
-  for (int i = lane; i < nkeys; i += BLOCK) keys[i] = load_sc64(slots + i);
-  __syncthreads();
-  for (int j = lane; j < p.rows_per_group; j += BLOCK) {
+__device__ void finalize_group(const GreedyParams& p, int64_t g, int own, uint64_t own_key, int64_t* ids,
+                               uint64_t* keys) {
+  const int t = threadIdx.x, lane = t & (kWave - 1);
+  const int k = p.k;
+  const int rpg = p.rows_per_group, splits = p.splits;
+  const int nkeys = rpg * splits;
+  uint64_t* slots = p.slots + g * nkeys;
+  // the thread that stored this workgroup's key clears it (same address, same
+  // thread: the stores land in program order)
+  if (t == 0) store_sc64(slots + own, 0);
+  if (nkeys <= kWave) {
+    if (t >= kWave) return;
+    const int64_t dtok = (k > 0 && !p.draft && lane < k) ? p.draft_tokens[g * k + lane] : -1;
+    // this workgroup's own key is taken from registers (its store may still be in flight)
+    const uint64_t key = lane == own ? own_key : (lane < nkeys ? take_key(slots + lane) : 0);
     uint64_t best = 0;
-    for (int s = 0; s < p.splits; ++s) best = keys[j * p.splits + s] > best ? keys[j * p.splits + s] : best;
+    for (int s = 0; s < splits; ++s) {
+      const uint64_t o = __shfl(key, lane < rpg ? lane * splits + s : 0);
+      best = o > best ? o : best;
+    }
+    const int64_t id = lane < rpg ? static_cast<int64_t>(argmax_key_index(best)) : -1;
+    if (lane == 0) store_sc(p.counters + g * kCounterStride, 0u);
+    if (k == 0) {
+      if (lane == 0) p.out[g] = id;
+      return;
+    }
+    // draft id of position lane: the draft row's argmax or the caller's id
+    const int64_t d = p.draft ? __shfl(id, lane < k ? k + 1 + lane : 0) : dtok;
+    const uint64_t bad = __ballot(lane < k && d != id);
+    const int a = bad ? __builtin_ctzll(bad) : k;
+    if (lane <= k) p.tokens[g * (k + 1) + lane] = lane <= a ? id : -1;
+    if (p.row_argmax) {
+      if (lane <= k) p.row_argmax[g * (2 * k + 1) + lane] = id;
+      if (lane < k) p.row_argmax[g * (2 * k + 1) + k + 1 + lane] = d;
+    }
+    if (lane == 0) p.accept_len[g] = a;
+    return;
+  }
+  // caller-supplied draft ids go where the draft rows' argmax would be
+  if (k > 0 && !p.draft && t < k) ids[k + 1 + t] = p.draft_tokens[g * k + t];
+  for (int i = t; i < nkeys; i += BLOCK) keys[i] = i == own ? own_key : take_key(slots + i);
+  __syncthreads();
+  for (int j = t; j < rpg; j += BLOCK) {
+    uint64_t best = 0;
+    for (int s = 0; s < splits; ++s) best = keys[j * splits + s] > best ? keys[j * splits + s] : best;
     ids[j] = argmax_key_index(best);
   }
   __syncthreads();
-  if (lane != 0) return;
-  store_sc(p.counters + g * kCounterStride, 0u);
-  if (p.k == 0) {
-    p.out[g] = ids[0];
+  if (t == 0) store_sc(p.counters + g * kCounterStride, 0u);
+  if (k == 0) {
+    if (t == 0) p.out[g] = ids[0];
     return;
   }
-  const int k = p.k;
-  int accepted = 0;
-  bool run = true;
-  for (int i = 0; i <= k; ++i) {
-    const int64_t t = ids[i];
-    const int64_t d = i < k ? (p.draft ? ids[k + 1 + i] : p.draft_tokens[g * k + i]) : -1;
-    p.tokens[g * (k + 1) + i] = run ? t : -1;
-    if (run && i < k && d == t) {
-      ++accepted;
-    } else {
-      run = false;
-    }
-    if (p.row_argmax) {
-      p.row_argmax[g * (2 * k + 1) + i] = t;
-      if (i < k) p.row_argmax[g * (2 * k + 1) + k + 1 + i] = d;
-    }
+  // every wave forms the same mask over draft positions 0..k-1 (k <= 64)
+  const uint64_t bad = __ballot(lane < k && ids[k + 1 + lane] != ids[lane]);
+  const int a = bad ? __builtin_ctzll(bad) : k;
+  if (t <= k) p.tokens[g * (k + 1) + t] = t <= a ? ids[t] : -1;
+  if (p.row_argmax) {
+    if (t <= k) p.row_argmax[g * (2 * k + 1) + t] = ids[t];
+    if (t < k) p.row_argmax[g * (2 * k + 1) + k + 1 + t] = ids[k + 1 + t];
   }
-  p.accept_len[g] = accepted;
+  if (t == 0) p.accept_len[g] = a;
 }
 
 // Grid: direct mode (argmax, one workgroup per row) is 1-D over rows;
@@ -183,10 +233,20 @@ __global__ __launch_bounds__(BLOCK) void greedy_kernel(GreedyParams p) {
   __shared__ int64_t ids[kMaxRowsPerGroup];
   __shared__ uint64_t keys[kMaxRowsPerGroup * 4];
   __shared__ int last;
-  const int split = p.direct ? 0 : static_cast<int>(blockIdx.x);
-  const int j = p.direct ? 0 : static_cast<int>(blockIdx.y);
-  const int64_t g = p.direct ? static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.z);
-  const char* row = row_ptr(p, g, j);
+  // The row address is formed with selects from parameters that are all
+  // fetched in one round of scalar loads (a branch on the row kind would
+  // chain dependent kernel-argument loads ahead of the first logits load).
+  int64_t tbs = p.t_bstride, tps = p.t_pstride, dbs = p.d_bstride, dps = p.d_pstride;
+  int kk = p.k, direct = p.direct;
+  asm volatile("" : "+s"(tbs), "+s"(tps), "+s"(dbs), "+s"(dps), "+s"(kk), "+s"(direct));
+  const char* tbase = p.target;
+  const char* dbase = p.draft;
+  const int split = direct ? 0 : static_cast<int>(blockIdx.x);
+  const int j = direct ? 0 : static_cast<int>(blockIdx.y);
+  const int64_t g = direct ? static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.z);
+  const bool is_t = j <= kk;
+  const char* row = (is_t ? tbase : dbase) + g * (is_t ? tbs : dbs) +
+                    static_cast<int64_t>(is_t ? j : j - kk - 1) * (is_t ? tps : dps);
 
   uint64_t key;
   if constexpr (VEC) {
@@ -200,18 +260,18 @@ __global__ __launch_bounds__(BLOCK) void greedy_kernel(GreedyParams p) {
   }
   key = block_max_u64<BLOCK>(key, red);
 
-  if (p.direct) {
+  if (direct) {
     if (threadIdx.x == 0) p.out[g] = argmax_key_index(key);
     return;
   }
+  const int own = j * p.splits + split;
   if (threadIdx.x == 0) {
-    store_sc64(p.slots + (g * p.rows_per_group + j) * p.splits + split, key);
-    drain_stores();
+    store_sc64(p.slots + g * p.rows_per_group * p.splits + own, key);
     const uint32_t prev = atomic_arrive(p.counters + g * kCounterStride);
     last = prev == static_cast<uint32_t>(p.rows_per_group * p.splits - 1);
   }
   __syncthreads();
-  if (last) finalize_group<BLOCK>(p, g, ids, keys);
+  if (last) finalize_group<BLOCK>(p, g, own, key, ids, keys);
 }
 
 // Workspace: kMaxGroups counter lines, then rows * kMaxSplits key slots.

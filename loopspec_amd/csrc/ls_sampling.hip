@@ -1098,13 +1098,18 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   const int t = threadIdx.x;
   const int nslots = p.nch * p.cap;
   const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
+  // this workgroup's scalars, loaded before the row work so that their latency
+  // is not paid after it
+  const float u_acc = p.uniforms[g * rpg + i];        // i < k: acceptance draw
+  const float u_draw = p.uniforms[g * rpg + k + i];   // residual draw (bonus draw u[2k] when i == k)
+  const int64_t x = i < k ? p.draft_tokens[g * k + i] : -1;
   if (i == k) {
     const int64_t r[1] = {g * rpg + k};
     RowStat st[1];
     float P_tok[1];
     int n_sup[1];
     finalize_rows<DT, 1>(p, sh, r, false, st, P_tok, n_sup, [] {});
-    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, p.uniforms[g * rpg + 2 * k], row_of(p, g, k), bm);
+    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, u_draw, row_of(p, g, k), bm);
     publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
     return;
   }
@@ -1131,10 +1136,9 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   const RowStat& st_t = st[0];
   const RowStat& st_d = st[1];
   // accept bit of x_i
-  const int64_t x = p.draft_tokens[g * k + i];
-  const bool acc = x >= 0 && x < p.vocab && accept_draw(p.uniforms[g * rpg + i], P_tok[0] < 0.0f ? 0.0f : P_tok[0],
+  const bool acc = x >= 0 && x < p.vocab && accept_draw(u_acc, P_tok[0] < 0.0f ? 0.0f : P_tok[0],
                                                         P_tok[1] < 0.0f ? 0.0f : P_tok[1]);
-  const float u = p.uniforms[g * rpg + k + i];
+  const float u = u_draw;
   const bool unf_t = st_t.flags & kFlagUnfiltered;
   const bool unf_d = st_d.flags & kFlagUnfiltered;
   auto Qof = [&](float l, int idx) {
