@@ -1,31 +1,36 @@
 // (a) logit processing and (c) lossless speculative sampling for gfx950.
 //
-// One persistent launch does the whole path (plus a penalty-bitmap pre-pass
-// when a repetition penalty is on, and a dense-output pass in filter mode).
-// Workgroups of 256 lanes stream (row, chunk) items of kChunk logits in
-// row-major order, with the next item's loads in flight while the current one
-// is processed. Per item:
-//   chunk max m_j of the penalised logits, mc_j = RN(m_j c) (c = log2 e / T),
-//   e = exp2q(fma(x, c, -mc_j)), the chunk mass M_j (binary32, fixed
-//   summation order), a histogram of the binary exponents of e, and the
-//   chunk's largest entries (every e >= 2^(1-K_j), at most cap of them, K_j
-//   the most leading exponent bins that fit) compacted in index order into
-//   the workspace; then
-//   each wave arrives on the row's counter.
-// The wave that arrives last makes its workgroup finalise the row: row max,
-// f_j = exp2q(mc_j - max), S = sum f_j M_j, g_j = RN(f_j / S), p = RN(e g_j)
-// for the candidates, and the exact top-p cutoff by a radix select on the
-// binary32 bits of p with 2^-46 fixed-point masses (replacing sort + cumsum +
-// searchsorted, distributions.py:59-70). The cutoff is valid for the whole
-// row iff it exceeds every p outside the candidates; otherwise the row is
-// re-streamed for an exact select. Then, per mode:
-//   spec    publish the row's statistics and the filtered probability of its
-//           draft token, arrive on the batch element's counter; the last of
-//           its 2k+1 rows runs the chain verify: accept tests, then the
-//           residual or bonus draw over the target row's candidates;
-//   sample  draw one token from the filtered distribution;
-//   dense   publish the statistics for dense_kernel, which writes p and/or the
-//           filtered, renormalised rows.
+// Two launches per call (a third, first, with a repetition penalty; a last
+// one for dense outputs):
+//   bitmap_kernel    one workgroup per batch element turns its token history
+//                    into a vocabulary bitmap in the workspace.
+//   chunk_kernel     persistent, one wave per (row, chunk) item of kChunk =
+//                    2048 logits, items in row-major order, the next item's
+//                    loads in flight while the current one is processed. Per
+//                    item: the penalised chunk max m_j, mc_j = RN(m_j c) with
+//                    c = RN(log2e RN(1/T)), e = exp2q(fma(x, c, -mc_j)), the
+//                    chunk mass M_j (a fixed pairwise tree), a histogram of
+//                    exp2q's exponent (bins 0..15 below the chunk max) and the
+//                    chunk's candidates: every e >= kCandScale 2^-K, K the
+//                    number of leading bins holding at most cap entries
+//                    together, written in index order; then a 32-byte record
+//                    (mc_j, K, count, M_j, e of the row's draft token).
+//   spec_row_kernel  one 512-lane workgroup per (batch element, position i):
+//                    the target and the draft row of position i side by side
+//                    (the bonus row alone for i == k). S = sum_j f_j M_j with
+//                    f_j = exp2q(mc_j - max mc), g_j = RN(f_j / S),
+//                    p = RN(e g_j) for the candidates; the exact top-p cutoff
+//                    by a radix select on the binary32 bits of p with 2^-46
+//                    fixed-point masses (replacing sort + cumsum +
+//                    searchsorted, distributions.py:59-70), valid iff it
+//                    exceeds the bound on every p outside the candidates
+//                    (otherwise the row is re-read for an exact select); the
+//                    accept bit of x_i and the residual draw. The last of the
+//                    k+1 workgroups of a batch element writes its accepted
+//                    length and tokens.
+//   row_kernel       sample and dense modes: one workgroup per row, the same
+//                    finalisation, then a draw or the row statistics.
+//   dense_kernel     dense mode: p and/or the filtered, renormalised rows.
 // The arithmetic is the declared arithmetic of ls_numerics.hpp (restated by
 // oracle/sampling.py), so every output is bit-identical to the oracle's.
 #include "ls_common.hpp"
@@ -126,7 +131,6 @@ struct SampParams {
   ChunkRec* chunks;             // [rows, nch]
   uint64_t* cands;              // [rows, nch, kChunkCand] of (idx << 32 | bits(e))
   RowStat* stats;               // [rows]
-  uint32_t* row_cnt;            // [kMaxRows * kCounterStride]
   uint32_t* grp_cnt;            // [kMaxSpecBatch * kCounterStride]
   uint32_t* bitmap;             // [groups, bm_words] penalty bits
   int64_t* draws;               // spec: [B, k+1] residual draws, then the bonus draw
@@ -500,6 +504,7 @@ struct RowSh {
   float g[2][kMaxChunks];
   float mcj[2][kMaxChunks];
   uint32_t n[2][kMaxChunks];
+  uint8_t kb[2][kMaxChunks];           // K of each chunk (kOctBins: complete)
   uint32_t gbits[2][kGather];
   uint64_t gw[2][kGather];
   uint32_t gcount[2];
@@ -510,6 +515,7 @@ struct RowSh {
   uint32_t u32s[8];
   float f32s[2][4];
   float slow_cut[2];
+  float wmin[kRW];                     // per-wave minima (negated) of the slow path
   uint64_t slow_mass[2];
   uint64_t draws[64 + 1];
 };
@@ -579,11 +585,13 @@ __device__ __forceinline__ RowScale row_scale(RowSh& sh, int set, const ChunkRec
     sh.g[set][ja] = ga;
     sh.mcj[set][ja] = ra.mc;
     sh.n[set][ja] = ra.n;
+    sh.kb[set][ja] = static_cast<uint8_t>((ra.flags & kChunkComplete) ? kOctBins : ra.K);
   }
   if (ib) {
     sh.g[set][jb] = gb;
     sh.mcj[set][jb] = rb.mc;
     sh.n[set][jb] = rb.n;
+    sh.kb[set][jb] = static_cast<uint8_t>((rb.flags & kChunkComplete) ? kOctBins : rb.K);
   }
   rs.p_bound = wave_max_f32(__builtin_fmaxf(ia ? chunk_bound(ra, ga) : 0.0f, ib ? chunk_bound(rb, gb) : 0.0f));
   const bool ta = ia && (ra.flags & kChunkHasTok), tb = ib && (rb.flags & kChunkHasTok);
@@ -841,28 +849,93 @@ __device__ int64_t pick_dense(RowSh& sh, int vocab, float u, W weight) {
   return static_cast<int64_t>(sh.u64s[3]);
 }
 
+// The candidates' cutoff cut of the row of set `set` did not clear the
+// worst-case bound on the p outside the candidates. Re-reads only the chunks
+// whose bound reaches cut and checks their non-candidates exactly: true iff
+// every p outside the candidates is below cut, in which case cut and the
+// candidates' mass are the row's (no element outside the candidates can
+// reach a value >= cut). Runs inside slow_select.
+template <int DT>
+__device__ __forceinline__ bool bound_repair(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c,
+                                             float pen, float inv_pen, int vocab, int nch, float cut) {
+  const int t = threadIdx.x;
+  bool bad = false;
+  for (int j = 0; j < nch; ++j) {
+    const int K = sh.kb[set][j];
+    if (K >= kOctBins) continue;
+    const float gj = sh.g[set][j];
+    const float th = K > 0 ? __builtin_ldexpf(kCandScale, -K) : __builtin_inff();
+    if (K > 0 && !(th * gj >= cut)) continue;  // chunk_bound below cut
+    const float nmc = -sh.mcj[set][j];
+    const int c0 = j * kChunk;
+#pragma unroll
+    for (int q = 0; q < kChunk / kRB; ++q) {
+      const int i = c0 + t + q * kRB;
+      if (i < vocab) {
+        float l = load_elem<DT>(rowp, i);
+        if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
+        const float e = exp2q(__builtin_fmaf(l, c, nmc));
+        bad = bad || (!(e >= th) && e * gj >= cut);
+      }
+    }
+  }
+  // block-wide OR through LDS (no device-library call)
+  if (t == 0) sh.u32s[6] = 0u;
+  __syncthreads();
+  if (bad) sh.u32s[6] = 1u;
+  __syncthreads();
+  const bool any = sh.u32s[6] != 0u;
+  __syncthreads();
+  return !any;
+}
+
 // Exact select over every element of the row of set `set` (its candidates
-// did not hold the cutoff): p recomputed from the re-read logits with the
+// did not hold the cutoff; first, when they held top_p, the bound repair,
+// which returns kRepaired when the candidates' cutoff cand_cut stands): p recomputed from the re-read logits with the
 // set's g_j. When keep is set, leaves the support {p >= c} in index order in
 // sh.slot[set] (as idx << 32 | bits(p)) and returns its size, or -1 if it does
 // not fit. The cutoff and its fx46 mass go to sh.slow_cut / sh.slow_mass.
 // Out of line, with plain arguments and no pointers into the caller's frame,
 // so the common path's registers are unaffected.
+constexpr int kRepaired = -2;  // slow_select: the candidates' cutoff stands
+
 template <int DT>
 __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
-                                        float inv_pen, int vocab, uint64_t thr, bool keep) {
+                                        float inv_pen, int vocab, int nch, int nslots, uint64_t thr, bool keep) {
   const int t = threadIdx.x, wid = t / kWave;
   const float* mcj = sh.mcj[set];
   const float* gj = sh.g[set];
   auto pval = [&](int i) { return p_elem<DT>(rowp, bm, c, pen, inv_pen, mcj, gj, i); };
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
-  __syncthreads();
   const uint64_t thr1[1] = {thr};
   bool found[1];
   float cc1[1];
   uint64_t mfx1[1];
+  // 1. the candidates' select again (their p are still in sh.slot[set]); when
+  //    they hold top_p, the bound repair may confirm their cutoff
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
+  __syncthreads();
+  radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
+    for (int sl = t; sl < nslots; sl += kRB) {
+      const uint32_t bits = static_cast<uint32_t>(sh.slot[set][sl]);
+      const float x = __uint_as_float(bits);
+      if (x > 0.0f) f(bits, fx46(x));
+    }
+  }, found, cc1, mfx1);
+  if (found[0] && bound_repair<DT>(sh, set, rowp, bm, c, pen, inv_pen, vocab, nch, cc1[0])) {
+    if (t == 0) {
+      sh.slow_cut[set] = cc1[0];
+      sh.slow_mass[set] = mfx1[0];
+    }
+    __syncthreads();
+    return kRepaired;
+  }
+  // 2. exact select over the whole row
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
+  __syncthreads();
   radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
     for (int i = t; i < vocab; i += kRB) {
       const float pv = pval(i);
@@ -881,10 +954,13 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
       tot += fx46(pv);
     }
     mn = wave_max_f32(-mn);
-    if ((t & (kWave - 1)) == 0) sh.f32s[set][wid] = mn;
+    if ((t & (kWave - 1)) == 0) sh.wmin[wid] = mn;
     uint64_t all;
-    (void)block_excl_scan(tot, sh.red, &all);
-    cc = -nmax(nmax(sh.f32s[set][0], sh.f32s[set][1]), nmax(sh.f32s[set][2], sh.f32s[set][3]));
+    (void)block_excl_scan(tot, sh.red, &all);  // its barriers also publish wmin
+    float m = sh.wmin[0];
+#pragma unroll
+    for (int w = 1; w < kRW; ++w) m = nmax(m, sh.wmin[w]);
+    cc = -m;
     mfx = all;
     __syncthreads();
   }
@@ -1012,14 +1088,15 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
         st[s].cutoff = cut[s];
         st[s].mass_fx = mfx[s];
       } else {
-        st[s].flags |= kFlagSlow;
         const int64_t g = r[s] / p.rpg;
         const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
-        n_sup[s] = slow_select<DT>(sh, s, row_of(p, g, static_cast<int>(r[s] - g * p.rpg)), bm, p.c, p.pen, p.inv_pen,
-                                   p.vocab, thr[s], keep_support);
+        const int n = slow_select<DT>(sh, s, row_of(p, g, static_cast<int>(r[s] - g * p.rpg)), bm, p.c, p.pen,
+                                      p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support);
         st[s].cutoff = sh.slow_cut[s];
         st[s].mass_fx = sh.slow_mass[s];
-        if (!keep_support || n_sup[s] < 0) st[s].flags |= kFlagDense;
+        const bool rep = n == kRepaired;
+        st[s].flags |= rep ? 0u : (kFlagSlow | ((!keep_support || n < 0) ? kFlagDense : 0u));
+        n_sup[s] = rep ? nslots : n;
       }
     }
     st[s].mass = unf[s] ? 1.0f : mass_to_f32(st[s].mass_fx);
@@ -1290,18 +1367,17 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
 // Host side
 // ===========================================================================
 struct Layout {
-  uint64_t row_cnt, grp_cnt, chunks, cands, stats, draws, bitmap, total;
+  uint64_t grp_cnt, chunks, cands, stats, draws, bitmap, total;
 };
 
-// Workspace: [pair arrival counters, one 64-byte line each, for up to
-// kMaxRows rows] [group counters for up to kMaxSpecBatch elements] (both at
-// fixed places, so calls of any shape find them zero) [chunk records]
-// [candidates] [row statistics] [draws] [penalty bitmaps, one per group].
+// Workspace: [group arrival counters, one 64-byte line each, for up to
+// kMaxSpecBatch batch elements] (at a fixed place, so calls of any shape find
+// them zero) [chunk records] [candidates] [row statistics] [draws] [penalty
+// bitmaps, one per group].
 Layout ws_layout(int64_t rows, int64_t groups, int nch) {
   auto al = [](uint64_t x) { return (x + 255u) & ~255ull; };
   Layout l{};
-  l.row_cnt = 0;
-  l.grp_cnt = al(static_cast<uint64_t>(kMaxRows) * kCounterStride * 4u);
+  l.grp_cnt = 0;
   uint64_t off = al(l.grp_cnt + static_cast<uint64_t>(kMaxSpecBatch) * kCounterStride * 4u);
   l.chunks = off;
   off = al(off + static_cast<uint64_t>(rows) * nch * sizeof(ChunkRec));
@@ -1319,7 +1395,6 @@ Layout ws_layout(int64_t rows, int64_t groups, int nch) {
 
 void bind_workspace(SampParams& p, void* ws, const Layout& l) {
   char* b = static_cast<char*>(ws);
-  p.row_cnt = reinterpret_cast<uint32_t*>(b + l.row_cnt);
   p.grp_cnt = reinterpret_cast<uint32_t*>(b + l.grp_cnt);
   p.chunks = reinterpret_cast<ChunkRec*>(b + l.chunks);
   p.cands = reinterpret_cast<uint64_t*>(b + l.cands);

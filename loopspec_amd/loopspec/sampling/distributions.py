@@ -3,12 +3,13 @@
 Same functions, arguments and results as the reference
 (sglang_recurrent/loopspec/sampling/distributions.py:14-171). Softmax,
 temperature and the top-p cutoff run as gfx950 kernels that read the logits
-once with one workgroup per 8192-element chunk (no sort: the cutoff is found
-by a mass-ordered radix select over the chunks' largest entries); joint
+once, one wave per 2048-element chunk (no sort: the cutoff is found by a
+radix select over the chunks' largest entries with exact masses); joint
 top-k/top-p adds one row pass for the k-th largest value. The arithmetic is
-the library's declared one (chunked softmax with a fixed polynomial exp, exact
-2^-46 fixed-point masses), so values agree with the reference's float32 torch
-path to rounding while the cutoff rule, ties included, is the same.
+the library's declared one (chunked base-2 softmax with a fixed polynomial
+exp2, exact 2^-46 fixed-point masses), so values agree with the reference's
+float32 torch path to rounding while the cutoff rule, ties included, is the
+same.
 
 The top-p context returned by prepare_sampling_probabilities keeps arity 3 but
 carries (unfiltered probs [B, V], cutoff values [B, 1], zero ranks [B, 1]) in

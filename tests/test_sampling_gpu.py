@@ -13,6 +13,7 @@ import torch
 from oracle import numerics as nm
 from oracle import sampling as osmp
 from loopspec_amd import philox, verify, workloads
+from tests import candidates
 from tests.conftest import announce
 
 pytestmark = pytest.mark.gpu
@@ -104,6 +105,73 @@ def test_filter_logits_edge_rows(gpu, case):
         want = oracle_filter(x[r].numpy(), 1.0, top_p)
         assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), (case, r)
         assert res["cutoff"][r].item() == want.cutoff
+
+
+def test_filter_logits_repair_and_slow_rows(gpu):
+    """Rows whose candidates' cutoff misses the worst-case bound: re-checked
+    chunk by chunk (repair) or selected exactly over the row (slow)."""
+    rows = candidates.repair_rows()
+    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["repair"][::-1].copy()]))
+    announce("filter repair/slow rows")
+    res = verify.filter_logits(x.to(gpu), 1.0, 0.9, want_probs=True)
+    torch.cuda.synchronize()
+    for r in range(x.shape[0]):
+        want = oracle_filter(x[r].numpy(), 1.0, 0.9)
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
+        assert res["cutoff"][r].item() == want.cutoff, r
+        assert res["mass"][r].item() == nm.mass_to_f32(want.mass_fx), r
+
+
+def test_sample_and_spec_repair_and_slow_rows(gpu):
+    rows = candidates.repair_rows()
+    v = rows["repair"].shape[0]
+    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"]] * 4))
+    u = torch.from_numpy(philox.uniforms((x.shape[0],), seed=21))
+    announce("sample repair/slow rows")
+    got = verify.sample_logits(x.to(gpu), u.to(gpu), 1.0, 0.9)
+    torch.cuda.synchronize()
+    want = [osmp.categorical_pick(oracle_filter(x[r].numpy(), 1.0, 0.9).P, u[r].item()) for r in range(x.shape[0])]
+    assert got.cpu().tolist() == want
+    # spec verify, B=4, k=1: target rows (pos 0, bonus) and draft rows from the two kinds
+    cfg = workloads.SamplingConfig("repair", 4, 1, v, torch.float32, 1.0, 0.9)
+    inp = workloads.sampling_inputs(cfg, 13)
+    for b in range(4):
+        inp["target"][b, 0] = torch.from_numpy(rows["repair" if b % 2 else "slow"])
+        inp["target"][b, 1] = torch.from_numpy(rows["slow" if b % 2 else "repair"])
+        inp["draft"][b, 0] = torch.from_numpy(rows["repair" if b < 2 else "slow"])
+    drafts = draft_tokens_from(inp, cfg)
+    announce("spec repair/slow rows")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
+
+
+def test_top_p_just_below_one(gpu):
+    """top_p = 1 - 2^-24: on many rows the exact retained masses sum below it,
+    so no cutoff reaches top_p and the whole row is kept (cutoff = min p)."""
+    top_p = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(8, 49152, generator=g) * 3
+    announce("filter top_p just below one")
+    res = verify.filter_logits(x.to(gpu), 1.0, top_p, want_probs=True)
+    torch.cuda.synchronize()
+    kept_all = 0
+    for r in range(x.shape[0]):
+        want = oracle_filter(x[r].numpy(), 1.0, top_p)
+        kept_all += int(want.cutoff == want.soft.p.min())
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
+        assert res["cutoff"][r].item() == want.cutoff, r
+        assert res["mass"][r].item() == nm.mass_to_f32(want.mass_fx), r
+    assert kept_all > 0  # the whole-row case was exercised
+    cfg = workloads.SamplingConfig("near1", 4, 2, 49152, torch.float32, 1.0, top_p)
+    inp = workloads.sampling_inputs(cfg, 17)
+    drafts = draft_tokens_from(inp, cfg)
+    announce("spec top_p just below one")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
 
 
 def test_filter_per_row_thresholds(gpu):
