@@ -97,11 +97,13 @@ uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
  * Shared processing of a logits row (any of f32/bf16/f16, contiguous vocab,
  * 16-byte aligned rows, vocab*elem_bytes a multiple of 16):
  *   x = logits; for ids in the row's history (if penalty != 1):
- *       x <- x < 0 ? x*penalty : x*RN(1/penalty);  then x <- x*RN(1/T) (T != 1);
- *   p = softmax(x) in the library's declared arithmetic: chunks of 8192
- *   elements, e = exp(x - chunk max) by a fixed polynomial, exact 2^-46
- *   fixed-point chunk masses combined with f_j = exp(chunk max - row max),
- *   p = RN(RN(e * f_j) / S);
+ *       x <- x < 0 ? x*penalty : x*RN(1/penalty);
+ *   p = softmax(x / T) in the library's declared arithmetic (base 2, chunks of
+ *   2048 elements): c = RN(log2(e) * RN(1/T)), mc_j = RN(c * chunk max),
+ *   e = exp2q(fma(x, c, -mc_j)) with exp2q a fixed degree-5 polynomial times
+ *   2^k, chunk masses M_j summed in a fixed pairwise order,
+ *   f_j = exp2q(mc_j - max mc), S = pairwise sum of RN(f_j * M_j),
+ *   g_j = RN(f_j / S), p = RN(e * g_j);
  *   top_p < 1: keep p >= c with c = max{v : sum_{p>=v} fx46(p) >= fx46(top_p)}
  *   (ties kept; the whole row if no v qualifies), renormalise by the retained
  *   mass -- the value semantics of sort + cumsum + searchsorted(right=False)
@@ -140,7 +142,7 @@ uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 
 /* Filter each logits row and draw one token per row with uniforms[row]
  * (float32 [rows]) into out_tokens (int64 [rows]); history rows as above,
- * one per logits row; rows <= 65535. Workspace: ls_sample_logits_workspace
+ * one per logits row; rows <= 65536. Workspace: ls_sample_logits_workspace
  * bytes (no zero-fill needed). Replaces prepare_sampling_probabilities followed
  * by sample_probabilities / CategoricalSampler.sample
  * (sglang_recurrent/loopspec/sampling/distributions.py:89-171). */
@@ -156,7 +158,7 @@ uint64_t ls_sample_logits_workspace(int64_t rows, int64_t vocab);
  * distribution (p itself when top_p == 1); cutoff_out / mass_out (optional,
  * float32 [rows]) the cutoff value (0 when unfiltered) and binary32 retained
  * mass. top_p_rows (optional, float32 [rows]) overrides top_p per row when
- * top_p < 1. rows <= 65535. Workspace: ls_filter_logits_workspace bytes.
+ * top_p < 1. rows <= 65536. Workspace: ls_filter_logits_workspace bytes.
  * Replaces filtered_probabilities and the probability/cutoff part of
  * prepare_sampling_probabilities (distributions.py:14-149). */
 int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows,
