@@ -1180,19 +1180,10 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   const float u_acc = p.uniforms[g * rpg + i];        // i < k: acceptance draw
   const float u_draw = p.uniforms[g * rpg + k + i];   // residual draw (bonus draw u[2k] when i == k)
   const int64_t x = i < k ? p.draft_tokens[g * k + i] : -1;
-  if (i == k) {
-    const int64_t r[1] = {g * rpg + k};
-    RowStat st[1];
-    float P_tok[1];
-    int n_sup[1];
-    finalize_rows<DT, 1>(p, sh, r, false, st, P_tok, n_sup, [] {});
-    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, u_draw, row_of(p, g, k), bm);
-    publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
-    return;
-  }
-  const int64_t r[2] = {g * rpg + i, g * rpg + k + 1 + i};
-  const char* trow = row_of(p, g, i);
-  const char* drow = row_of(p, g, k + 1 + i);
+  const bool bonus = i == k;
+  const int64_t r[2] = {g * rpg + (bonus ? k : i), g * rpg + (bonus ? k : k + 1 + i)};
+  const char* trow = row_of(p, g, bonus ? k : i);
+  const char* drow = row_of(p, g, bonus ? k : k + 1 + i);
   // the draft logits at the target's candidates, gathered during the selects
   float lq[kSlotsPerLane];
   auto gather = [&] {
@@ -1210,6 +1201,11 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   float P_tok[2];
   int n_sup[2];
   finalize_rows<DT, 2>(p, sh, r, false, st, P_tok, n_sup, gather);
+  if (bonus) {
+    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, u_draw, trow, bm);
+    publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
+    return;
+  }
   const RowStat& st_t = st[0];
   const RowStat& st_d = st[1];
   // accept bit of x_i
