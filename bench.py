@@ -61,29 +61,7 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
         t, d = sets[i]
         verify.greedy_verify(t, d, accept_len=acc[i], tokens=tok[i], workspace=ws)
 
-    for i in range(nsets):  # eager warm-up (and lazy library load) before capture
-        step(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(nsets):
-            step(i)
-    replays = max(1, -(-steps // nsets))
-    wreplays = max(1, -(-warmup // nsets))
-    for _ in range(wreplays):
-        graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(replays):
-        graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    timed_steps = replays * nsets
-    ms_per_step = ms / timed_steps
+    ms_per_step, timed_steps, wsteps = _time_graph(step, nsets, steps, warmup)
     accepted = acc.sum().item() / nsets  # accepted drafts per step
     tokens_per_step = accepted + cfg.batch  # + one correction/bonus token per row
     nbytes = workloads.greedy_algorithmic_bytes(cfg)
@@ -93,7 +71,7 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
         "value": cfg.batch / (ms_per_step * 1e-3),
         "unit": "rows/s",
         "steps": timed_steps,
-        "warmup": wreplays * nsets,
+        "warmup": wsteps,
         "ms_per_step": ms_per_step,
         "dtype": "bf16",
         "config": {
@@ -277,8 +255,16 @@ def traffic_from_profile(kernel: str, workload: str) -> float | None:
     return None
 
 
+_LAST_PERCENTILES: dict = {}
+
+
 def _time_graph(step, nsets: int, steps: int, warmup: int):
-    """Capture one graph of nsets steps, replay it; return (ms/step, steps, warmup steps)."""
+    """Capture one graph of nsets steps, replay it; return (ms/step, steps, warmup steps).
+
+    Two events on the stream bracket the whole timed region. A second pass
+    with an event after every 5 replays (events between replays add a small gap
+    of their own, so they stay out of the timed region) gives the p10/p50/p90
+    of the per-step time over 40 windows, left in _LAST_PERCENTILES."""
     for i in range(nsets):
         step(i)
     torch.cuda.synchronize()
@@ -298,7 +284,20 @@ def _time_graph(step, nsets: int, steps: int, warmup: int):
         graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (replays * nsets), replays * nsets, wreplays * nsets
+    ms_per_step = start.elapsed_time(end) / (replays * nsets)
+    per_window, windows = 5, 40
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(windows + 1)]
+    marks[0].record(stream)
+    for w in range(windows):
+        for _ in range(per_window):
+            graph.replay()
+        marks[w + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = sorted(marks[w].elapsed_time(marks[w + 1]) / (per_window * nsets) for w in range(windows))
+    q = lambda f: per_step[min(len(per_step) - 1, int(f * len(per_step)))]
+    _LAST_PERCENTILES.clear()
+    _LAST_PERCENTILES.update({"ms_per_step_p10": q(0.1), "ms_per_step_p50": q(0.5), "ms_per_step_p90": q(0.9)})
+    return ms_per_step, replays * nsets, wreplays * nsets
 
 
 def cpu_baseline_greedy(max_seconds: float = 20.0) -> dict:
@@ -340,6 +339,77 @@ def cpu_baseline_greedy(max_seconds: float = 20.0) -> dict:
     }
 
 
+def cpu_baseline_c1(max_seconds: float = 10.0) -> dict:
+    """C1, the reference's CPU target shape: batch-1 greedy verify steps (k=2,
+    V=49152, fp32) on the torch-CPU restatement of decisions.py, up to 10k
+    seeded steps or max_seconds, at all threads."""
+    from loopspec_amd import workloads
+    from oracle import torch_ref
+
+    cfg = workloads.C1
+    n_inputs = 16
+    inputs = [workloads.greedy_inputs(cfg, seed=100 + i, device="cpu") for i in range(n_inputs)]
+    steps = 0
+    t0 = time.perf_counter()
+    while steps < 10000 and time.perf_counter() - t0 < max_seconds:
+        target, draft = inputs[steps % n_inputs]
+        torch_ref.greedy_verify_step(target[0], draft[0])
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {"workload": cfg.name, "steps": steps, "steps_per_s": steps / dt, "seconds": dt}
+
+
+def cpu_baseline_spec(cfg, max_seconds: float = 20.0) -> dict:
+    """Reference torch-CPU sampling verify (oracle.torch_ref.speculative_verify:
+    filtered_probabilities over each element's 2k+1 rows, the q1 rule per
+    position, residual or bonus draw) on batch elements of cfg's shape, for
+    about max_seconds / 2 at all threads and at one thread."""
+    from loopspec_amd import workloads
+    from oracle import torch_ref
+
+    inp = workloads.sampling_inputs(cfg, seed=11, device="cpu")
+    k, b_n = cfg.k, cfg.batch
+    target, draft = inp["target"].float(), inp["draft"].float()
+    hists = None
+    if cfg.penalty != 1.0:
+        hists = [inp["history"][b, : int(inp["history_len"][b])] for b in range(b_n)]
+    # draft tokens sampled from the filtered draft rows (not timed)
+    drafts = torch.zeros((b_n, k), dtype=torch.int64)
+    for b in range(b_n):
+        rows = draft[b]
+        if hists is not None:
+            rows = torch_ref.apply_penalty(rows, hists[b], cfg.penalty)
+        q = torch_ref.filtered_probabilities(rows, cfg.temperature, 1 << 30, cfg.top_p)
+        drafts[b] = torch_ref.categorical_pick(q, inp["draft_uniforms"][b])
+    threads = len(os.sched_getaffinity(0))
+    results = {}
+    for nthreads in (threads, 1):
+        torch.set_num_threads(nthreads)
+        done = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < max_seconds / 2:
+            b = done % b_n
+            torch_ref.speculative_verify(target[b:b + 1], draft[b:b + 1], drafts[b:b + 1], inp["uniforms"][b:b + 1],
+                                         cfg.temperature, cfg.top_p, cfg.penalty,
+                                         None if hists is None else hists[b:b + 1])
+            done += 1
+        results[nthreads] = done / (time.perf_counter() - t0)
+    torch.set_num_threads(threads)
+    return {
+        "value": results[threads],
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{cfg.name} batch elements one at a time for ~{max_seconds / 2:.0f}s per thread setting; "
+                  "torch-CPU restatement of the reference's filter + q1 verify + residual/bonus draw",
+        "value_1_thread": results[1],
+        "torch_threads": threads,
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model(),
+        "torch_version": torch.__version__,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -370,15 +440,20 @@ def main() -> int:
     elif args.config in ("C3", "C4"):
         cfg = workloads.C3 if args.config == "C3" else workloads.C4
         result = bench_spec(cfg, args.steps, args.warmup, device, args.sets)
-        args.no_cpu_baseline = True
     elif args.config == "C5":
         result = bench_c5(args.steps, args.warmup, device, args.sets)
         args.no_cpu_baseline = True
     else:
         print(f"unknown config {args.config}", file=sys.stderr)
         return 2
-    result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                   "data": "synthetic (seeded N(0,3^2) logits, draft = target + N(0,1), 1% planted ties)"})
+    data = {
+        "C2": "synthetic (seeded N(0,3^2) bf16 logits, draft = target + N(0,1), 1% planted ties)",
+        "C3": "synthetic (seeded N(0,3^2) fp32 logits, draft = target + N(0,1), drafts sampled from q, Philox uniforms)",
+        "C4": "synthetic (seeded N(0,4^2) bf16 logits, draft = target + N(0,1), Zipf(1.1) histories of "
+              "U(256,4096) ids, drafts sampled from q, Philox uniforms)",
+        "C5": "synthetic (C3 logits at B=128, drafts sampled from q; random bf16 KV pool, context U(512,8192))",
+    }[args.config]
+    result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": data})
     # Traffic summaries are per launch unit: the greedy kernel (C2), or the
     # kernels of one ls_spec_verify call together (C3, C4).
     kernel_name = {"C2": "greedy_kernel", "C3": "spec_verify", "C4": "spec_verify"}.get(args.config)
@@ -386,10 +461,16 @@ def main() -> int:
         result["roofline"]["traffic"] = traffic_from_profile(kernel_name, args.config)
     if args.copy_calibration:
         copy_calibration(device, args.copy_calibration)
+    result.update(_LAST_PERCENTILES)
     if not args.no_cpu_baseline:
         _log("timing CPU baseline")
-        result["cpu_baseline"] = cpu_baseline_greedy()
-    order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+        if args.config == "C2":
+            result["cpu_baseline"] = cpu_baseline_greedy()
+            result["cpu_baseline"]["c1"] = cpu_baseline_c1()
+        else:
+            result["cpu_baseline"] = cpu_baseline_spec(workloads.C3 if args.config == "C3" else workloads.C4)
+    order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "ms_per_step_p10",
+             "ms_per_step_p50", "ms_per_step_p90", "higher_is_better",
              "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"]
     line = {k: result[k] for k in order if k in result}
     line.update({k: v for k, v in result.items() if k not in line})

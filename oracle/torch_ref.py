@@ -162,15 +162,29 @@ def rejection_run(first: torch.Tensor, target: torch.Tensor, second: torch.Tenso
     return int(prediction[0]), int(accepted[0]), int((hs & ~accepted)[0])
 
 
+def apply_penalty(rows: torch.Tensor, history: torch.Tensor, penalty: float) -> torch.Tensor:
+    """Repetition penalty over a token history: for ids in the history,
+    l < 0 ? l * penalty : l / penalty (transformers' closed form,
+    generation/logits_process.py:409-412; SGLang's penalizer, which the
+    reference's baseline path would use, is not installed)."""
+    out = rows.clone()
+    ids = torch.unique(history.long())
+    sel = out[:, ids]
+    out[:, ids] = torch.where(sel < 0, sel * penalty, sel / penalty)
+    return out
+
+
 def speculative_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_tokens: torch.Tensor,
-                       uniforms: torch.Tensor, temperature: float, top_p: float):
+                       uniforms: torch.Tensor, temperature: float, top_p: float, penalty: float = 1.0,
+                       histories=None):
     """Chain-of-k lossless verify built from the reference's own ops.
 
     Per batch element: filter every endpoint row together (policy.py:228-233),
     verify position by position with the q1 rule (sampler.py:451-452); on the
     first rejection sample the residual fallback (rejection.py:60-69 and the
     sample_with_uniforms callback); if all accept, sample the last target row
-    directly (policy.py:156-165).
+    directly (policy.py:156-165). With penalty != 1 the rows of element b are
+    penalised over histories[b] first.
     Returns (accept_len int32 [B], tokens int64 [B, k+1]).
     """
     b_n, kp1, vocab = target_logits.shape
@@ -179,6 +193,8 @@ def speculative_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, 
     tok = torch.full((b_n, kp1), -1, dtype=torch.int64)
     for b in range(b_n):
         rows = torch.cat([target_logits[b], draft_logits[b]]).float()
+        if penalty != 1.0:
+            rows = apply_penalty(rows, histories[b], penalty)
         dist = filtered_probabilities(rows, temperature, 1 << 30, top_p)
         P, Q = dist[:kp1], dist[kp1:]
         a = 0
