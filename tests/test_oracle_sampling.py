@@ -323,3 +323,30 @@ def test_conditional_residual_matches_triton_restatement():
     assert np.allclose(R, want_R.numpy(), rtol=2e-6, atol=1e-12)
     assert np.array_equal(ids[1:], torch_ref.categorical_pick(r[1:], u[1:]).numpy())
     assert act[0] == 0 and (R[0] == 0).all()
+
+
+def test_penalised_speculative_verify_matches_torch_reference():
+    """The repetition penalty in both restatements (x * RN(1/r) vs x / r differ
+    by at most an ulp) leaves accept lengths and tokens equal on seeded rows."""
+    from loopspec_amd import philox
+
+    g = torch.Generator().manual_seed(9)
+    b, k, v = 4, 3, 8192
+    target = torch.randn(b, k + 1, v, generator=g) * 4
+    draft = target[:, :k] + torch.randn(b, k, v, generator=g)
+    hists = [torch.randint(0, v, (int(n),), generator=g) for n in (50, 400, 1, 2000)]
+    x = torch.randn(3, v, generator=g) * 4
+    pt = torch_ref.apply_penalty(x, hists[1], 1.1)
+    po = np.stack([os_.apply_penalty(x[r].numpy(), hists[1].numpy(), 1.1) for r in range(3)])
+    assert np.allclose(pt.numpy(), po, rtol=2e-7, atol=0)
+    drafts = torch.zeros(b, k, dtype=torch.int64)
+    du = torch.from_numpy(philox.uniforms((b, k), seed=5))
+    for i in range(b):
+        q = torch_ref.filtered_probabilities(torch_ref.apply_penalty(draft[i], hists[i], 1.1), 0.7, 1 << 30, 0.9)
+        drafts[i] = torch_ref.categorical_pick(q, du[i])
+    u = torch.from_numpy(philox.uniforms((b, 2 * k + 1), seed=6))
+    a_ref, t_ref = torch_ref.speculative_verify(target, draft, drafts, u, 0.7, 0.9, 1.1, hists)
+    res = os_.speculative_verify(target.numpy(), draft.numpy(), drafts.numpy(), u.numpy(), 0.7, 0.9, 1.1,
+                                 [h.numpy() for h in hists])
+    assert np.array_equal(res.accept_len, a_ref.numpy())
+    assert np.array_equal(res.tokens, t_ref.numpy())
