@@ -180,7 +180,7 @@ def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
                                       cfg.top_p)
         inp["draft_tokens"] = drafts.reshape(cfg.batch, cfg.k)
         sets.append(inp)
-    total_steps = steps + warmup + 4 * nsets
+    total_steps = steps + warmup + 4 * nsets + _PCT_WINDOWS * _PCT_PER_WINDOW * nsets
     state = workloads.kv_commit_state(kvc, cfg.batch, cfg.k, total_steps, seed=5, device=device)
     ws = torch.zeros(verify.spec_verify_workspace_bytes(cfg.batch, cfg.k, cfg.vocab), dtype=torch.uint8,
                      device=device)
@@ -256,6 +256,7 @@ def traffic_from_profile(kernel: str, workload: str) -> float | None:
 
 
 _LAST_PERCENTILES: dict = {}
+_PCT_WINDOWS, _PCT_PER_WINDOW = 40, 5  # percentile pass: windows of replays
 
 
 def _time_graph(step, nsets: int, steps: int, warmup: int):
@@ -285,7 +286,7 @@ def _time_graph(step, nsets: int, steps: int, warmup: int):
     end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / (replays * nsets)
-    per_window, windows = 5, 40
+    per_window, windows = _PCT_PER_WINDOW, _PCT_WINDOWS
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(windows + 1)]
     marks[0].record(stream)
     for w in range(windows):

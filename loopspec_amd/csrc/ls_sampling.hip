@@ -1200,11 +1200,27 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   RowStat st[2];
   float P_tok[2];
   int n_sup[2];
-  finalize_rows<DT, 2>(p, sh, r, false, st, P_tok, n_sup, gather);
+  // keep_support: a row whose cutoff needed the whole-row select keeps its
+  // support (if it fits the slots) in index order, so its draw stays on slots
+  finalize_rows<DT, 2>(p, sh, r, true, st, P_tok, n_sup, gather);
+  // target slots: the candidates, or the kept support of a slow row
+  const int nt = (st[0].flags & kFlagSlow) ? n_sup[0] : nslots;
   if (bonus) {
-    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nslots, u_draw, trow, bm);
+    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nt, u_draw, trow, bm);
     publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
     return;
+  }
+  if ((st[0].flags & (kFlagSlow | kFlagDense)) == kFlagSlow) {
+    // the support replaced the candidates: gather the draft logits again
+#pragma unroll
+    for (int q = 0; q < kSlotsPerLane; ++q) {
+      const int sl = t + q * kRB;
+      lq[q] = 0.0f;
+      if (sl < nt) {
+        const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
+        lq[q] = load_elem<DT>(drow, idx < p.vocab ? idx : 0);
+      }
+    }
   }
   const RowStat& st_t = st[0];
   const RowStat& st_d = st[1];
@@ -1228,7 +1244,7 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
     for (int q = 0; q < kSlotsPerLane; ++q) {
       const int sl = t + q * kRB;
       P[q] = D[q] = 0.0f;
-      if (sl < nslots) {
+      if (sl < nt) {
         const uint64_t v = sh.slot[0][sl];
         const float pv = __uint_as_float(static_cast<uint32_t>(v));
         if (pv > 0.0f && pv >= st_t.cutoff) {
@@ -1251,10 +1267,10 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
       float dq = D[q], pq = P[q];
       asm volatile("" : "+v"(dq), "+v"(pq));
       const int sl = t + q * kRB;
-      if (sl < nslots) sh.w[sl] = (use_d ? dq : pq) / den;
+      if (sl < nt) sh.w[sl] = (use_d ? dq : pq) / den;
     }
     __syncthreads();
-    const int win = pick_slot(sh, nslots, u, [&](int s) { return fx46(sh.w[s]); });
+    const int win = pick_slot(sh, nt, u, [&](int s) { return fx46(sh.w[s]); });
     token = win < 0 ? 0 : static_cast<int64_t>(sh.slot[0][win] >> 32);
   } else {
     // dense target row: the whole vocabulary
