@@ -137,3 +137,35 @@ def test_argmax_rows_inside_graph_replays(gpu):
         assert torch.equal(out, eager), rep
         x[rep, 123] = 100.0  # eager work between replays changes the input
         eager = torch.argmax(x.float(), -1)
+
+
+@pytest.mark.parametrize("batch,k,vocab,mode", [
+    (1, 64, 2048, "logits"),    # the largest k: 129 rows per batch element, the multi-wave combine
+    (3, 64, 1000, "tokens"),    # caller draft ids, unaligned vocabulary
+    (2, 31, 4096, "logits"),    # 63 rows per element
+    (2, 32, 4096, "logits"),    # 65 rows per element
+    (5, 1, 4096, "tokens"),     # the smallest k
+])
+def test_edge_shapes(gpu, batch, k, vocab, mode):
+    g = torch.Generator().manual_seed(batch * 1000 + k)
+    target = torch.randn(batch, k + 1, vocab, generator=g) * 3
+    draft = target[:, :k] + torch.randn(batch, k, vocab, generator=g) * 0.3  # mostly accepted prefixes
+    announce(f"greedy edge B={batch} k={k} V={vocab} {mode}")
+    if mode == "logits":
+        acc, tok = verify.greedy_verify(target.to(gpu), draft.to(gpu))
+        a0, t0, _ = _oracle(target, draft)
+    else:
+        ids = torch.argmax(draft, dim=-1)
+        acc, tok = verify.greedy_verify(target.to(gpu), draft_tokens=ids.to(gpu))
+        a0, t0, _ = _oracle(target, draft_tokens=ids)
+    torch.cuda.synchronize()
+    assert np.array_equal(acc.cpu().numpy(), a0)
+    assert np.array_equal(tok.cpu().numpy(), t0)
+
+
+def test_empty_batch(gpu):
+    target = torch.zeros(0, 3, 4096, device=gpu)
+    draft = torch.zeros(0, 2, 4096, device=gpu)
+    acc, tok = verify.greedy_verify(target, draft)
+    torch.cuda.synchronize()
+    assert acc.shape == (0,) and tok.shape == (0, 3)

@@ -305,3 +305,29 @@ def test_spec_verify_alternating_shapes_share_workspace(gpu):
         want = oracle_spec(cfg, inp, drafts)
         assert np.array_equal(acc.cpu().numpy(), want.accept_len), (b, k)
         assert np.array_equal(tok.cpu().numpy(), want.tokens), (b, k)
+
+
+@pytest.mark.parametrize("batch,k,vocab,dtype,top_p", [
+    (1, 64, 4096, torch.float32, 0.8),        # the largest k: 65 draws per element
+    (2, 1, 262144, torch.bfloat16, 0.9),      # the largest vocabulary: 128 chunks, 16 slots each
+    (2, 2, 5000, torch.float32, 0.7),         # a partial last chunk
+    (3, 3, 32000, torch.float16, 0.5),
+])
+def test_spec_verify_edge_shapes(gpu, batch, k, vocab, dtype, top_p):
+    cfg = workloads.SamplingConfig("edge", batch, k, vocab, dtype, 1.0, top_p, noise_std=0.3)
+    inp = workloads.sampling_inputs(cfg, batch + k)
+    drafts = draft_tokens_from(inp, cfg)
+    announce(f"spec edge B={batch} k={k} V={vocab} {dtype}")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
+
+
+def test_spec_verify_empty_batch(gpu):
+    t = torch.zeros(0, 3, 4096, device=gpu)
+    d = torch.zeros(0, 2, 4096, device=gpu)
+    acc, tok = verify.speculative_verify(t, d, torch.zeros(0, 2, dtype=torch.int64, device=gpu),
+                                         torch.zeros(0, 5, device=gpu), 1.0, 0.7)
+    torch.cuda.synchronize()
+    assert acc.shape == (0,) and tok.shape == (0, 3)
