@@ -14,10 +14,8 @@ thread_local std::string g_last_error;
 std::mutex g_mu;
 std::map<std::string, int64_t>& options_map() {
   static std::map<std::string, int64_t> m = {
-      {"greedy_splits", 0},   // workgroups per row in the greedy kernels
-      {"greedy_block", 0},    // unused placeholder kept for sweeps
-      {"sample_splits", 0},   // chunk workgroups per row in dense sampling
-      {"spec_block", 0},      // threads per row in the fused sampling verify
+      {"greedy_splits", 0},   // workgroups per row in the greedy kernels (0: by CU balance)
+      {"greedy_block", 0},    // greedy workgroup size, 256 / 512 / 1024 (0: 256)
   };
   return m;
 }
