@@ -511,6 +511,7 @@ struct RowSh {
   uint32_t sel32[2][2];
   uint64_t sel64[2][3];
   uint64_t red[2 * kRW];
+  uint64_t red2[2 * kRW];              // block_sum_n's own buffer
   uint64_t u64s[8];
   uint32_t u32s[8];
   float f32s[2][4];
@@ -545,6 +546,27 @@ __device__ __forceinline__ void block_excl_scan_n(const uint64_t (&v)[NS], uint6
       t += x;
     }
     ex[s] = base + inc[s] - v[s];
+    tot[s] = t;
+  }
+}
+
+// Sums over the workgroup of NS values at once, with one barrier. smem (NS *
+// kRW words) must not be read by a wave still inside a previous use: the
+// callers give it a buffer of its own.
+template <int NS>
+__device__ __forceinline__ void block_sum_n(const uint64_t (&v)[NS], uint64_t* smem, uint64_t (&tot)[NS]) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint64_t w = wave_scan_add_u64(v[s]);
+    if (lane == kWave - 1) smem[s * kRW + wid] = w;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint64_t t = 0;
+#pragma unroll
+    for (int i = 0; i < kRW; ++i) t += smem[s * kRW + i];
     tot[s] = t;
   }
 }
@@ -795,10 +817,10 @@ __device__ int pick_slot(RowSh& sh, int n, float u, W weight) {
   uint64_t sum = 0;
 #pragma unroll
   for (int q = 0; q < kSlotsPerLane; ++q) sum += s0 + q < n ? weight(s0 + q) : 0;
+  // the scan's barriers publish this before any lane can set it
+  if (t == 0) sh.u32s[3] = kNone;
   uint64_t total;
   const uint64_t ex = block_excl_scan(sum, sh.red, &total);
-  if (t == 0) sh.u32s[3] = kNone;
-  __syncthreads();
   if (total > 0) {
     const uint64_t target = floor_u_times(u, total);
     if (ex <= target && target < ex + sum) {
@@ -1256,8 +1278,8 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
         }
       }
     }
-    uint64_t ex[2], tot[2];
-    block_excl_scan_n<2>(sums, sh.red, ex, tot);
+    uint64_t tot[2];
+    block_sum_n<2>(sums, sh.red2, tot);
     const bool use_d = tot[0] > 0;
     const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
 #pragma unroll
