@@ -512,6 +512,7 @@ struct RowSh {
   uint64_t sel64[2][3];
   uint64_t red[2 * kRW];
   uint64_t red2[2 * kRW];              // block_sum_n's own buffer
+  uint64_t red3[2 * kRW];              // the radix selects' own scan buffer
   uint64_t u64s[8];
   uint32_t u32s[8];
   float f32s[2][4];
@@ -522,15 +523,17 @@ struct RowSh {
 };
 
 // Exclusive scans in lane order over the workgroup of NS values at once;
-// tot receives the sums. smem holds NS * kRW words.
-template <int NS>
+// tot receives the sums. smem holds NS * kRW words. LEAD = false drops the
+// leading barrier, for a caller whose smem has a barrier between this and its
+// previous use.
+template <int NS, bool LEAD = true>
 __device__ __forceinline__ void block_excl_scan_n(const uint64_t (&v)[NS], uint64_t* smem, uint64_t (&ex)[NS],
                                                   uint64_t (&tot)[NS]) {
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   uint64_t inc[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) inc[s] = wave_scan_add_u64(v[s]);
-  __syncthreads();
+  if constexpr (LEAD) __syncthreads();
   if (lane == kWave - 1) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) smem[s * kRW + wid] = inc[s];
@@ -670,6 +673,12 @@ __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Vis
       }
       __syncthreads();
     }
+    // this round's crossing digit and gather count start empty (the barrier
+    // below orders these stores before any use)
+    if (t < NS) {
+      sh.sel32[t][0] = kNone;
+      sh.gcount[t] = 0;
+    }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if (!done[s]) {
@@ -693,9 +702,7 @@ __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Vis
         sum[s] += v[s][q];
       }
     }
-    block_excl_scan_n<NS>(sum, sh.red, ex, tot);
-    if (t < NS) sh.sel32[t][0] = kNone;
-    __syncthreads();
+    block_excl_scan_n<NS, false>(sum, sh.red3, ex, tot);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       uint64_t before = above[s] + ex[s];
@@ -711,7 +718,6 @@ __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Vis
         }
       }
     }
-    if (t < NS) sh.gcount[t] = 0;
     __syncthreads();
     uint64_t binmass[NS];
 #pragma unroll
