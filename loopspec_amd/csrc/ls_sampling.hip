@@ -823,10 +823,14 @@ __device__ int pick_slot(RowSh& sh, int n, float u, W weight) {
   uint64_t sum = 0;
 #pragma unroll
   for (int q = 0; q < kSlotsPerLane; ++q) sum += s0 + q < n ? weight(s0 + q) : 0;
-  // the scan's barriers publish this before any lane can set it
+  // the scan's barrier publishes this before any lane can set it
   if (t == 0) sh.u32s[3] = kNone;
-  uint64_t total;
-  const uint64_t ex = block_excl_scan(sum, sh.red, &total);
+  const uint64_t vv[1] = {sum};
+  uint64_t exv[1], totv[1];
+  // no leading barrier: every caller reaches this through a barrier after
+  // its last other use of sh.red
+  block_excl_scan_n<1, false>(vv, sh.red, exv, totv);
+  const uint64_t ex = exv[0], total = totv[0];
   if (total > 0) {
     const uint64_t target = floor_u_times(u, total);
     if (ex <= target && target < ex + sum) {
@@ -1005,7 +1009,10 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
   for (int i = a; i < b; ++i) cnt += pval(i) >= cc ? 1 : 0;
   uint64_t total;
   const uint64_t ex = block_excl_scan(cnt, sh.red, &total);
-  if (total > static_cast<uint64_t>(kRowCand)) return -1;
+  if (total > static_cast<uint64_t>(kRowCand)) {
+    __syncthreads();  // every wave is past its reads of sh.red
+    return -1;
+  }
   int pos = static_cast<int>(ex);
   for (int i = a; i < b; ++i) {
     const float pv = pval(i);
@@ -1171,22 +1178,22 @@ __device__ void publish_draw(const SampParams& p, RowSh& sh, int64_t g, int i, u
     sh.u32s[7] = last ? 1u : 0u;
   }
   __syncthreads();
-  if (!sh.u32s[7]) return;
-  if (t <= k) sh.draws[t] = load_sc64(reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1) + t);
-  int64_t x = -1;
-  if (wid == 0 && lane < k) x = p.draft_tokens[g * k + lane];
-  __syncthreads();
-  if (wid == 0) {
-    const uint64_t bad = __ballot(lane < k && !(sh.draws[lane] >> 63));
-    const int a = bad ? __builtin_ctzll(bad) : k;
-    const int64_t da = static_cast<int64_t>(sh.draws[a] & ~(1ull << 63));
-    int64_t* out = p.tokens + g * (k + 1);
-    if (lane < a) out[lane] = x;
-    if (lane == a) out[lane] = da;
-    if (lane > a && lane <= k) out[lane] = -1;
-    if (k >= kWave && lane == 0) out[k] = a == k ? da : -1;
-    if (lane == 0) p.accept_len[g] = a;
-  }
+  if (!sh.u32s[7] || wid != 0) return;
+  // wave 0 alone: lane l holds draw l (lane 0 also draw 64 when k == 64)
+  const uint64_t* dw = reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1);
+  const uint64_t d = lane <= k ? load_sc64(dw + lane) : 0;
+  const uint64_t d64 = (k >= kWave && lane == 0) ? load_sc64(dw + kWave) : 0;
+  const int64_t x = lane < k ? p.draft_tokens[g * k + lane] : -1;
+  const uint64_t bad = __ballot(lane < k && !(d >> 63));
+  const int a = bad ? __builtin_ctzll(bad) : k;
+  const uint64_t wa = a < kWave ? __shfl(d, a) : __shfl(d64, 0);
+  const int64_t da = static_cast<int64_t>(wa & ~(1ull << 63));
+  int64_t* out = p.tokens + g * (k + 1);
+  if (lane < a) out[lane] = x;
+  if (lane == a) out[lane] = da;
+  if (lane > a && lane <= k) out[lane] = -1;
+  if (k >= kWave && lane == 0) out[k] = a == k ? da : -1;
+  if (lane == 0) p.accept_len[g] = a;
 }
 
 // Spec mode: one workgroup per (batch element g, position i). i < k: the
