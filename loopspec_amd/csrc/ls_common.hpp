@@ -61,6 +61,29 @@ __device__ __forceinline__ float load_elem(const void* row, int64_t i) {
   }
 }
 
+// Element i's storage bits (16-bit types zero-extended by the load itself) and
+// their decode, apart: a gather of bits leaves its loads outstanding until the
+// decode at the values' use, where a decoding load would wait for them at once.
+template <int DT>
+__device__ __forceinline__ uint32_t load_bits(const void* row, int64_t i) {
+  if constexpr (DT == F32) {
+    return static_cast<const uint32_t*>(row)[i];
+  } else {
+    return static_cast<const uint16_t*>(row)[i];
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float bits_to_float(uint32_t b) {
+  if constexpr (DT == F32) {
+    return __uint_as_float(b);
+  } else if constexpr (DT == BF16) {
+    return __uint_as_float(b << 16);
+  } else {
+    return f16_bits_to_float(b);
+  }
+}
+
 // NaN-propagating maximum (IEEE-754 2019 `maximum`); lowers to v_maximum3_f32.
 __device__ __forceinline__ float nmax(float a, float b) {
   return __builtin_elementwise_maximum(a, b);

@@ -1219,16 +1219,18 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   const int64_t r[2] = {g * rpg + (bonus ? k : i), g * rpg + (bonus ? k : k + 1 + i)};
   const char* trow = row_of(p, g, bonus ? k : i);
   const char* drow = row_of(p, g, bonus ? k : k + 1 + i);
-  // the draft logits at the target's candidates, gathered during the selects
-  float lq[kSlotsPerLane];
+  // the draft logits' bits at the target's candidates, gathered during the
+  // selects and decoded at their use (the bonus workgroup has no draft row)
+  uint32_t lq[kSlotsPerLane];
   auto gather = [&] {
+    if (bonus) return;
 #pragma unroll
     for (int q = 0; q < kSlotsPerLane; ++q) {
       const int sl = t + q * kRB;
-      lq[q] = 0.0f;
+      lq[q] = 0u;
       if (sl < nslots && slot_valid(sh, 0, p, sl)) {
         const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
-        lq[q] = load_elem<DT>(drow, idx < p.vocab ? idx : 0);
+        lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
       }
     }
   };
@@ -1250,10 +1252,10 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
 #pragma unroll
     for (int q = 0; q < kSlotsPerLane; ++q) {
       const int sl = t + q * kRB;
-      lq[q] = 0.0f;
+      lq[q] = 0u;
       if (sl < nt) {
         const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
-        lq[q] = load_elem<DT>(drow, idx < p.vocab ? idx : 0);
+        lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
       }
     }
   }
@@ -1284,7 +1286,7 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
         const float pv = __uint_as_float(static_cast<uint32_t>(v));
         if (pv > 0.0f && pv >= st_t.cutoff) {
           P[q] = pv / st_t.mass;
-          const float dv = P[q] - Qof(lq[q], static_cast<int>(v >> 32));
+          const float dv = P[q] - Qof(bits_to_float<DT>(lq[q]), static_cast<int>(v >> 32));
           D[q] = dv > 0.0f ? dv : 0.0f;
           sums[0] += fx46(D[q]);
           sums[1] += fx46(P[q]);

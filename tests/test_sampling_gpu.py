@@ -307,6 +307,33 @@ def test_spec_verify_alternating_shapes_share_workspace(gpu):
         assert np.array_equal(tok.cpu().numpy(), want.tokens), (b, k)
 
 
+@pytest.mark.parametrize("support", [300, 1000, 1900])
+def test_spec_verify_large_draft_supports(gpu, support):
+    """Rows whose top-p support is `support` near-equal tokens out of 65536
+    (32 chunks, 2048 candidate slots). At 300 and 1000 every chunk's support
+    fits its candidates (fast path, hundreds of residual terms); at 1900 some
+    chunks hold more than 64 and the rows take the whole-row select, keeping
+    their support on the slots for the residual and bonus draws."""
+    vocab, batch, k = 65536, 3, 2
+    rng = np.random.default_rng(support)
+    target = np.full((batch, k + 1, vocab), -30.0, dtype=np.float32)
+    for b in range(batch):
+        for i in range(k + 1):
+            pos = rng.choice(vocab, size=support, replace=False)
+            target[b, i, pos] = 5.0 + rng.normal(0.0, 0.05, size=support)
+    draft = target[:, :k] + np.where(target[:, :k] > 0, rng.normal(0.0, 0.05, size=(batch, k, vocab)), 0.0)
+    cfg = workloads.SamplingConfig("support", batch, k, vocab, torch.float32, 1.0, 0.9)
+    inp = {"target": torch.from_numpy(target), "draft": torch.from_numpy(draft.astype(np.float32)),
+           "uniforms": torch.from_numpy(philox.uniforms((batch, 2 * k + 1), seed=support)),
+           "draft_uniforms": torch.from_numpy(philox.uniforms((batch, k), seed=support + 1))}
+    drafts = draft_tokens_from(inp, cfg)
+    announce(f"spec large draft support {support}")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
+
+
 @pytest.mark.parametrize("batch,k,vocab,dtype,top_p", [
     (1, 64, 4096, torch.float32, 0.8),        # the largest k: 65 draws per element
     (2, 1, 262144, torch.bfloat16, 0.9),      # the largest vocabulary: 128 chunks, 16 slots each
