@@ -645,10 +645,15 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t bits, int shift, uint32_t 
 // top; sh.H[s] zero on entry); after each round a bucket of at most kGather
 // entries is finished by one wave (wave s for set s). found[s] is false when
 // the set's total mass is below thr. The sets advance in lockstep, so NS rows
-// cost the barriers of one.
-template <int NS, typename Visit>
+// cost the barriers of one. after_r0(d) runs on every lane once round 0 has
+// found set 0's crossing digit d (the top 12 bits, bits >> kRound0Shift; kNone
+// if the set holds less than thr): every element of p >= the cutoff has a
+// digit >= d, so loads issued there for those elements overlap the rest.
+constexpr int kRound0Shift = 19;
+
+template <int NS, typename Visit, typename AfterR0>
 __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Visit visit, bool (&found)[NS],
-                               float (&cut)[NS], uint64_t (&mass)[NS]) {
+                               float (&cut)[NS], uint64_t (&mass)[NS], AfterR0 after_r0) {
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
   uint32_t prefix[NS], pmask[NS];
   uint64_t above[NS];
@@ -661,7 +666,7 @@ __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Vis
     found[s] = false;
   }
   for (int round = 0; round < 3; ++round) {
-    const int shift = round == 0 ? 19 : (round == 1 ? 8 : 0);
+    const int shift = round == 0 ? kRound0Shift : (round == 1 ? 8 : 0);
     const uint32_t dmask = round == 0 ? 0xfffu : (round == 1 ? 0x7ffu : 0xffu);
     if (round > 0) {
 #pragma unroll
@@ -735,6 +740,7 @@ __device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Vis
         }
       }
     }
+    if (round == 0) after_r0(sh.sel32[0][0]);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if (!done[s]) {
@@ -954,7 +960,7 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
       const float x = __uint_as_float(bits);
       if (x > 0.0f) f(bits, fx46(x));
     }
-  }, found, cc1, mfx1);
+  }, found, cc1, mfx1, [](uint32_t) {});
   if (found[0] && bound_repair<DT>(sh, set, rowp, bm, c, pen, inv_pen, vocab, nch, cc1[0])) {
     if (t == 0) {
       sh.slow_cut[set] = cc1[0];
@@ -973,7 +979,7 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
       const float pv = pval(i);
       f(__float_as_uint(pv), fx46(pv));
     }
-  }, found, cc1, mfx1);
+  }, found, cc1, mfx1, [](uint32_t) {});
   float cc = cc1[0];
   uint64_t mfx = mfx1[0];
   if (!found[0]) {
@@ -1034,13 +1040,13 @@ __device__ __forceinline__ bool slot_valid(const RowSh& sh, int set, const SampP
 // Finalisation of NS rows side by side (set s = row r[s]): scales, p of the
 // candidates into sh.slot[s] (idx << 32 | bits(p), 0 for empty slots), the
 // exact top-p cutoff (candidates, or the re-streamed row when they do not hold
-// it). after_p() runs once the slots are written, before the selects, so
-// loads issued there overlap them. Outputs the row statistics, the filtered
-// probability of each row's draft token (-1 if the row has none) and, for a
-// row that took the slow path with keep_support, the size of its support.
-template <int DT, int NS, typename After>
+// it). after_r0 is the candidates' select's round-0 hook (set 0's crossing
+// digit). Outputs the row statistics, the filtered probability of each row's
+// draft token (-1 if the row has none) and, for a row that took the slow path
+// with keep_support, the size of its support.
+template <int DT, int NS, typename AfterR0>
 __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)[NS], bool keep_support,
-                              RowStat (&st)[NS], float (&P_tok)[NS], int (&n_sup)[NS], After after_p) {
+                              RowStat (&st)[NS], float (&P_tok)[NS], int (&n_sup)[NS], AfterR0 after_r0) {
   const int t = threadIdx.x, wid = t / kWave;
   const int nch = p.nch;
   const int nslots = nch * p.cap;
@@ -1089,7 +1095,6 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
       if (sl < nslots) sh.slot[s][sl] = ((cv[s][q] >> 32) << 32) | __float_as_uint(pv[s][q]);
     }
   }
-  after_p();
   // 4. cutoffs
   uint64_t thr[NS];
   bool found[NS];
@@ -1107,7 +1112,7 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
         const float x = pv[s][q];
         if (x > 0.0f) f(__float_as_uint(x), fx46(x));
       }
-    }, found, cut, mfx);
+    }, found, cut, mfx, after_r0);
   }
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -1219,18 +1224,23 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   const int64_t r[2] = {g * rpg + (bonus ? k : i), g * rpg + (bonus ? k : k + 1 + i)};
   const char* trow = row_of(p, g, bonus ? k : i);
   const char* drow = row_of(p, g, bonus ? k : k + 1 + i);
-  // the draft logits' bits at the target's candidates, gathered during the
-  // selects and decoded at their use (the bonus workgroup has no draft row)
-  uint32_t lq[kSlotsPerLane];
-  auto gather = [&] {
-    if (bonus) return;
+  // the draft logits' bits at the target's candidates that can be in its
+  // support (digit >= the target select's round-0 crossing digit d0), gathered
+  // during the rest of the select and decoded at their use (the bonus
+  // workgroup has no draft row)
+  uint32_t lq[kSlotsPerLane] = {};
+  auto gather = [&](uint32_t d0) {
+    if (bonus || d0 == kNone) return;
 #pragma unroll
     for (int q = 0; q < kSlotsPerLane; ++q) {
       const int sl = t + q * kRB;
-      lq[q] = 0u;
-      if (sl < nslots && slot_valid(sh, 0, p, sl)) {
-        const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
-        lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
+      if (sl < nslots) {
+        const uint64_t v = sh.slot[0][sl];
+        const uint32_t bits = static_cast<uint32_t>(v);
+        if (bits != 0u && (bits >> kRound0Shift) >= d0) {
+          const int idx = static_cast<int>(v >> 32);
+          lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
+        }
       }
     }
   };
@@ -1354,7 +1364,7 @@ __global__ __launch_bounds__(kRB) void row_kernel(const SampParams p) {
   RowStat st[1];
   float P_tok[1];
   int n_sup[1];
-  finalize_rows<DT, 1>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [] {});
+  finalize_rows<DT, 1>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [](uint32_t) {});
   if constexpr (MODE == kModeSample) {
     const uint32_t* bm = p.use_pen ? p.bitmap + r[0] * p.bm_words : nullptr;
     const int64_t token = own_draw<DT>(p, sh, 0, st[0], (st[0].flags & kFlagSlow) ? n_sup[0] : p.nch * p.cap,
