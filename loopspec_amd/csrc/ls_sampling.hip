@@ -63,7 +63,8 @@ constexpr int64_t kMaxSpecBatch = 16384;
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
-enum RowFlag : uint32_t { kFlagUnfiltered = 1u, kFlagDense = 2u, kFlagSlow = 4u };
+// kFlagRebuilt: the candidates of some chunks were replaced (same slot layout)
+enum RowFlag : uint32_t { kFlagUnfiltered = 1u, kFlagDense = 2u, kFlagSlow = 4u, kFlagRebuilt = 8u };
 enum ChunkFlag : uint32_t { kChunkComplete = 1u, kChunkHasTok = 2u };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -927,19 +928,109 @@ __device__ __forceinline__ bool bound_repair(RowSh& sh, int set, const char* row
   return !any;
 }
 
-// Exact select over every element of the row of set `set` (its candidates
-// did not hold the cutoff; first, when they held top_p, the bound repair,
-// which returns kRepaired when the candidates' cutoff cand_cut stands): p recomputed from the re-read logits with the
-// set's g_j. When keep is set, leaves the support {p >= c} in index order in
-// sh.slot[set] (as idx << 32 | bits(p)) and returns its size, or -1 if it does
-// not fit. The cutoff and its fx46 mass go to sh.slow_cut / sh.slow_mass.
-// Out of line, with plain arguments and no pointers into the caller's frame,
-// so the common path's registers are unaffected.
-constexpr int kRepaired = -2;  // slow_select: the candidates' cutoff stands
+// Chunk rebuild, when the bound repair found a non-candidate p >= cut (the
+// candidates' cutoff): the candidates of every chunk whose bound reaches cut
+// become {p >= cut} of that chunk, in index order, if they fit its cap slots.
+// cut is a lower bound of the row's cutoff (the candidates alone hold top_p
+// at p >= cut), and the other chunks hold no p >= cut, so afterwards the
+// slots hold every element of p >= the row's cutoff and their select is exact.
+// Returns false (slots partly rewritten) if some chunk does not fit. Out of
+// line, like slow_select.
+template <int DT>
+__device__ __noinline__ bool rebuild_chunks(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c,
+                                               float pen, float inv_pen, int vocab, int nch, int cap, float cut) {
+  constexpr int kQ = kChunk / kRB;
+  static_assert(kQ * kRW <= kGather, "per-(q, wave) counts fit sh.gbits[0]");
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  // at fixed offsets (sets are rebuilt one at a time), so the count reads
+  // take immediate offsets rather than per-read addresses
+  uint32_t* cnt = sh.gbits[0];
+#pragma nounroll
+  for (int j = 0; j < nch; ++j) {
+    const int K = sh.kb[set][j];
+    if (K >= kOctBins) continue;
+    const float gj = sh.g[set][j];
+    const float th = K > 0 ? __builtin_ldexpf(kCandScale, -K) : __builtin_inff();
+    if (K > 0 && !(th * gj >= cut)) continue;  // chunk_bound below cut
+    const float nmc = -sh.mcj[set][j];
+    const int c0 = j * kChunk;
+    float pq[kQ];
+    uint64_t mq[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      // element c0 + q*kRB + t: (q, t) order is index order
+      const int i = c0 + t + q * kRB;
+      pq[q] = 0.0f;
+      if (i < vocab) {
+        float l = load_elem<DT>(rowp, i);
+        if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
+        pq[q] = exp2q(__builtin_fmaf(l, c, nmc)) * gj;
+      }
+      mq[q] = __ballot(pq[q] > 0.0f && pq[q] >= cut);
+      if (lane == 0) cnt[q * kRW + wid] = static_cast<uint32_t>(__builtin_popcountll(mq[q]));
+    }
+    __syncthreads();
+    // lane l < kQ*kRW holds count l = (q, w) in (q, t) order; an inclusive
+    // scan over the lanes gives each wave base[q], the flagged elements
+    // before its own of round q
+    int incl = lane < kQ * kRW ? static_cast<int>(cnt[lane]) : 0;
+#pragma unroll
+    for (int d = 1; d < kQ * kRW; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      incl += lane >= d ? o : 0;
+    }
+    const int total = __shfl(incl, kQ * kRW - 1);
+    int base[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int l = q * kRW + wid;
+      base[q] = __shfl(incl, l) - static_cast<int>(cnt[l]);
+    }
+    if (total > cap) {
+      __syncthreads();  // every wave is past its reads of cnt
+      return false;
+    }
+    uint64_t* slots = sh.slot[set] + j * cap;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      if ((mq[q] >> lane) & 1u) {
+        const int pos = base[q] + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                      static_cast<uint32_t>(mq[q] >> 32),
+                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mq[q]), 0u)));
+        slots[pos] = (static_cast<uint64_t>(c0 + t + q * kRB) << 32) | __float_as_uint(pq[q]);
+      }
+    }
+    if (t >= total && t < cap) slots[t] = 0;
+    if (t == 0) {
+      sh.n[set][j] = static_cast<uint32_t>(total);
+      sh.kb[set][j] = static_cast<uint8_t>(kOctBins);
+    }
+    __syncthreads();  // slots written; cnt free for the next chunk
+  }
+  return true;
+}
+
+// Cutoff of the row of set `set` when its candidates' cutoff did not pass the
+// bound. mode kSlowCand: the candidates' select again; if they hold top_p,
+// the bound repair returns kRepaired when their cutoff stands, else
+// kNeedRebuild (for the chunk rebuild, then mode kSlowRebuilt: the select over
+// the rebuilt slots, exact, returns kRebuilt). Otherwise (and in mode
+// kSlowRow) the exact select over every element of the row, p recomputed from
+// the re-read logits with the set's g_j; when keep is set, it leaves the
+// support {p >= c} in index order in sh.slot[set] (as idx << 32 | bits(p))
+// and returns its size, or -1 if it does not fit. The cutoff and its fx46
+// mass go to sh.slow_cut / sh.slow_mass. Out of line, with plain arguments
+// and no pointers into the caller's frame, so the common path's registers are
+// unaffected.
+constexpr int kRepaired = -2;     // the candidates' cutoff stands
+constexpr int kRebuilt = -3;      // the rebuilt slots' cutoff
+constexpr int kNeedRebuild = -4;  // the candidates hold top_p but a non-candidate reaches their cutoff
+enum SlowMode : int { kSlowCand = 0, kSlowRebuilt = 1, kSlowRow = 2 };
 
 template <int DT>
 __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
-                                        float inv_pen, int vocab, int nch, int nslots, uint64_t thr, bool keep) {
+                                        float inv_pen, int vocab, int nch, int nslots, uint64_t thr, bool keep,
+                                        int mode) {
   const int t = threadIdx.x, wid = t / kWave;
   const float* mcj = sh.mcj[set];
   const float* gj = sh.g[set];
@@ -948,26 +1039,33 @@ __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, co
   bool found[1];
   float cc1[1];
   uint64_t mfx1[1];
-  // 1. the candidates' select again (their p are still in sh.slot[set]); when
-  //    they hold top_p, the bound repair may confirm their cutoff
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
-  __syncthreads();
-  radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
-    for (int sl = t; sl < nslots; sl += kRB) {
-      const uint32_t bits = static_cast<uint32_t>(sh.slot[set][sl]);
-      const float x = __uint_as_float(bits);
-      if (x > 0.0f) f(bits, fx46(x));
-    }
-  }, found, cc1, mfx1, [](uint32_t) {});
-  if (found[0] && bound_repair<DT>(sh, set, rowp, bm, c, pen, inv_pen, vocab, nch, cc1[0])) {
-    if (t == 0) {
-      sh.slow_cut[set] = cc1[0];
-      sh.slow_mass[set] = mfx1[0];
-    }
+  // 1. the select over the slots (the candidates' p are still in
+  //    sh.slot[set], or the rebuilt chunks')
+  if (mode != kSlowRow) {
     __syncthreads();
-    return kRepaired;
+#pragma unroll
+    for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
+    __syncthreads();
+    radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
+      for (int sl = t; sl < nslots; sl += kRB) {
+        const uint32_t bits = static_cast<uint32_t>(sh.slot[set][sl]);
+        const float x = __uint_as_float(bits);
+        if (x > 0.0f) f(bits, fx46(x));
+      }
+    }, found, cc1, mfx1, [](uint32_t) {});
+    if (found[0]) {
+      if (mode == kSlowCand && !bound_repair<DT>(sh, set, rowp, bm, c, pen, inv_pen, vocab, nch, cc1[0])) {
+        if (t == 0) sh.slow_cut[set] = cc1[0];
+        __syncthreads();
+        return kNeedRebuild;
+      }
+      if (t == 0) {
+        sh.slow_cut[set] = cc1[0];
+        sh.slow_mass[set] = mfx1[0];
+      }
+      __syncthreads();
+      return mode == kSlowCand ? kRepaired : kRebuilt;
+    }
   }
   // 2. exact select over the whole row
   __syncthreads();
@@ -1130,13 +1228,21 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
       } else {
         const int64_t g = r[s] / p.rpg;
         const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
-        const int n = slow_select<DT>(sh, s, row_of(p, g, static_cast<int>(r[s] - g * p.rpg)), bm, p.c, p.pen,
-                                      p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support);
+        const char* rowp = row_of(p, g, static_cast<int>(r[s] - g * p.rpg));
+        int n = slow_select<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
+                                kSlowCand);
+        if (n == kNeedRebuild) {
+          // the deficient chunks' candidates become {p >= the candidates' cutoff}
+          const bool fits = rebuild_chunks<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, p.cap,
+                                               sh.slow_cut[s]);
+          n = slow_select<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
+                              fits ? kSlowRebuilt : kSlowRow);
+        }
         st[s].cutoff = sh.slow_cut[s];
         st[s].mass_fx = sh.slow_mass[s];
-        const bool rep = n == kRepaired;
-        st[s].flags |= rep ? 0u : (kFlagSlow | ((!keep_support || n < 0) ? kFlagDense : 0u));
-        n_sup[s] = rep ? nslots : n;
+        const bool rep = n == kRepaired, reb = n == kRebuilt;
+        st[s].flags |= rep ? 0u : (reb ? kFlagRebuilt : (kFlagSlow | ((!keep_support || n < 0) ? kFlagDense : 0u)));
+        n_sup[s] = rep || reb ? nslots : n;
       }
     }
     st[s].mass = unf[s] ? 1.0f : mass_to_f32(st[s].mass_fx);
@@ -1257,15 +1363,19 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
     publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
     return;
   }
-  if ((st[0].flags & (kFlagSlow | kFlagDense)) == kFlagSlow) {
-    // the support replaced the candidates: gather the draft logits again
+  if ((st[0].flags & kFlagRebuilt) || (st[0].flags & (kFlagSlow | kFlagDense)) == kFlagSlow) {
+    // the support or rebuilt chunks replaced candidates: gather the draft
+    // logits again (slots with p > 0 hold token indices)
 #pragma unroll
     for (int q = 0; q < kSlotsPerLane; ++q) {
       const int sl = t + q * kRB;
       lq[q] = 0u;
       if (sl < nt) {
-        const int idx = static_cast<int>(sh.slot[0][sl] >> 32);
-        lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
+        const uint64_t v = sh.slot[0][sl];
+        if (static_cast<uint32_t>(v) != 0u) {
+          const int idx = static_cast<int>(v >> 32);
+          lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
+        }
       }
     }
   }

@@ -10,10 +10,13 @@ build rows that take each path:
           outside the candidates (kCandScale * 2^-K_j * g_j per chunk);
   repair  it does not, but re-reading the chunks whose bound reaches it shows
           every non-candidate p below it (the candidates' cutoff stands);
-  slow    some non-candidate reaches it, or the candidates hold less than
-          top_p: the whole row is selected exactly.
+  rebuild some non-candidate reaches it, and in every chunk whose bound
+          reaches it {p >= the candidates' cutoff} fits the chunk's slots: those
+          chunks' candidates are replaced by that set and selected again;
+  slow    otherwise, or when the candidates hold less than top_p: the whole
+          row is selected exactly.
 
-The three paths must give identical results; the oracle computes the result
+The four paths must give identical results; the oracle computes the result
 directly, without candidates.
 """
 
@@ -70,18 +73,29 @@ def row_path(x: np.ndarray, temperature: float, top_p: float, epv: int = 4) -> s
     if cut > max(bounds):
         return "fast"
     outside = p[~cand]
-    return "repair" if not (outside >= cut).any() else "slow"
+    if not (outside >= cut).any():
+        return "repair"
+    for j in range(nch):
+        if bounds[j] >= cut and int((p[j * CHUNK:(j + 1) * CHUNK] >= cut).sum()) > cap:
+            return "slow"
+    return "rebuild"
 
 
 def repair_rows(vocab: int = 4096) -> dict[str, np.ndarray]:
-    """Rows of two chunks built to take the repair and the slow path.
+    """Rows of two chunks built to take the repair, rebuild and slow paths.
 
-    Chunk 1 holds 60 entries at its max (exponent bin 0) and 10 just below
-    (bin 1), so its K is 1 and only the 60 are candidates, with a worst-case
-    bound of 0.7071 g on the rest. Chunk 0 (same max) holds one entry at the
-    max and five at 2^-0.6, which set the cutoff at 0.66 g for top_p 0.9,
-    below that bound. The ten bin-1 entries sit at 2^-1 (repair: they stay
-    below the cutoff) or at 2^-0.52 (slow: they reach it).
+    repair / slow: chunk 1 holds 60 entries at its max (exponent bin 0) and
+    10 just below (bin 1), so its K is 1 and only the 60 are candidates, with
+    a worst-case bound of 0.7071 g on the rest. Chunk 0 (same max) holds one
+    entry at the max and five at 2^-0.6, which set the cutoff at 0.66 g for
+    top_p 0.9, below that bound. The ten bin-1 entries sit at 2^-1 (repair:
+    they stay below the cutoff) or at 2^-0.52 (slow: they reach it, and chunk
+    1's {p >= cutoff} is 70 entries, more than its 64 slots).
+
+    rebuild: chunk 0 holds 40 entries at the max and 20 at 2^-0.6; chunk 1
+    holds 50 at the max, 10 at 2^-0.52 and 5 at 2^-0.99 (15 in bin 1, so K is
+    1 and its 50 max entries are its candidates). The candidates' cutoff is
+    0.66 g, the ten at 2^-0.52 reach it, and chunk 1's {p >= cutoff} is 60.
     """
     ln2 = float(np.log(2.0))
     rows = {}
@@ -92,4 +106,11 @@ def repair_rows(vocab: int = 4096) -> dict[str, np.ndarray]:
         x[CHUNK:CHUNK + 60] = 10.0
         x[CHUNK + 500:CHUNK + 510] = 10.0 - depth * ln2
         rows[name] = x
+    x = np.full(vocab, -30.0, dtype=np.float32)
+    x[0:40] = 10.0
+    x[100:120] = 10.0 - 0.6 * ln2
+    x[CHUNK:CHUNK + 50] = 10.0
+    x[CHUNK + 500:CHUNK + 510] = 10.0 - 0.52 * ln2
+    x[CHUNK + 700:CHUNK + 705] = 10.0 - 0.99 * ln2
+    rows["rebuild"] = x
     return rows

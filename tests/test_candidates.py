@@ -10,6 +10,8 @@ def test_constructed_rows_take_each_path():
     rows = candidates.repair_rows()
     assert candidates.row_path(rows["repair"], 1.0, 0.9) == "repair"
     assert candidates.row_path(rows["slow"], 1.0, 0.9) == "slow"
+    assert candidates.row_path(rows["rebuild"], 1.0, 0.9) == "rebuild"
+    assert candidates.row_path(rows["rebuild"][::-1].copy(), 1.0, 0.9) == "rebuild"
 
 
 def test_typical_rows_are_fast():

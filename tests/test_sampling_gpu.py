@@ -109,9 +109,11 @@ def test_filter_logits_edge_rows(gpu, case):
 
 def test_filter_logits_repair_and_slow_rows(gpu):
     """Rows whose candidates' cutoff misses the worst-case bound: re-checked
-    chunk by chunk (repair) or selected exactly over the row (slow)."""
+    chunk by chunk (repair), with the deficient chunks' candidates rebuilt
+    (rebuild), or selected exactly over the row (slow)."""
     rows = candidates.repair_rows()
-    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["repair"][::-1].copy()]))
+    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["repair"][::-1].copy(), rows["rebuild"],
+                                   rows["rebuild"][::-1].copy()]))
     announce("filter repair/slow rows")
     res = verify.filter_logits(x.to(gpu), 1.0, 0.9, want_probs=True)
     torch.cuda.synchronize()
@@ -125,20 +127,21 @@ def test_filter_logits_repair_and_slow_rows(gpu):
 def test_sample_and_spec_repair_and_slow_rows(gpu):
     rows = candidates.repair_rows()
     v = rows["repair"].shape[0]
-    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"]] * 4))
+    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["rebuild"]] * 4))
     u = torch.from_numpy(philox.uniforms((x.shape[0],), seed=21))
     announce("sample repair/slow rows")
     got = verify.sample_logits(x.to(gpu), u.to(gpu), 1.0, 0.9)
     torch.cuda.synchronize()
     want = [osmp.categorical_pick(oracle_filter(x[r].numpy(), 1.0, 0.9).P, u[r].item()) for r in range(x.shape[0])]
     assert got.cpu().tolist() == want
-    # spec verify, B=4, k=1: target rows (pos 0, bonus) and draft rows from the two kinds
-    cfg = workloads.SamplingConfig("repair", 4, 1, v, torch.float32, 1.0, 0.9)
+    # spec verify, B=6, k=1: target rows (pos 0, bonus) and draft rows from the three kinds
+    cfg = workloads.SamplingConfig("repair", 6, 1, v, torch.float32, 1.0, 0.9)
     inp = workloads.sampling_inputs(cfg, 13)
-    for b in range(4):
-        inp["target"][b, 0] = torch.from_numpy(rows["repair" if b % 2 else "slow"])
-        inp["target"][b, 1] = torch.from_numpy(rows["slow" if b % 2 else "repair"])
-        inp["draft"][b, 0] = torch.from_numpy(rows["repair" if b < 2 else "slow"])
+    kinds = ["repair", "slow", "rebuild"]
+    for b in range(6):
+        inp["target"][b, 0] = torch.from_numpy(rows[kinds[b % 3]])
+        inp["target"][b, 1] = torch.from_numpy(rows[kinds[(b + 1) % 3]])
+        inp["draft"][b, 0] = torch.from_numpy(rows[kinds[(b // 2) % 3]])
     drafts = draft_tokens_from(inp, cfg)
     announce("spec repair/slow rows")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
