@@ -8,7 +8,10 @@ NSETS launches replayed K/NSETS times; the timed region is bracketed by HIP
 events on the stream the kernels run on, with device synchronisation on both
 sides. Prints one JSON line.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H]
+
+C2H is the vocabulary head fused with the greedy argmax (hidden states of C2's
+320 endpoint rows, Ouro-1.4B head: H=2048, V=49152, bf16 weight).
 """
 
 from __future__ import annotations
@@ -24,6 +27,7 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X published dense bf16 MFMA rate
 METRIC = "verify+sample rows/s + achieved HBM GB/s (% of peak), vocab 49152, B=64, k=2"
 COPY_CAL_ROWS, COPY_CAL_ROW_BYTES = 4096, 65536  # 256 MiB plain copy for PMC byte calibration
 
@@ -94,6 +98,74 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
         },
+    }
+
+
+# ---------------------------------------------------------------------------
+# C2H: vocabulary head fused with the greedy argmax
+# ---------------------------------------------------------------------------
+
+def bench_lm_head(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    from loopspec_amd import verify, workloads
+
+    rows, h, v = workloads.C2.batch * (2 * workloads.C2.k + 1), 2048, workloads.C2.vocab
+    _log(f"generating {nsets} hidden sets [{rows}, {h}] and two [{v}, {h}] bf16 head weights")
+    g = torch.Generator(device=device).manual_seed(31)
+    hid = [(torch.randn(rows, h, generator=g, device=device)).to(torch.bfloat16) for _ in range(nsets)]
+    # two weights (2 x 201 MB, more than the 256 MB Infinity Cache) alternate, so
+    # every step streams its weight from HBM as it would between model layers
+    wts = [(torch.randn(v, h, generator=g, device=device) * h ** -0.5).to(torch.bfloat16) for _ in range(2)]
+    out = torch.empty((nsets, rows), dtype=torch.int64, device=device)
+
+    def step(i: int) -> None:
+        verify.lm_head_argmax(hid[i], wts[i % 2], out=out[i])
+
+    ms_per_step, timed_steps, wsteps = _time_graph(step, nsets, steps, warmup)
+    pct = dict(_LAST_PERCENTILES)
+    # the unfused device path for comparison: bf16 GEMM (torch / hipBLASLt), then argmax
+    logits = [torch.empty((rows, v), dtype=torch.bfloat16, device=device) for _ in range(2)]
+    uout = torch.empty((nsets, rows), dtype=torch.int64, device=device)
+
+    def unfused(i: int) -> None:
+        torch.matmul(hid[i], wts[i % 2].t(), out=logits[i % 2])
+        verify.argmax_rows(logits[i % 2], out=uout[i])
+
+    unfused_ms, _, _ = _time_graph(unfused, nsets, steps // 4, warmup)
+    _LAST_PERCENTILES.clear()
+    _LAST_PERCENTILES.update(pct)
+    flops = 2.0 * rows * h * v
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    wbytes = v * h * 2
+    return {
+        "metric": "greedy rows/s from hidden states (vocab head + argmax), vocab 49152, H=2048, 320 rows",
+        "value": rows / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "steps": timed_steps,
+        "warmup": wsteps,
+        "ms_per_step": ms_per_step,
+        "dtype": "bf16",
+        "config": {
+            "workload": "C2H-lmhead-argmax-m320-h2048-v49152-bf16",
+            "rows": rows,
+            "hidden_size": h,
+            "vocab": v,
+            "input_sets": nsets,
+            "weights": 2,
+            "kernel": "ls::lm_head_kernel + ls::lm_head_finish_kernel",
+            "submission": "hipGraph of one call per step",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": None,
+            "weight_GBps": wbytes / (ms_per_step * 1e-3) / 1e9,
+            "weight_hbm_frac": wbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        },
+        "unfused_ms_per_step": unfused_ms,
+        "speedup_vs_unfused": unfused_ms / ms_per_step,
     }
 
 
@@ -340,6 +412,25 @@ def cpu_baseline_greedy(max_seconds: float = 20.0) -> dict:
     }
 
 
+def cpu_baseline_lm_head(max_seconds: float = 15.0) -> dict:
+    """torch-CPU vocabulary head + argmax (fp32 matmul of the bf16 inputs) on
+    64 rows at a time for about max_seconds; scaled to rows/s."""
+    rows, h, v = 64, 2048, 49152
+    g = torch.Generator().manual_seed(7)
+    hid = torch.randn(rows, h, generator=g).to(torch.bfloat16).float()
+    w = (torch.randn(v, h, generator=g) * h ** -0.5).to(torch.bfloat16).float()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        torch.argmax(hid @ w.T, dim=-1)
+        n += 1
+        if time.perf_counter() - t0 > max_seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": n * rows / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n} batches of 64 rows (H=2048, V=49152) in {dt:.1f}s; torch-CPU fp32 matmul + argmax",
+            "cpu_model": _cpu_model()}
+
+
 def cpu_baseline_c1(max_seconds: float = 10.0) -> dict:
     """C1, the reference's CPU target shape: batch-1 greedy verify steps (k=2,
     V=49152, fp32) on the torch-CPU restatement of decisions.py, up to 10k
@@ -444,6 +535,8 @@ def main() -> int:
     elif args.config == "C5":
         result = bench_c5(args.steps, args.warmup, device, args.sets)
         args.no_cpu_baseline = True
+    elif args.config == "C2H":
+        result = bench_lm_head(args.steps, args.warmup, device, args.sets)
     else:
         print(f"unknown config {args.config}", file=sys.stderr)
         return 2
@@ -453,6 +546,7 @@ def main() -> int:
         "C4": "synthetic (seeded N(0,4^2) bf16 logits, draft = target + N(0,1), Zipf(1.1) histories of "
               "U(256,4096) ids, drafts sampled from q, Philox uniforms)",
         "C5": "synthetic (C3 logits at B=128, drafts sampled from q; random bf16 KV pool, context U(512,8192))",
+        "C2H": "synthetic (seeded N(0,1) bf16 hidden states, two N(0,1/H) bf16 head weights alternated)",
     }[args.config]
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": data})
     # Traffic summaries are per launch unit: the greedy kernel (C2), or the
@@ -468,6 +562,8 @@ def main() -> int:
         if args.config == "C2":
             result["cpu_baseline"] = cpu_baseline_greedy()
             result["cpu_baseline"]["c1"] = cpu_baseline_c1()
+        elif args.config == "C2H":
+            result["cpu_baseline"] = cpu_baseline_lm_head()
         else:
             result["cpu_baseline"] = cpu_baseline_spec(workloads.C3 if args.config == "C3" else workloads.C4)
     order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "ms_per_step_p10",

@@ -91,6 +91,27 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride,
                      ls_stream_t stream);
 uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 
+/* Vocabulary head fused with the greedy argmax: out[m] = argmax_n of
+ * sum_k hidden[m][k] * weight[n][k] (bf16 inputs, fp32 MFMA accumulation;
+ * first index of the maximum, NaN first), without materialising the
+ * [rows, vocab] logits.
+ * Replaces: the logits producer (SGLang's LogitsProcessor over the
+ *   ParallelLMHead, sglang_recurrent/modeling/components.py:175-194) followed by
+ *   GreedyDecisionPolicy.queue's torch.argmax (sglang_recurrent/loopspec/decisions.py:116).
+ * hidden: bf16 [rows, hidden_size], row stride hidden_stride elements.
+ * weight: bf16 [vocab, hidden_size] (nn.Linear layout), row stride weight_stride.
+ * Both 16-byte aligned, strides multiples of 8 elements; hidden_size a multiple
+ * of 64; rows <= 65535 * 320. out: int64 [rows]. Workspace:
+ * ls_lm_head_argmax_workspace bytes (one partial key per 192 columns and row; no
+ * initial contents needed, every byte read is written first in the same call).
+ * Logits equal to fp32 accumulation in any order up to rounding: a row whose
+ * top two logits lie within that rounding may return either index. */
+int ls_lm_head_argmax(const void* hidden, int64_t hidden_stride, const void* weight,
+                      int64_t weight_stride, int dtype, int64_t rows, int64_t hidden_size,
+                      int64_t vocab, int64_t* out, void* workspace, uint64_t workspace_bytes,
+                      ls_stream_t stream);
+uint64_t ls_lm_head_argmax_workspace(int64_t rows, int64_t vocab);
+
 /* ------------------------------------------------------------------------------
  * (a) logit processing + (c) lossless speculative sampling
  *

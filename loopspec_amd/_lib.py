@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _P],
     ),
     "ls_greedy_verify_workspace": (_U64, [_I64, _I64, _I64]),
+    "ls_lm_head_argmax": (_I32, [_P, _I64, _P, _I64, _I32, _I64, _I64, _I64, _P, _P, _U64, _P]),
+    "ls_lm_head_argmax_workspace": (_U64, [_I64, _I64]),
     "ls_spec_verify": (
         _I32,
         [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I32, _I64, _I64, _I64, _F32, _F32, _I64, _F32,

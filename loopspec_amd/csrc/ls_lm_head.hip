@@ -1,0 +1,306 @@
+// Vocabulary head fused with the greedy argmax for gfx950.
+//
+// ids[m] = argmax_n sum_k hidden[m][k] * weight[n][k] (first index of the
+// maximum, NaN first), without writing the [M, V] logits: the reference
+// computes the logits with the vocabulary head (SGLang's LogitsProcessor over
+// ParallelLMHead, sglang_recurrent/modeling/components.py:175-194) and then
+// takes torch.argmax over every endpoint row
+// (sglang_recurrent/loopspec/decisions.py:116).
+//
+// Both operands are K-contiguous (hidden [M, H] row-major, weight [V, H] as
+// nn.Linear stores it), so each MFMA operand fragment is one 16-byte load.
+// One 512-lane workgroup computes a 320-row x 192-column tile with
+// v_mfma_f32_16x16x32_bf16: waves form a 2 (rows) x 4 (columns) grid, each
+// wave 10 x 3 tiles of 16 x 16 (120 accumulator registers). Both operands are
+// staged through LDS in k-blocks of 64 (16-byte chunks XOR-swizzled by row):
+// the weight by direct global-to-LDS loads (global_load_lds_dwordx4) two
+// blocks ahead into a ring of three buffers, so two blocks of HBM reads are in
+// flight while one is multiplied and no registers hold them; the hidden rows
+// (L2-resident) through registers one block ahead into two buffers. Each
+// block ends with an explicit wait that leaves the newest block's loads in
+// flight and a bare s_barrier (a workgroup fence would wait for them too).
+// The weight is read once; the hidden block (M x H bf16) is re-read by every
+// column block from L2. The epilogue reduces each row's
+// (value, -index) key over the tile's columns (in-lane over the three column
+// tiles, shuffles over the 16 lanes of a row, LDS over the four column waves)
+// and writes one key per (column block, row); a second kernel reduces a row's
+// keys to its index.
+#include "ls_common.hpp"
+#include "ls_runtime.hpp"
+
+namespace ls {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLmLanes = 512;
+constexpr int kLmMT = 10;                      // 16-row tiles per wave
+constexpr int kLmNT = 3;                       // 16-column tiles per wave
+constexpr int kLmRowsPerWave = 16 * kLmMT;     // 160
+constexpr int kLmColsPerWave = 16 * kLmNT;     // 48
+constexpr int kLmBM = 2 * kLmRowsPerWave;      // 320 rows per workgroup
+constexpr int kLmBN = 4 * kLmColsPerWave;      // 192 columns per workgroup
+constexpr int kLmKB = 64;                      // k per LDS block
+constexpr int kLmRowBytes = kLmKB * 2;         // 128 bytes of a row's k-block
+constexpr int kLmChunks = kLmBM * kLmRowBytes / 16;         // 2560 16-byte chunks per A block
+constexpr int kLmChunksPerLane = kLmChunks / kLmLanes;      // 5
+constexpr int kLmBChunks = kLmBN * kLmRowBytes / 16;        // 1536 per B block
+constexpr int kLmBChunksPerLane = kLmBChunks / kLmLanes;    // 3
+static_assert(kLmChunks % kLmLanes == 0 && kLmBChunks % kLmLanes == 0, "block chunks spread evenly");
+
+struct LmParams {
+  const char* hidden;   // [M, H] bf16, row stride hs elements
+  int64_t hs;
+  const char* weight;   // [V, H] bf16, row stride ws elements
+  int64_t ws;
+  int64_t M, H, V;
+  int nblk;             // column blocks (ceil(V / 192))
+  uint64_t* keys;       // [nblk, M] partial keys
+  int64_t* out;         // [M]
+};
+
+constexpr int kLmABytes = kLmBM * kLmRowBytes;  // 40 KB
+constexpr int kLmBBytes = kLmBN * kLmRowBytes;  // 24 KB
+static_assert(kLmBM * 4 * 8 <= kLmABytes, "epilogue keys fit an A buffer");
+
+
+
+// Direct global-to-LDS load of 16 bytes per lane: lane l's bytes land at LDS
+// address lds + 16 l (lds wave-uniform). Issued as an instruction the compiler
+// does not track, so that its own LDS-hazard waits do not stall reads of the
+// other buffers while the load is in flight; the caller waits for it
+// explicitly (vmcnt) before the workgroup reads the buffer.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+
+// Byte offset of 16-byte chunk c of row r in an A block.
+__device__ __forceinline__ int a_off(int r, int c) { return r * kLmRowBytes + ((c ^ (r & 7)) << 4); }
+
+__global__ __launch_bounds__(kLmLanes) void lm_head_kernel(const LmParams p) {
+  // separate arrays, so that the compiler's wait for a direct load into one
+  // weight buffer does not hold up reads of the others
+  __shared__ __attribute__((aligned(16))) uint8_t a0[kLmABytes], a1[kLmABytes];
+  __shared__ __attribute__((aligned(16))) uint8_t b0[kLmBBytes], b1[kLmBBytes], b2[kLmBBytes];
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int wm = wid >> 2, wn = wid & 3;
+  const int nblk = static_cast<int>(blockIdx.x);
+  const int64_t m_base = static_cast<int64_t>(blockIdx.y) * kLmBM;
+  const int64_t n_base = static_cast<int64_t>(nblk) * kLmBN;
+  const int nkb = static_cast<int>(p.H / kLmKB);
+
+  // Direct loads: round i of wave w puts lane l's 16 bytes at LDS chunk
+  // j = (8i + w) * 64 + l, i.e. row j/8 of the buffer, swizzled chunk l & 7,
+  // so the lane fetches logical chunk (l & 7) ^ (row & 7) of that row. Rows
+  // past the matrix are clamped into it (their results are never used).
+  // Byte offsets from the block's first row.
+  const uint32_t lchunk = static_cast<uint32_t>(((lane & 7) ^ ((lane >> 3) & 7)) << 4);
+  const char* abase = p.hidden + m_base * p.hs * 2;
+  uint32_t aoff[kLmChunksPerLane];
+#pragma unroll
+  for (int i = 0; i < kLmChunksPerLane; ++i) {
+    const int r = (i * 8 + wid) * 8 + (lane >> 3);
+    const int64_t rr = m_base + r < p.M ? r : p.M - 1 - m_base;
+    aoff[i] = static_cast<uint32_t>(rr * p.hs * 2) + lchunk;
+  }
+  const char* bbase = p.weight + n_base * p.ws * 2;
+  uint32_t boff[kLmBChunksPerLane];
+#pragma unroll
+  for (int i = 0; i < kLmBChunksPerLane; ++i) {
+    const int r = (i * 8 + wid) * 8 + (lane >> 3);
+    const int64_t rr = n_base + r < p.V ? r : p.V - 1 - n_base;
+    boff[i] = static_cast<uint32_t>(rr * p.ws * 2) + lchunk;
+  }
+  auto dma_a = [&](int kb, uint8_t* dst) {
+    const char* base = abase + static_cast<int64_t>(kb) * kLmRowBytes;
+#pragma unroll
+    for (int i = 0; i < kLmChunksPerLane; ++i) {
+      const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 8 + wid) * 1024;
+      dma16(base + aoff[i], __builtin_amdgcn_readfirstlane(lds));
+    }
+  };
+  auto dma_b = [&](int kb, uint8_t* dst) {
+    const char* base = bbase + static_cast<int64_t>(kb) * kLmRowBytes;
+#pragma unroll
+    for (int i = 0; i < kLmBChunksPerLane; ++i) {
+      const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 8 + wid) * 1024;
+      dma16(base + boff[i], __builtin_amdgcn_readfirstlane(lds));
+    }
+  };
+
+  f32x4 acc[kLmMT][kLmNT];
+#pragma unroll
+  for (int mt = 0; mt < kLmMT; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < kLmNT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // fragment rows: this wave's first row / column plus lane & 15 (tiles are a
+  // multiple of 16 rows apart, so the swizzle is fixed per lane and the rest
+  // is an immediate offset)
+  const int fr_a = (wm * kLmRowsPerWave + (lane & 15)) * kLmRowBytes;
+  const int fr_b = (wn * kLmColsPerWave + (lane & 15)) * kLmRowBytes;
+  auto compute = [&](const uint8_t* abuf, const uint8_t* bbuf) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int sw = ((ks * 4 + (lane >> 4)) ^ (lane & 7)) << 4;
+      const uint8_t* const fa = abuf + fr_a + sw;
+      const uint8_t* const fb = bbuf + fr_b + sw;
+      bf16x8 b[kLmNT];
+#pragma unroll
+      for (int nt = 0; nt < kLmNT; ++nt)
+        b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fb + nt * 16 * kLmRowBytes));
+      // rows in pairs of tiles, each pair's fragments read just before its
+      // MFMAs (a scheduling fence keeps all the reads from being hoisted)
+#pragma unroll
+      for (int mp = 0; mp < kLmMT; mp += 2) {
+        bf16x8 a[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          a[h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fa + (mp + h) * 16 * kLmRowBytes));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int nt = 0; nt < kLmNT; ++nt)
+            acc[mp + h][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h], b[nt], acc[mp + h][nt], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // End of block kb: every direct load but the newest weight block's
+  // (kLmBChunksPerLane of them, when issued) has landed in LDS, this lane's
+  // LDS reads are done, then the workgroup meets.
+  auto block_end = [&](bool newest_in_flight) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (newest_in_flight) {
+      __builtin_amdgcn_s_waitcnt(0x0073);  // vmcnt(3) expcnt(7) lgkmcnt(0)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7) lgkmcnt(0)
+    }
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  static_assert(kLmBChunksPerLane == 3, "block_end's vmcnt counts the newest block's direct loads");
+
+  // block kb: hidden rows in a[kb & 1], weight rows in b[kb % 3]; unrolled by
+  // six so that every buffer is named statically. Per block, the hidden rows
+  // of kb + 1, then the weight rows of kb + 2, go out before kb is multiplied,
+  // and block_end leaves only the latter in flight.
+  dma_a(0, a0);
+  dma_b(0, b0);
+  if (nkb > 1) dma_b(1, b1);
+  block_end(nkb > 1);
+  uint8_t* const A[2] = {a0, a1};
+  uint8_t* const B[3] = {b0, b1, b2};
+  for (int kb0 = 0; kb0 < nkb; kb0 += 6) {
+#pragma unroll
+    for (int u = 0; u < 6; ++u) {
+      const int kb = kb0 + u;
+      if (kb < nkb) {
+        if (kb + 1 < nkb) dma_a(kb + 1, A[(u + 1) & 1]);
+        const bool ahead = kb + 2 < nkb;
+        if (ahead) dma_b(kb + 2, B[(u + 2) % 3]);
+        compute(A[u & 1], B[u % 3]);
+        block_end(ahead);
+      }
+    }
+  }
+
+  uint64_t* const keys = reinterpret_cast<uint64_t*>(a0);  // every read of a0 is behind the last barrier
+  // epilogue: row keys over this wave's 48 columns, then over the 4 column waves
+#pragma unroll
+  for (int mt = 0; mt < kLmMT; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int nt = 0; nt < kLmNT; ++nt) {
+        const int64_t col = n_base + wn * kLmColsPerWave + nt * 16 + (lane & 15);
+        const uint64_t key = col < p.V ? argmax_key(acc[mt][nt][i], static_cast<uint32_t>(col)) : 0ull;
+        best = key > best ? key : best;
+      }
+#pragma unroll
+      for (int s = 1; s < 16; s <<= 1) {
+        const uint64_t o = __shfl_xor(best, s);
+        best = o > best ? o : best;
+      }
+      if ((lane & 15) == 0) keys[(wm * kLmRowsPerWave + mt * 16 + (lane >> 4) * 4 + i) * 4 + wn] = best;
+    }
+  }
+  __syncthreads();
+  for (int r = t; r < kLmBM; r += kLmLanes) {
+    const int64_t m = m_base + r;
+    if (m < p.M) {
+      uint64_t best = keys[r * 4];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) best = keys[r * 4 + w] > best ? keys[r * 4 + w] : best;
+      p.keys[static_cast<int64_t>(nblk) * p.M + m] = best;
+    }
+  }
+}
+
+// One wave per row: the maximum of the row's nblk keys.
+__global__ __launch_bounds__(256) void lm_head_finish_kernel(const LmParams p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (m >= p.M) return;
+  uint64_t best = 0;
+  for (int b = lane; b < p.nblk; b += kWave) {
+    const uint64_t k = p.keys[static_cast<int64_t>(b) * p.M + m];
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  if (lane == 0) p.out[m] = argmax_key_index(best);
+}
+
+}  // namespace
+}  // namespace ls
+
+using namespace ls;
+
+extern "C" {
+
+uint64_t ls_lm_head_argmax_workspace(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  const int64_t nblk = (vocab + kLmBN - 1) / kLmBN;
+  return (static_cast<uint64_t>(nblk) * static_cast<uint64_t>(rows) * 8u + 255u) & ~255ull;
+}
+
+int ls_lm_head_argmax(const void* hidden, int64_t hidden_stride, const void* weight, int64_t weight_stride,
+                      int dtype, int64_t rows, int64_t hidden_size, int64_t vocab, int64_t* out, void* workspace,
+                      uint64_t ws_bytes, ls_stream_t stream) {
+  if (dtype != LS_DTYPE_BF16) return fail(LS_ERR_VALUE, "lm_head_argmax: bf16 hidden states and weight only");
+  if (rows < 0 || hidden_size <= 0 || vocab <= 0 || vocab > 0x7fffffffLL)
+    return fail(LS_ERR_VALUE, "lm_head_argmax: need rows >= 0, hidden_size > 0, 0 < vocab < 2^31");
+  if (hidden_size % kLmKB != 0) return fail(LS_ERR_VALUE, "lm_head_argmax: hidden_size must be a multiple of 64");
+  if (rows == 0) return LS_OK;
+  if (hidden == nullptr || weight == nullptr || out == nullptr)
+    return fail(LS_ERR_VALUE, "lm_head_argmax: NULL pointer");
+  if (!aligned16(hidden) || !aligned16(weight) || hidden_stride % 8 != 0 || weight_stride % 8 != 0 ||
+      hidden_stride < hidden_size || weight_stride < hidden_size)
+    return fail(LS_ERR_VALUE, "lm_head_argmax: rows must be 16-byte aligned with strides >= hidden_size");
+  const int64_t nblk = (vocab + kLmBN - 1) / kLmBN;
+  const int64_t mblk = (rows + kLmBM - 1) / kLmBM;
+  if (mblk > 65535) return fail(LS_ERR_VALUE, "lm_head_argmax: too many rows");
+  if (workspace == nullptr || ws_bytes < ls_lm_head_argmax_workspace(rows, vocab))
+    return fail(LS_ERR_VALUE, "lm_head_argmax: workspace too small");
+  LmParams p{};
+  p.hidden = static_cast<const char*>(hidden);
+  p.hs = hidden_stride;
+  p.weight = static_cast<const char*>(weight);
+  p.ws = weight_stride;
+  p.M = rows;
+  p.H = hidden_size;
+  p.V = vocab;
+  p.nblk = static_cast<int>(nblk);
+  p.keys = static_cast<uint64_t*>(workspace);
+  p.out = out;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(lm_head_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(mblk)),
+                     dim3(kLmLanes), 0, st, p);
+  hipLaunchKernelGGL(lm_head_finish_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st, p);
+  return check_launch("lm_head_argmax launch");
+}
+
+}  // extern "C"

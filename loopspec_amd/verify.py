@@ -42,6 +42,40 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     return out
 
 
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy token of each row straight from the hidden states: argmax_n of
+    hidden [M, H] @ weight[V, H]^T (bf16, fp32 accumulation), one fused pass
+    that never writes the [M, V] logits.
+
+    Returns int64 [M]. Replaces the vocabulary head's logits
+    (sglang_recurrent/modeling/components.py:175-194) followed by torch.argmax
+    in GreedyDecisionPolicy.queue (sglang_recurrent/loopspec/decisions.py:116).
+    A row whose two largest logits lie within fp32 accumulation rounding may
+    return either index.
+    """
+    _lib.require_cuda(hidden, "lm_head_argmax")
+    _lib.require_cuda(weight, "lm_head_argmax")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("lm_head_argmax expects hidden [M, H] and weight [V, H]")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("lm_head_argmax: bf16 hidden states and weight only")
+    if hidden.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("lm_head_argmax: the hidden axis must be contiguous")
+    rows, h = hidden.shape
+    vocab = weight.shape[0]
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=hidden.device)
+    elif out.shape != (rows,) or out.dtype != torch.int64 or not out.is_contiguous():
+        raise ValueError("lm_head_argmax: out must be contiguous int64 [rows]")
+    nbytes = _lib.query("ls_lm_head_argmax_workspace", rows, vocab)
+    ws = _lib.WORKSPACE.get(hidden.device, nbytes, "lm_head")
+    _lib.call(
+        "ls_lm_head_argmax", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0),
+        _lib.dtype_code(hidden), rows, h, vocab, out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(hidden.device),
+    )
+    return out
+
+
 def greedy_verify(
     target_logits: torch.Tensor,
     draft_logits: torch.Tensor | None = None,

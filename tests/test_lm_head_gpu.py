@@ -1,0 +1,132 @@
+"""GPU parity of the fused vocabulary head + argmax (ls_lm_head_argmax).
+
+The logits are floating point, so parity is stated with a tolerance: the
+reference value is the float64 product of the bf16 inputs (every bf16 x bf16
+product is exact, so only the sum rounds), and fp32 accumulation in any order
+differs from it by at most (K/32 + 32) * 2^-24 * sum_k |a_k b_k| (the MFMA
+adds 32-term products into its fp32 accumulator K/32 times). The returned
+index must hold a logit within two such bounds of the row maximum, and must be
+the exact argmax whenever the top two logits are further apart than that.
+Ties between bit-identical columns must resolve to the lower index.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from loopspec_amd import verify
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def reference(hidden: torch.Tensor, weight: torch.Tensor):
+    a = hidden.double().cpu()
+    b = weight.double().cpu()
+    logits = a @ b.T
+    bound = (a.abs() @ b.abs().T) * ((a.shape[1] / 32 + 32) * 2.0 ** -24)
+    return logits.numpy(), bound.numpy()
+
+
+def check(got: np.ndarray, logits: np.ndarray, bound: np.ndarray) -> int:
+    """Return the number of rows decided exactly (gap above the bound)."""
+    exact = 0
+    for m in range(logits.shape[0]):
+        row, tol = logits[m], bound[m]
+        best = int(np.argmax(row))
+        i = int(got[m])
+        assert 0 <= i < row.shape[0], (m, i)
+        assert row[i] >= row[best] - (tol[i] + tol[best]), (m, i, best, row[i], row[best])
+        top2 = np.partition(row, -2)[-2:]
+        if top2[1] - top2[0] > 2 * tol.max():
+            assert i == best, (m, i, best)
+            exact += 1
+    return exact
+
+
+def make(rows, hidden_size, vocab, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    hidden = (torch.randn(rows, hidden_size, generator=g) * scale).to(torch.bfloat16)
+    weight = (torch.randn(vocab, hidden_size, generator=g) * (hidden_size ** -0.5)).to(torch.bfloat16)
+    return hidden, weight
+
+
+@pytest.mark.parametrize("rows,hidden_size,vocab", [
+    (320, 2048, 49152),   # C2's endpoint rows over the Ouro-1.4B head
+    (1, 64, 192),         # one row, one column block, one k-block
+    (7, 128, 1000),       # partial row tile, partial column block (1000 = 5 x 192 + 40)
+    (333, 256, 4096),     # two row blocks, the second of 13 rows
+    (700, 64, 2000),      # three row blocks
+])
+def test_lm_head_argmax_matches_float64(gpu, rows, hidden_size, vocab):
+    hidden, weight = make(rows, hidden_size, vocab, rows + vocab)
+    announce(f"lm_head_argmax M={rows} H={hidden_size} V={vocab}")
+    got = verify.lm_head_argmax(hidden.to(gpu), weight.to(gpu))
+    torch.cuda.synchronize()
+    logits, bound = reference(hidden, weight)
+    exact = check(got.cpu().numpy(), logits, bound)
+    assert exact >= rows // 2  # most rows are decided exactly, not only within tolerance
+
+
+def test_lm_head_argmax_ties_take_the_lower_index(gpu):
+    """Duplicate weight rows give bit-identical logits; the lower index wins,
+    also across column blocks and column waves."""
+    rows, hidden_size, vocab = 40, 128, 1000
+    hidden, weight = make(rows, hidden_size, vocab, 3, scale=1.0)
+    logits, _ = reference(hidden, weight)
+    best = np.argmax(logits, axis=1)
+    # copy every row's winning column to a later index (in another block when possible)
+    w = weight.clone()
+    targets = {}
+    for m in range(rows):
+        dst = (int(best[m]) + 193 + 7 * m) % vocab
+        if dst > best[m] and dst not in targets.values() and dst not in best:
+            w[dst] = weight[best[m]]
+            targets[m] = dst
+    announce("lm_head_argmax ties")
+    got = verify.lm_head_argmax(hidden.to(gpu), w.to(gpu)).cpu().numpy()
+    logits2, _ = reference(hidden, w)
+    for m, dst in targets.items():
+        if np.argmax(logits2[m]) == best[m]:
+            assert got[m] == best[m], (m, got[m], best[m], dst)
+    assert len(targets) > 10
+
+
+def test_lm_head_argmax_strided_hidden_and_out(gpu):
+    rows, hidden_size, vocab = 96, 256, 3000
+    hidden, weight = make(rows, hidden_size + 64, vocab, 9)
+    view = hidden.to(gpu)[:, :hidden_size]  # row stride hidden_size + 64
+    wv = weight.to(gpu)[:, :hidden_size].contiguous()
+    out = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+    announce("lm_head_argmax strided hidden")
+    verify.lm_head_argmax(view, wv, out=out)
+    torch.cuda.synchronize()
+    logits, bound = reference(hidden[:, :hidden_size], weight[:, :hidden_size])
+    check(out.cpu().numpy(), logits, bound)
+
+
+def test_lm_head_argmax_matches_unfused_path(gpu):
+    """Against the unfused device path (torch matmul, then argmax) on rows
+    whose top two logits are well separated."""
+    rows, hidden_size, vocab = 64, 2048, 49152
+    hidden, weight = make(rows, hidden_size, vocab, 5, scale=2.0)
+    h, w = hidden.to(gpu), weight.to(gpu)
+    announce("lm_head_argmax vs unfused")
+    got = verify.lm_head_argmax(h, w)
+    unfused = verify.argmax_rows((h.float() @ w.float().T).contiguous())
+    torch.cuda.synchronize()
+    logits, bound = reference(hidden, weight)
+    check(got.cpu().numpy(), logits, bound)
+    check(unfused.cpu().numpy(), logits, bound)
+
+
+def test_lm_head_argmax_rejects_bad_shapes(gpu):
+    h = torch.zeros(4, 100, dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(10, 100, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(Exception):
+        verify.lm_head_argmax(h, w)  # hidden_size not a multiple of 64
+    with pytest.raises(ValueError):
+        verify.lm_head_argmax(h.float()[:, :64], w[:, :64])
+    empty = verify.lm_head_argmax(torch.zeros(0, 64, dtype=torch.bfloat16, device=gpu),
+                                  torch.zeros(10, 64, dtype=torch.bfloat16, device=gpu))
+    assert empty.shape == (0,)
