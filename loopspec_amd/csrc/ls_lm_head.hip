@@ -140,31 +140,49 @@ __global__ __launch_bounds__(kLmLanes) void lm_head_kernel(const LmParams p) {
   // is an immediate offset)
   const int fr_a = (wm * kLmRowsPerWave + (lane & 15)) * kLmRowBytes;
   const int fr_b = (wn * kLmColsPerWave + (lane & 15)) * kLmRowBytes;
+  // One k-block: 2 k-steps x 5 pairs of row tiles. Each pair's fragments
+  // (and each k-step's column fragments) are read one pair ahead, before the
+  // current pair's MFMAs, so the LDS latency overlaps them; a scheduling fence
+  // after each pair keeps the compiler from hoisting every read (which would
+  // need some 50 more registers).
   auto compute = [&](const uint8_t* abuf, const uint8_t* bbuf) {
+    constexpr int kPairs = kLmMT / 2;
+    auto sw = [&](int ks) { return ((ks * 4 + (lane >> 4)) ^ (lane & 7)) << 4; };
+    auto read_a = [&](int ks, int mp, bf16x8 (&a)[2]) {
+      const uint8_t* const fa = abuf + fr_a + sw(ks);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int sw = ((ks * 4 + (lane >> 4)) ^ (lane & 7)) << 4;
-      const uint8_t* const fa = abuf + fr_a + sw;
-      const uint8_t* const fb = bbuf + fr_b + sw;
-      bf16x8 b[kLmNT];
+      for (int h = 0; h < 2; ++h)
+        a[h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fa + (mp + h) * 16 * kLmRowBytes));
+    };
+    auto read_b = [&](int ks, bf16x8 (&b)[kLmNT]) {
+      const uint8_t* const fb = bbuf + fr_b + sw(ks);
 #pragma unroll
       for (int nt = 0; nt < kLmNT; ++nt)
         b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fb + nt * 16 * kLmRowBytes));
-      // rows in pairs of tiles, each pair's fragments read just before its
-      // MFMAs (a scheduling fence keeps all the reads from being hoisted)
+    };
+    bf16x8 acur[2], anext[2], bcur[kLmNT], bnext[kLmNT];
+    read_b(0, bcur);
+    read_a(0, 0, acur);
 #pragma unroll
-      for (int mp = 0; mp < kLmMT; mp += 2) {
-        bf16x8 a[2];
+    for (int g = 0; g < 2 * kPairs; ++g) {
+      const int ks = g / kPairs, mp = 2 * (g % kPairs);
+      if (g + 1 < 2 * kPairs) {
+        const int ks1 = (g + 1) / kPairs, mp1 = 2 * ((g + 1) % kPairs);
+        if (ks1 != ks) read_b(ks1, bnext);
+        read_a(ks1, mp1, anext);
+      }
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          a[h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fa + (mp + h) * 16 * kLmRowBytes));
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int nt = 0; nt < kLmNT; ++nt)
+          acc[mp + h][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(acur[h], bcur[nt], acc[mp + h][nt], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      acur[0] = anext[0];
+      acur[1] = anext[1];
+      if (g + 1 == kPairs) {
 #pragma unroll
-          for (int nt = 0; nt < kLmNT; ++nt)
-            acc[mp + h][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h], b[nt], acc[mp + h][nt], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int nt = 0; nt < kLmNT; ++nt) bcur[nt] = bnext[nt];
       }
     }
   };
