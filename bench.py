@@ -550,8 +550,10 @@ def main() -> int:
     }[args.config]
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": data})
     # Traffic summaries are per launch unit: the greedy kernel (C2), or the
-    # kernels of one ls_spec_verify call together (C3, C4).
-    kernel_name = {"C2": "greedy_kernel", "C3": "spec_verify", "C4": "spec_verify"}.get(args.config)
+    # kernels of one ls_spec_verify (C3, C4) or ls_lm_head_argmax (C2H) call
+    # together.
+    kernel_name = {"C2": "greedy_kernel", "C3": "spec_verify", "C4": "spec_verify",
+                   "C2H": "lm_head_argmax"}.get(args.config)
     if kernel_name:
         result["roofline"]["traffic"] = traffic_from_profile(kernel_name, args.config)
     if args.copy_calibration:
