@@ -130,3 +130,21 @@ def test_lm_head_argmax_rejects_bad_shapes(gpu):
     empty = verify.lm_head_argmax(torch.zeros(0, 64, dtype=torch.bfloat16, device=gpu),
                                   torch.zeros(10, 64, dtype=torch.bfloat16, device=gpu))
     assert empty.shape == (0,)
+
+
+def test_lm_head_argmax_nan_columns_win_lowest_first(gpu):
+    """torch.argmax treats NaN as the maximum and returns the first one: a NaN
+    in weight rows 700 and 300 makes column 300 every row's answer; a NaN in
+    one hidden row makes that row's answer column 0."""
+    rows, hidden_size, vocab = 24, 128, 1000
+    hidden, weight = make(rows, hidden_size, vocab, 21)
+    w = weight.clone()
+    w[700, 5] = float("nan")
+    w[300, 64] = float("nan")
+    h = hidden.clone()
+    h[3, 10] = float("nan")
+    announce("lm_head_argmax NaN columns")
+    got = verify.lm_head_argmax(h.to(gpu), w.to(gpu)).cpu().numpy()
+    want = torch.argmax(h.float() @ w.float().T, dim=-1).numpy()
+    assert want[0] == 300 and want[3] == 0
+    assert np.array_equal(got, want)
