@@ -8,10 +8,12 @@ NSETS launches replayed K/NSETS times; the timed region is bracketed by HIP
 events on the stream the kernels run on, with device synchronisation on both
 sides. Prints one JSON line.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H|SLOTS]
 
 C2H is the vocabulary head fused with the greedy argmax (hidden states of C2's
-320 endpoint rows, Ouro-1.4B head: H=2048, V=49152, bf16 weight).
+320 endpoint rows, Ouro-1.4B head: H=2048, V=49152, bf16 weight). SLOTS is the
+GPU-resident decode-slot pool at C5's shape: per step, the 384 slots of the
+previous step are released and 384 rows allocate.
 """
 
 from __future__ import annotations
@@ -167,6 +169,70 @@ def bench_lm_head(steps: int, warmup: int, device: torch.device, nsets: int) -> 
         "unfused_ms_per_step": unfused_ms,
         "speedup_vs_unfused": unfused_ms / ms_per_step,
     }
+
+
+# ---------------------------------------------------------------------------
+# SLOTS: GPU-resident decode-slot pool
+# ---------------------------------------------------------------------------
+
+SLOTS_CAP, SLOTS_PRE, SLOTS_ROWS = 65536, 4096, 384
+
+
+def bench_slots(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    from loopspec_amd.loopspec.branching import DeviceSlotPool
+
+    pool = DeviceSlotPool(SLOTS_CAP, device)
+    pool.begin(SLOTS_PRE)
+    markers = torch.zeros(SLOTS_ROWS, dtype=torch.int64, device=device)
+    out = [torch.empty(SLOTS_ROWS, dtype=torch.int64, device=device) for _ in range(nsets)]
+    pool.allocate(markers, out[-1])
+
+    def step(i: int) -> None:
+        # the previous step's slots are released, then this step's rows allocate
+        pool.release(out[i - 1])
+        pool.allocate(markers, out[i])
+
+    ms_per_step, timed_steps, wsteps = _time_graph(step, nsets, steps, warmup)
+    if pool.errors():
+        raise RuntimeError(f"slot pool reported errors {pool.errors()}")
+    nbytes = SLOTS_ROWS * 8 * 5  # markers, ring reads, out; released ids, ring writes
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": "decode-slot bookkeeping steps/s (release 384 slots + allocate 384 rows)",
+        "value": 1.0 / (ms_per_step * 1e-3),
+        "unit": "steps/s",
+        "steps": timed_steps,
+        "warmup": wsteps,
+        "ms_per_step": ms_per_step,
+        "dtype": "int64",
+        "config": {"workload": "SLOTS-pool-cap65536-rows384", "capacity": SLOTS_CAP,
+                   "prompt_slots": SLOTS_PRE, "rows": SLOTS_ROWS,
+                   "kernel": "ls::pool_release_kernel + ls::pool_allocate_kernel",
+                   "submission": "hipGraph of one release + one allocate per step"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "note": "latency-bound: two single-workgroup launches per step"},
+    }
+
+
+def cpu_baseline_slots(max_seconds: float = 10.0) -> dict:
+    """The reference pool's bookkeeping (its CPU sequence, recycle list and live
+    set, restated in oracle/graph_ops.py) for the same steps, 1 thread."""
+    from oracle import graph_ops as og
+
+    pool = og.DecodeSlotPool(SLOTS_CAP)
+    pool.begin(SLOTS_PRE)
+    prev = pool.allocate(SLOTS_ROWS)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < max_seconds:
+        pool.release(prev)
+        prev = pool.allocate(SLOTS_ROWS)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"{n} steps of release 384 + allocate 384 in {dt:.1f}s (oracle DecodeSlotPool, the "
+                      "reference's CPU bookkeeping; the ring upload and graph replay are not included)",
+            "cpu_model": _cpu_model()}
 
 
 # ---------------------------------------------------------------------------
@@ -537,6 +603,8 @@ def main() -> int:
         args.no_cpu_baseline = True
     elif args.config == "C2H":
         result = bench_lm_head(args.steps, args.warmup, device, args.sets)
+    elif args.config == "SLOTS":
+        result = bench_slots(args.steps, args.warmup, device, args.sets)
     else:
         print(f"unknown config {args.config}", file=sys.stderr)
         return 2
@@ -547,6 +615,7 @@ def main() -> int:
               "U(256,4096) ids, drafts sampled from q, Philox uniforms)",
         "C5": "synthetic (C3 logits at B=128, drafts sampled from q; random bf16 KV pool, context U(512,8192))",
         "C2H": "synthetic (seeded N(0,1) bf16 hidden states, two N(0,1/H) bf16 head weights alternated)",
+        "SLOTS": "synthetic (every row valid; all 384 slots of the previous step released)",
     }[args.config]
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": data})
     # Traffic summaries are per launch unit: the greedy kernel (C2), or the
@@ -566,6 +635,8 @@ def main() -> int:
             result["cpu_baseline"]["c1"] = cpu_baseline_c1()
         elif args.config == "C2H":
             result["cpu_baseline"] = cpu_baseline_lm_head()
+        elif args.config == "SLOTS":
+            result["cpu_baseline"] = cpu_baseline_slots()
         else:
             result["cpu_baseline"] = cpu_baseline_spec(workloads.C3 if args.config == "C3" else workloads.C4)
     order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "ms_per_step_p10",

@@ -275,6 +275,35 @@ int ls_allocate_decode_slots(const int64_t* free_slots, int64_t capacity,
                              int64_t* allocation_cursor, const int64_t* valid_markers,
                              int64_t batch, int64_t* out_cache_locs, ls_stream_t stream);
 
+/* GPU-resident decode-slot pool: the ring of reusable KV slot IDs 1..capacity
+ * and its ownership live on the device, so allocation and release need no CPU
+ * mirror and no readback. state: int64 [3] = {allocation cursor (the scalar
+ * ls_allocate_decode_slots advances), end of the ID sequence, error bits};
+ * ring: int64 [capacity] (position q of the sequence at ring[q % capacity]);
+ * live: uint32 [ls_slot_pool_live_words(capacity)], one bit per ID.
+ * Error bits (read state[2] whenever convenient; nothing is rolled back):
+ * 1 = an allocate found fewer IDs than rows (it allocated nothing),
+ * 2 = an allocate took an ID that was still live, 4 = a release named an ID
+ * that was not live or out of range (that ID is skipped).
+ * Replaces: DecodeSlotPool.begin / allocate / release
+ *   (sglang_recurrent/loopspec/branching/decode_slots.py:50-74, 113-151, 153-166),
+ *   whose CPU sequence, recycle list and live set this keeps on the device,
+ *   and the ring refills of _append_to_ring (decode_slots.py:88-111). */
+int64_t ls_slot_pool_live_words(int64_t capacity);
+/* IDs 1..allocated_slots are taken by the prompt (never decode-owned); the
+ * ring is rewritten to 1..capacity, the live set and errors cleared. */
+int ls_slot_pool_begin(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
+                       int64_t allocated_slots, ls_stream_t stream);
+/* Rows with valid_markers[b] >= 0 take the next IDs in batch order (as
+ * ls_allocate_decode_slots), which become live; skipped rows keep their output. */
+int ls_slot_pool_allocate(const int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
+                          const int64_t* valid_markers, int64_t batch, int64_t* out_cache_locs,
+                          ls_stream_t stream);
+/* slots[0..count) (int64, in order) stop being live and rejoin the sequence
+ * after every ID not yet consumed. */
+int ls_slot_pool_release(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
+                         const int64_t* slots, int64_t count, ls_stream_t stream);
+
 /* mapping: int32 [request_capacity, mapping_stride] (first max_context_len
  * columns used). For each row b: copy_lens[b] > 0 copies
  * mapping[source_rows[b], :copy_len] to mapping[request_rows[b], :copy_len];

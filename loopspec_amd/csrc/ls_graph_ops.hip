@@ -11,6 +11,9 @@
 //                          free-page ring) and destination slots
 //  kv_commit_copy          16-byte copies of every plane's token row, branch
 //                          slot -> main-timeline slot
+//  slot pool               GPU-resident DecodeSlotPool (branching/decode_slots.py):
+//                          begin / allocate / release on the device ring with a
+//                          live bitmap and error bits, no CPU mirror
 // All integer work is exact; every kernel bounds-checks slot and page ids and
 // skips (and reports) entries that fall outside the tables it was given.
 #include "ls_common.hpp"
@@ -194,6 +197,103 @@ __global__ __launch_bounds__(kCopyBlock) void kv_copy_kernel(char* __restrict__ 
   }
 }
 
+// GPU-resident decode-slot pool (sglang_recurrent/loopspec/branching/decode_slots.py:13-166).
+// State st[3] (int64): st[0] the allocation cursor (absolute consumed count,
+// the same scalar allocate_decode_slots advances), st[1] the absolute end of
+// the ID sequence, st[2] error bits. The ring holds sequence position q at
+// ring[q % capacity]. A released ID is appended at the end of the sequence at
+// once, in release order; the reference appends its recycled IDs only when the
+// unconsumed part runs short (decode_slots.py:122-142), but appends them at
+// the same place (after the unconsumed IDs, in release order), so both consume
+// IDs in the same order. live: one bit per ID 1..capacity.
+constexpr int64_t kPoolErrExhausted = 1;  // allocate: fewer IDs than rows (nothing allocated)
+constexpr int64_t kPoolErrLive = 2;       // allocate: a ring entry was still live
+constexpr int64_t kPoolErrUnowned = 4;    // release: an ID that was not live (or out of range); skipped
+
+__global__ __launch_bounds__(kCopyBlock) void pool_begin_kernel(int64_t* __restrict__ ring, int64_t capacity,
+                                                                int64_t* __restrict__ st, uint32_t* __restrict__ live,
+                                                                int64_t words, int64_t allocated) {
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kCopyBlock + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCopyBlock;
+  for (int64_t i = i0; i < capacity; i += stride) ring[i] = i + 1;
+  for (int64_t i = i0; i < words; i += stride) live[i] = 0u;
+  if (i0 == 0) {
+    st[0] = allocated;
+    st[1] = capacity;
+    st[2] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kScanBlock) void pool_allocate_kernel(const int64_t* __restrict__ ring, int64_t capacity,
+                                                                   int64_t* st, uint32_t* live,
+                                                                   const int64_t* __restrict__ markers, int64_t batch,
+                                                                   int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t cursor = st[0], end = st[1];
+  int64_t count = 0;
+  for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
+    const int64_t b = b0 + threadIdx.x;
+    uint32_t total;
+    (void)block_excl_scan_u32(b < batch && markers[b] >= 0 ? 1u : 0u, red, &total);
+    count += total;
+  }
+  if (cursor + count > end) {  // uniform: every lane formed the same count
+    if (threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrExhausted);
+    return;
+  }
+  int64_t carry = 0;
+  bool bad = false;
+  for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
+    const int64_t b = b0 + threadIdx.x;
+    const bool valid = b < batch && markers[b] >= 0;
+    uint32_t total;
+    const uint32_t rank = block_excl_scan_u32(valid ? 1u : 0u, red, &total);
+    if (valid) {
+      const int64_t slot = ring[(cursor + carry + rank) % capacity];
+      out[b] = slot;
+      if (slot >= 1 && slot <= capacity) {
+        const uint32_t bit = 1u << (slot & 31);
+        bad = bad || (atomicOr(live + (slot >> 5), bit) & bit) != 0u;
+      } else {
+        bad = true;
+      }
+    }
+    carry += total;
+  }
+  if (bad) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrLive);
+  __syncthreads();  // every lane has read st[0]
+  if (threadIdx.x == 0) st[0] = cursor + count;
+}
+
+__global__ __launch_bounds__(kScanBlock) void pool_release_kernel(int64_t* __restrict__ ring, int64_t capacity,
+                                                                  int64_t* st, uint32_t* live,
+                                                                  const int64_t* __restrict__ slots, int64_t n) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t end = st[1];
+  int64_t carry = 0;
+  bool bad = false;
+  for (int64_t i0 = 0; i0 < n; i0 += kScanBlock) {
+    const int64_t i = i0 + threadIdx.x;
+    bool ok = false;
+    int64_t slot = 0;
+    if (i < n) {
+      slot = slots[i];
+      if (slot >= 1 && slot <= capacity) {
+        const uint32_t bit = 1u << (slot & 31);
+        ok = (atomicAnd(live + (slot >> 5), ~bit) & bit) != 0u;
+      }
+      bad = bad || !ok;
+    }
+    uint32_t total;
+    const uint32_t rank = block_excl_scan_u32(ok ? 1u : 0u, red, &total);
+    if (ok) ring[(end + carry + rank) % capacity] = slot;
+    carry += total;
+  }
+  if (bad) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrUnowned);
+  __syncthreads();  // every lane has read st[1]
+  if (threadIdx.x == 0) st[1] = end + carry;
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -284,6 +384,43 @@ int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t t
                      dim3(kCopyBlock), 0, st, static_cast<char*>(kv), planes, plane_stride_bytes, token_bytes,
                      num_pages * page_size, branch_slots, dst_slots, ppw);
   return check_launch("kv_commit copy launch");
+}
+
+int64_t ls_slot_pool_live_words(int64_t capacity) { return capacity > 0 ? capacity / 32 + 1 : 0; }
+
+int ls_slot_pool_begin(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live, int64_t allocated_slots,
+                       ls_stream_t stream) {
+  if (capacity <= 0 || allocated_slots < 0 || allocated_slots > capacity)
+    return fail(LS_ERR_VALUE, "slot_pool_begin: need capacity > 0 and 0 <= allocated_slots <= capacity");
+  if (!ring || !state || !live) return fail(LS_ERR_VALUE, "slot_pool_begin: NULL pointer");
+  const int64_t words = ls_slot_pool_live_words(capacity);
+  const int64_t work = capacity > words ? capacity : words;
+  int64_t blocks = (work + kCopyBlock - 1) / kCopyBlock;
+  blocks = blocks < 1024 ? blocks : 1024;
+  hipLaunchKernelGGL(pool_begin_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kCopyBlock), 0,
+                     static_cast<hipStream_t>(stream), ring, capacity, state, live, words, allocated_slots);
+  return check_launch("slot_pool_begin launch");
+}
+
+int ls_slot_pool_allocate(const int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
+                          const int64_t* valid_markers, int64_t batch, int64_t* out_cache_locs, ls_stream_t stream) {
+  if (capacity <= 0 || batch < 0) return fail(LS_ERR_VALUE, "slot_pool_allocate: invalid capacity or batch");
+  if (batch == 0) return LS_OK;
+  if (!ring || !state || !live || !valid_markers || !out_cache_locs)
+    return fail(LS_ERR_VALUE, "slot_pool_allocate: NULL pointer");
+  hipLaunchKernelGGL(pool_allocate_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
+                     capacity, state, live, valid_markers, batch, out_cache_locs);
+  return check_launch("slot_pool_allocate launch");
+}
+
+int ls_slot_pool_release(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live, const int64_t* slots,
+                         int64_t count, ls_stream_t stream) {
+  if (capacity <= 0 || count < 0) return fail(LS_ERR_VALUE, "slot_pool_release: invalid capacity or count");
+  if (count == 0) return LS_OK;
+  if (!ring || !state || !live || !slots) return fail(LS_ERR_VALUE, "slot_pool_release: NULL pointer");
+  hipLaunchKernelGGL(pool_release_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
+                     capacity, state, live, slots, count);
+  return check_launch("slot_pool_release launch");
 }
 
 }  // extern "C"

@@ -106,3 +106,61 @@ def kv_commit_copy(kv: np.ndarray, branch_slots, dst_slots):
             if ds[b, j] >= 0:
                 kv[:, ds[b, j]] = kv[:, bs[b, j]]
     return kv
+
+
+class DecodeSlotPool:
+    """CPU restatement of DecodeSlotPool's ID bookkeeping
+    (sglang_recurrent/loopspec/branching/decode_slots.py:13-166): the ID
+    sequence, its lazy refill with recycled IDs and the live set. The device
+    ring is modelled by `ring` (what _append_to_ring writes, decode_slots.py:88-111).
+    allocate/release raise RuntimeError where the reference does.
+    """
+
+    def __init__(self, capacity: int) -> None:
+        self.capacity = capacity
+        self.ring = list(range(1, capacity + 1))
+
+    def begin(self, allocated_slots: int) -> None:
+        # decode_slots.py:50-74
+        if not 0 <= allocated_slots <= self.capacity:
+            raise ValueError("invalid graph decode KV allocation offset")
+        self.ring = list(range(1, self.capacity + 1))
+        self.next = allocated_slots
+        self.ring_head = allocated_slots % self.capacity
+        self.cursor = allocated_slots
+        self.sequence = list(range(1, self.capacity + 1))
+        self.recycled: list[int] = []
+        self.live: set[int] = set()
+
+    def allocate(self, count: int) -> list[int]:
+        # decode_slots.py:113-151
+        end = self.next + count
+        if end > len(self.sequence):
+            remaining = self.sequence[self.next:]
+            sequence = remaining + self.recycled
+            if count > len(sequence):
+                raise RuntimeError("recurrent decode ran out of KV cache slots")
+            start = (self.ring_head + len(remaining)) % self.capacity
+            for i, s in enumerate(self.recycled):
+                self.ring[(start + i) % self.capacity] = s
+            self.sequence = sequence
+            self.recycled = []
+            self.next = 0
+            end = count
+        slots = self.sequence[self.next:end]
+        if any(s in self.live for s in slots):
+            raise RuntimeError("recurrent decode allocated a live KV slot")
+        self.live.update(slots)
+        self.next = end
+        self.ring_head = (self.ring_head + count) % self.capacity
+        self.cursor += count
+        return slots
+
+    def release(self, slots) -> None:
+        # decode_slots.py:153-166
+        for s in slots:
+            s = int(s)
+            if s not in self.live:
+                raise RuntimeError("recurrent decode released an unowned KV slot")
+            self.live.remove(s)
+            self.recycled.append(s)

@@ -7,6 +7,7 @@ import torch
 
 from oracle import graph_ops as og
 from loopspec_amd.loopspec import graph_ops as go
+from loopspec_amd.loopspec.branching.decode_slots import ERR_EXHAUSTED, ERR_UNOWNED, DeviceSlotPool
 from tests.conftest import announce
 
 pytestmark = pytest.mark.gpu
@@ -165,3 +166,100 @@ def test_kv_commit_reports_overflow(gpu):
     dst = go.commit_kv(None, acc, branch, pt, ctx, ring, cur, 2, status=status)
     assert status.item() == 1
     assert dst.cpu().tolist() == [[-1, -1]]
+
+
+def _pool_ops(seed, cap, pre, steps, batch):
+    """A seeded sequence of ('alloc', markers) / ('release', ids) operations,
+    with the oracle pool's expected allocations (None where it raises)."""
+    rng = np.random.default_rng(seed)
+    pool = og.DecodeSlotPool(cap)
+    pool.begin(pre)
+    live, ops = [], []
+    for _ in range(steps):
+        if live and rng.random() < 0.4:
+            k = int(rng.integers(1, min(len(live), 3 * batch) + 1))
+            ids = [live.pop(int(rng.integers(len(live)))) for _ in range(k)]
+            pool.release(ids)
+            ops.append(("release", np.array(ids, dtype=np.int64), None))
+        else:
+            markers = np.where(rng.random(batch) < 0.8, rng.integers(0, 99, batch), -1).astype(np.int64)
+            n = int((markers >= 0).sum())
+            try:
+                got = pool.allocate(n)
+            except RuntimeError:
+                ops.append(("alloc", markers, None))
+                break
+            live.extend(got)
+            ops.append(("alloc", markers, got))
+    return ops
+
+
+@pytest.mark.parametrize("cap,pre,batch", [(64, 0, 8), (1000, 37, 64), (5000, 4000, 300), (3000, 0, 1500)])
+def test_device_slot_pool_matches_reference_pool(gpu, cap, pre, batch):
+    ops = _pool_ops(cap + batch, cap, pre, 60, batch)
+    pool = DeviceSlotPool(cap, gpu)
+    pool.begin(pre)
+    announce(f"device slot pool cap={cap} pre={pre} B={batch}")
+    for kind, arr, want in ops:
+        if kind == "release":
+            pool.release(torch.from_numpy(arr).to(gpu))
+            continue
+        out = torch.full((batch,), -5, dtype=torch.int64, device=gpu)
+        pool.allocate(torch.from_numpy(arr).to(gpu), out)
+        got = out.cpu().numpy()
+        if want is None:
+            assert pool.errors() & ERR_EXHAUSTED
+            assert (got == -5).all()  # nothing allocated
+            break
+        assert pool.errors() == 0
+        assert got[arr >= 0].tolist() == want
+        assert (got[arr < 0] == -5).all()
+
+
+def test_device_slot_pool_reports_bad_releases(gpu):
+    pool = DeviceSlotPool(32, gpu)
+    pool.begin(4)
+    out = torch.empty(3, dtype=torch.int64, device=gpu)
+    pool.allocate(torch.zeros(3, dtype=torch.int64, device=gpu), out)
+    assert out.cpu().tolist() == [5, 6, 7]
+    pool.release(torch.tensor([6, 2, 99], dtype=torch.int64, device=gpu))  # 2: prompt slot, 99: out of range
+    assert pool.errors() == ERR_UNOWNED
+    with pytest.raises(RuntimeError, match="unowned"):
+        pool.check()
+    # 6 was released and rejoins after the unconsumed 8..32
+    out = torch.empty(26, dtype=torch.int64, device=gpu)
+    pool.allocate(torch.zeros(26, dtype=torch.int64, device=gpu), out)
+    assert out.cpu().tolist() == list(range(8, 33)) + [6]
+
+
+def test_device_slot_pool_in_graph_replays(gpu):
+    """allocate + release captured once and replayed: each replay continues
+    the same sequence the reference pool gives for the repeated operations."""
+    cap, batch = 256, 16
+    pool = DeviceSlotPool(cap, gpu)
+    pool.begin(10)
+    markers = torch.zeros(batch, dtype=torch.int64, device=gpu)
+    out = torch.empty(batch, dtype=torch.int64, device=gpu)
+    ref = og.DecodeSlotPool(cap)
+    ref.begin(10)
+    # warm: first allocation eagerly, so the captured release frees real IDs
+    pool.allocate(markers, out)
+    first = ref.allocate(batch)
+    assert out.cpu().tolist() == first
+    held = out.clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("device slot pool graph capture")
+    with torch.cuda.graph(g):
+        pool.release(held)
+        pool.allocate(markers, out)
+        held.copy_(out)
+    prev = first
+    for rep in range(5):
+        g.replay()
+        torch.cuda.synchronize()
+        ref.release(prev)
+        want = ref.allocate(batch)
+        assert out.cpu().tolist() == want, rep
+        prev = want
+    assert pool.errors() == 0

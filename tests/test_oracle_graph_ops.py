@@ -128,3 +128,55 @@ def test_kv_commit_copy_moves_accepted_rows_only():
     mask = np.ones(40, bool)
     mask[[4, 5, 9]] = False
     assert (out[:, mask] == kv[:, mask]).all()
+
+
+def test_decode_slot_pool_closed_forms():
+    """begin(a) leaves IDs a+1..capacity in order; released IDs come back in
+    release order once those run out; over-allocation and unowned or repeated
+    releases raise (decode_slots.py:113-166)."""
+    pool = og.DecodeSlotPool(10)
+    pool.begin(3)
+    assert pool.allocate(4) == [4, 5, 6, 7]
+    pool.release([6, 4])
+    assert pool.allocate(3) == [8, 9, 10]
+    assert pool.allocate(2) == [6, 4]
+    with pytest.raises(RuntimeError):
+        pool.allocate(1)
+    with pytest.raises(RuntimeError):
+        pool.release([2])  # a prompt slot is never decode-owned
+    pool.release([9])
+    with pytest.raises(RuntimeError):
+        pool.release([9])
+    assert pool.allocate(1) == [9]
+
+
+def test_decode_slot_pool_is_a_fifo_of_free_ids():
+    """Against an independent model: a FIFO queue of free IDs (prompt-free IDs
+    in order, then releases appended). The lazy refill must give the same
+    allocation order, never hand out a live ID, and conserve the IDs."""
+    import collections
+
+    rng = np.random.default_rng(4)
+    for cap, pre in ((16, 0), (64, 7), (200, 199)):
+        pool = og.DecodeSlotPool(cap)
+        pool.begin(pre)
+        fifo = collections.deque(range(pre + 1, cap + 1))
+        live = []
+        for _ in range(300):
+            if live and rng.random() < 0.45:
+                k = int(rng.integers(1, len(live) + 1))
+                pick = [live.pop(int(rng.integers(len(live)))) for _ in range(k)]
+                pool.release(pick)
+                fifo.extend(pick)
+            else:
+                n = int(rng.integers(0, 6))
+                if n > len(fifo):
+                    with pytest.raises(RuntimeError):
+                        pool.allocate(n)
+                    continue
+                got = pool.allocate(n)
+                want = [fifo.popleft() for _ in range(n)]
+                assert got == want
+                assert not set(got) & set(live)
+                live.extend(got)
+            assert sorted(live + list(fifo)) == list(range(pre + 1, cap + 1))
