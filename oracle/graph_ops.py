@@ -2,7 +2,9 @@
 
 Pinned by: exhaustive small cases and closed forms in tests/test_oracle_graph_ops.py
 (every valid/skip pattern up to B=10, ring wrap-around, copy-length signs,
-gather/scatter with skips, paged commit against a page-walk restatement).
+gather/scatter with skips, paged commit against a page-walk restatement; the
+DecodeSlotPool restatement against closed forms and an independent FIFO model
+of the free IDs over seeded allocate/release sequences).
 """
 
 from __future__ import annotations
