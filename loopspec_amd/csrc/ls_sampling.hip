@@ -936,7 +936,7 @@ __device__ __forceinline__ bool bound_repair(RowSh& sh, int set, const char* row
 // slots hold every element of p >= the row's cutoff and their select is exact.
 // Returns false (slots partly rewritten) if some chunk does not fit. Out of
 // line, like slow_select.
-template <int DT>
+template <int DT, int OCC>
 __device__ __noinline__ bool rebuild_chunks(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c,
                                                float pen, float inv_pen, int vocab, int nch, int cap, float cut) {
   constexpr int kQ = kChunk / kRB;
@@ -1027,7 +1027,7 @@ constexpr int kRebuilt = -3;      // the rebuilt slots' cutoff
 constexpr int kNeedRebuild = -4;  // the candidates hold top_p but a non-candidate reaches their cutoff
 enum SlowMode : int { kSlowCand = 0, kSlowRebuilt = 1, kSlowRow = 2 };
 
-template <int DT>
+template <int DT, int OCC>
 __device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
                                         float inv_pen, int vocab, int nch, int nslots, uint64_t thr, bool keep,
                                         int mode) {
@@ -1142,7 +1142,7 @@ __device__ __forceinline__ bool slot_valid(const RowSh& sh, int set, const SampP
 // digit). Outputs the row statistics, the filtered probability of each row's
 // draft token (-1 if the row has none) and, for a row that took the slow path
 // with keep_support, the size of its support.
-template <int DT, int NS, typename AfterR0>
+template <int DT, int NS, int OCC, typename AfterR0>
 __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)[NS], bool keep_support,
                               RowStat (&st)[NS], float (&P_tok)[NS], int (&n_sup)[NS], AfterR0 after_r0) {
   const int t = threadIdx.x, wid = t / kWave;
@@ -1229,13 +1229,13 @@ __device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)
         const int64_t g = r[s] / p.rpg;
         const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
         const char* rowp = row_of(p, g, static_cast<int>(r[s] - g * p.rpg));
-        int n = slow_select<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
+        int n = slow_select<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
                                 kSlowCand);
         if (n == kNeedRebuild) {
           // the deficient chunks' candidates become {p >= the candidates' cutoff}
-          const bool fits = rebuild_chunks<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, p.cap,
+          const bool fits = rebuild_chunks<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, p.cap,
                                                sh.slow_cut[s]);
-          n = slow_select<DT>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
+          n = slow_select<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
                               fits ? kSlowRebuilt : kSlowRow);
         }
         st[s].cutoff = sh.slow_cut[s];
@@ -1312,8 +1312,12 @@ __device__ void publish_draw(const SampParams& p, RowSh& sh, int64_t g, int i, u
 // of draft token x_i (u < min(1, P/Q), sampler.py:451-452) and the residual
 // draw normalize(max(P - Q, 0)) (fallback normalize(P), rejection.py:60-69)
 // with u[g, k+i]. i == k: the bonus row's draw with u[g, 2k].
-template <int DT>
-__global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
+// OCC = 4: built for two workgroups per CU (at most 128 registers, the
+// out-of-line slow path in its own copies), launched when the workgroups
+// outnumber the CUs; OCC = 0 otherwise (no spills).
+template <int DT, int OCC>
+__global__ __launch_bounds__(kRB) __attribute__((amdgpu_waves_per_eu(OCC > 0 ? OCC : 1)))
+void spec_row_kernel(const SampParams p) {
   __shared__ RowSh sh;
   const int k = p.k, rpg = 2 * k + 1;
   const int64_t g = blockIdx.x / (k + 1);
@@ -1355,7 +1359,7 @@ __global__ __launch_bounds__(kRB) void spec_row_kernel(const SampParams p) {
   int n_sup[2];
   // keep_support: a row whose cutoff needed the whole-row select keeps its
   // support (if it fits the slots) in index order, so its draw stays on slots
-  finalize_rows<DT, 2>(p, sh, r, true, st, P_tok, n_sup, gather);
+  finalize_rows<DT, 2, OCC>(p, sh, r, true, st, P_tok, n_sup, gather);
   // target slots: the candidates, or the kept support of a slow row
   const int nt = (st[0].flags & kFlagSlow) ? n_sup[0] : nslots;
   if (bonus) {
@@ -1474,7 +1478,7 @@ __global__ __launch_bounds__(kRB) void row_kernel(const SampParams p) {
   RowStat st[1];
   float P_tok[1];
   int n_sup[1];
-  finalize_rows<DT, 1>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [](uint32_t) {});
+  finalize_rows<DT, 1, 0>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [](uint32_t) {});
   if constexpr (MODE == kModeSample) {
     const uint32_t* bm = p.use_pen ? p.bitmap + r[0] * p.bm_words : nullptr;
     const int64_t token = own_draw<DT>(p, sh, 0, st[0], (st[0].flags & kFlagSlow) ? n_sup[0] : p.nch * p.cap,
@@ -1585,7 +1589,12 @@ void launch_dt(const SampParams& p, int64_t groups, int64_t rows, hipStream_t st
     hipLaunchKernelGGL((chunk_kernel<DT, false>), grid, dim3(kWave), 0, st, p);
   }
   if constexpr (MODE == kModeSpec) {
-    hipLaunchKernelGGL((spec_row_kernel<DT>), dim3(static_cast<unsigned>(groups * (p.k + 1))), dim3(kRB), 0, st, p);
+    const int64_t wgs_row = groups * (p.k + 1);
+    if (wgs_row > static_cast<int64_t>(device_cu_count())) {
+      hipLaunchKernelGGL((spec_row_kernel<DT, 4>), dim3(static_cast<unsigned>(wgs_row)), dim3(kRB), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((spec_row_kernel<DT, 0>), dim3(static_cast<unsigned>(wgs_row)), dim3(kRB), 0, st, p);
+    }
   } else {
     hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kRB), 0, st, p);
   }

@@ -361,3 +361,23 @@ def test_spec_verify_empty_batch(gpu):
                                          torch.zeros(0, 5, device=gpu), 1.0, 0.7)
     torch.cuda.synchronize()
     assert acc.shape == (0,) and tok.shape == (0, 3)
+
+
+def test_spec_verify_more_workgroups_than_cus(gpu):
+    """B=100, k=3: 400 row workgroups, more than the CUs, so the build for two
+    workgroups per CU runs; rows taking the repair, rebuild and slow paths are
+    planted so its out-of-line slow path runs too."""
+    rows = candidates.repair_rows()
+    v = rows["repair"].shape[0]
+    cfg = workloads.SamplingConfig("many", 100, 3, v, torch.float32, 1.0, 0.9)
+    inp = workloads.sampling_inputs(cfg, 23)
+    kinds = ["repair", "slow", "rebuild"]
+    for b in range(0, 100, 7):
+        inp["target"][b, b % 4] = torch.from_numpy(rows[kinds[b % 3]])
+        inp["draft"][b, b % 3] = torch.from_numpy(rows[kinds[(b + 1) % 3]])
+    drafts = draft_tokens_from(inp, cfg)
+    announce("spec verify 400 row workgroups")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    want = oracle_spec(cfg, inp, drafts)
+    assert np.array_equal(acc, want.accept_len)
+    assert np.array_equal(tok, want.tokens)
