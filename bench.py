@@ -188,9 +188,9 @@ def bench_slots(steps: int, warmup: int, device: torch.device, nsets: int) -> di
     pool.allocate(markers, out[-1])
 
     def step(i: int) -> None:
-        # the previous step's slots are released, then this step's rows allocate
-        pool.release(out[i - 1])
-        pool.allocate(markers, out[i])
+        # the previous step's slots are released, then this step's rows
+        # allocate (one launch)
+        pool.step(out[i - 1], markers, out[i])
 
     ms_per_step, timed_steps, wsteps = _time_graph(step, nsets, steps, warmup)
     if pool.errors():
@@ -207,11 +207,11 @@ def bench_slots(steps: int, warmup: int, device: torch.device, nsets: int) -> di
         "dtype": "int64",
         "config": {"workload": "SLOTS-pool-cap65536-rows384", "capacity": SLOTS_CAP,
                    "prompt_slots": SLOTS_PRE, "rows": SLOTS_ROWS,
-                   "kernel": "ls::pool_release_kernel + ls::pool_allocate_kernel",
-                   "submission": "hipGraph of one release + one allocate per step"},
+                   "kernel": "ls::pool_step_kernel (release, then allocate)",
+                   "submission": "hipGraph of one launch per step"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "note": "latency-bound: two single-workgroup launches per step"},
+                     "note": "latency-bound: one single-workgroup launch per step"},
     }
 
 

@@ -304,6 +304,11 @@ int ls_slot_pool_allocate(const int64_t* ring, int64_t capacity, int64_t* state,
 int ls_slot_pool_release(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
                          const int64_t* slots, int64_t count, ls_stream_t stream);
 
+/* ls_slot_pool_release then ls_slot_pool_allocate, in one launch. */
+int ls_slot_pool_step(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live,
+                      const int64_t* slots, int64_t count, const int64_t* valid_markers,
+                      int64_t batch, int64_t* out_cache_locs, ls_stream_t stream);
+
 /* mapping: int32 [request_capacity, mapping_stride] (first max_context_len
  * columns used). For each row b: copy_lens[b] > 0 copies
  * mapping[source_rows[b], :copy_len] to mapping[request_rows[b], :copy_len];

@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ls_slot_pool_begin": (_I32, [_P, _I64, _P, _P, _I64, _P]),
     "ls_slot_pool_allocate": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _P]),
     "ls_slot_pool_release": (_I32, [_P, _I64, _P, _P, _P, _I64, _P]),
+    "ls_slot_pool_step": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P]),
     "ls_spec_verify": (
         _I32,
         [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I32, _I64, _I64, _I64, _F32, _F32, _I64, _F32,

@@ -224,12 +224,12 @@ __global__ __launch_bounds__(kCopyBlock) void pool_begin_kernel(int64_t* __restr
   }
 }
 
-__global__ __launch_bounds__(kScanBlock) void pool_allocate_kernel(const int64_t* __restrict__ ring, int64_t capacity,
-                                                                   int64_t* st, uint32_t* live,
-                                                                   const int64_t* __restrict__ markers, int64_t batch,
-                                                                   int64_t* __restrict__ out) {
-  __shared__ uint32_t red[kScanBlock / kWave];
-  const int64_t cursor = st[0], end = st[1];
+// Allocation body (every lane of one 1024-lane workgroup): the valid rows
+// take ring[(cursor + rank) % capacity] if cursor + count <= end (else
+// nothing, and false); *bad collects live-ID hits. Returns the new cursor.
+__device__ bool pool_allocate_body(const int64_t* __restrict__ ring, int64_t capacity, uint32_t* live,
+                                   const int64_t* __restrict__ markers, int64_t batch, int64_t* __restrict__ out,
+                                   int64_t cursor, int64_t end, uint32_t* red, bool* bad, int64_t* new_cursor) {
   int64_t count = 0;
   for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
     const int64_t b = b0 + threadIdx.x;
@@ -237,12 +237,8 @@ __global__ __launch_bounds__(kScanBlock) void pool_allocate_kernel(const int64_t
     (void)block_excl_scan_u32(b < batch && markers[b] >= 0 ? 1u : 0u, red, &total);
     count += total;
   }
-  if (cursor + count > end) {  // uniform: every lane formed the same count
-    if (threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrExhausted);
-    return;
-  }
+  if (cursor + count > end) return false;  // uniform: every lane formed the same count
   int64_t carry = 0;
-  bool bad = false;
   for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
     const int64_t b = b0 + threadIdx.x;
     const bool valid = b < batch && markers[b] >= 0;
@@ -253,25 +249,24 @@ __global__ __launch_bounds__(kScanBlock) void pool_allocate_kernel(const int64_t
       out[b] = slot;
       if (slot >= 1 && slot <= capacity) {
         const uint32_t bit = 1u << (slot & 31);
-        bad = bad || (atomicOr(live + (slot >> 5), bit) & bit) != 0u;
+        *bad = *bad || (atomicOr(live + (slot >> 5), bit) & bit) != 0u;
       } else {
-        bad = true;
+        *bad = true;
       }
     }
     carry += total;
   }
-  if (bad) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrLive);
-  __syncthreads();  // every lane has read st[0]
-  if (threadIdx.x == 0) st[0] = cursor + count;
+  *new_cursor = cursor + count;
+  return true;
 }
 
-__global__ __launch_bounds__(kScanBlock) void pool_release_kernel(int64_t* __restrict__ ring, int64_t capacity,
-                                                                  int64_t* st, uint32_t* live,
-                                                                  const int64_t* __restrict__ slots, int64_t n) {
-  __shared__ uint32_t red[kScanBlock / kWave];
-  const int64_t end = st[1];
+// Release body (every lane of one workgroup): live IDs of slots[0..n) are
+// cleared and appended at ring[(end + rank) % capacity] in order; *bad
+// collects IDs that were not live. Returns the new end.
+__device__ int64_t pool_release_body(int64_t* __restrict__ ring, int64_t capacity, uint32_t* live,
+                                     const int64_t* __restrict__ slots, int64_t n, int64_t end, uint32_t* red,
+                                     bool* bad) {
   int64_t carry = 0;
-  bool bad = false;
   for (int64_t i0 = 0; i0 < n; i0 += kScanBlock) {
     const int64_t i = i0 + threadIdx.x;
     bool ok = false;
@@ -282,16 +277,65 @@ __global__ __launch_bounds__(kScanBlock) void pool_release_kernel(int64_t* __res
         const uint32_t bit = 1u << (slot & 31);
         ok = (atomicAnd(live + (slot >> 5), ~bit) & bit) != 0u;
       }
-      bad = bad || !ok;
+      *bad = *bad || !ok;
     }
     uint32_t total;
     const uint32_t rank = block_excl_scan_u32(ok ? 1u : 0u, red, &total);
     if (ok) ring[(end + carry + rank) % capacity] = slot;
     carry += total;
   }
+  return end + carry;
+}
+
+__global__ __launch_bounds__(kScanBlock) void pool_allocate_kernel(const int64_t* __restrict__ ring, int64_t capacity,
+                                                                   int64_t* st, uint32_t* live,
+                                                                   const int64_t* __restrict__ markers, int64_t batch,
+                                                                   int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t cursor = st[0], end = st[1];
+  bool bad = false;
+  int64_t nc = cursor;
+  const bool fit = pool_allocate_body(ring, capacity, live, markers, batch, out, cursor, end, red, &bad, &nc);
+  if (!fit && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrExhausted);
+  if (bad) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrLive);
+  __syncthreads();  // every lane has read st[0]
+  if (fit && threadIdx.x == 0) st[0] = nc;
+}
+
+__global__ __launch_bounds__(kScanBlock) void pool_release_kernel(int64_t* __restrict__ ring, int64_t capacity,
+                                                                  int64_t* st, uint32_t* live,
+                                                                  const int64_t* __restrict__ slots, int64_t n) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t end = st[1];
+  bool bad = false;
+  const int64_t ne = pool_release_body(ring, capacity, live, slots, n, end, red, &bad);
   if (bad) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrUnowned);
   __syncthreads();  // every lane has read st[1]
-  if (threadIdx.x == 0) st[1] = end + carry;
+  if (threadIdx.x == 0) st[1] = ne;
+}
+
+// Release then allocate in one launch (the order of a decode step: pruned
+// timelines give their IDs back before the next rows take theirs).
+__global__ __launch_bounds__(kScanBlock) void pool_step_kernel(int64_t* __restrict__ ring, int64_t capacity,
+                                                               int64_t* st, uint32_t* live,
+                                                               const int64_t* __restrict__ slots, int64_t n,
+                                                               const int64_t* __restrict__ markers, int64_t batch,
+                                                               int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  const int64_t cursor = st[0], end = st[1];
+  bool bad_rel = false, bad_live = false;
+  const int64_t ne = pool_release_body(ring, capacity, live, slots, n, end, red, &bad_rel);
+  __syncthreads();  // the appended ring entries are visible to every lane
+  int64_t nc = cursor;
+  const bool fit = pool_allocate_body(ring, capacity, live, markers, batch, out, cursor, ne, red, &bad_live, &nc);
+  if (bad_rel) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrUnowned);
+  if (bad_live) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrLive);
+  if (!fit && threadIdx.x == 0) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrExhausted);
+  __syncthreads();  // every lane has read st[0] and st[1]
+  if (threadIdx.x == 0) {
+    st[1] = ne;
+    if (fit) st[0] = nc;
+  }
 }
 
 }  // namespace
@@ -411,6 +455,18 @@ int ls_slot_pool_allocate(const int64_t* ring, int64_t capacity, int64_t* state,
   hipLaunchKernelGGL(pool_allocate_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
                      capacity, state, live, valid_markers, batch, out_cache_locs);
   return check_launch("slot_pool_allocate launch");
+}
+
+int ls_slot_pool_step(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live, const int64_t* slots,
+                      int64_t count, const int64_t* valid_markers, int64_t batch, int64_t* out_cache_locs,
+                      ls_stream_t stream) {
+  if (capacity <= 0 || count < 0 || batch < 0) return fail(LS_ERR_VALUE, "slot_pool_step: invalid sizes");
+  if (count == 0 && batch == 0) return LS_OK;
+  if (!ring || !state || !live || (count > 0 && !slots) || (batch > 0 && (!valid_markers || !out_cache_locs)))
+    return fail(LS_ERR_VALUE, "slot_pool_step: NULL pointer");
+  hipLaunchKernelGGL(pool_step_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
+                     capacity, state, live, slots, count, valid_markers, batch, out_cache_locs);
+  return check_launch("slot_pool_step launch");
 }
 
 int ls_slot_pool_release(int64_t* ring, int64_t capacity, int64_t* state, uint32_t* live, const int64_t* slots,

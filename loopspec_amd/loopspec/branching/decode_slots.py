@@ -77,6 +77,20 @@ class DeviceSlotPool:
         _lib.call("ls_slot_pool_release", self.free_slots.data_ptr(), self.capacity, self.state.data_ptr(),
                   self.live.data_ptr(), slots.data_ptr(), slots.numel(), self._stream())
 
+    def step(self, slots: torch.Tensor, valid_markers: torch.Tensor, out_cache_locs: torch.Tensor) -> None:
+        """release(slots) then allocate(valid_markers, out_cache_locs), in one
+        launch (a decode step's order: pruned timelines give their IDs back
+        before the next rows take theirs)."""
+        for t, what in ((slots, "slots"), (valid_markers, "valid_markers"), (out_cache_locs, "out_cache_locs")):
+            _lib.require_cuda(t, "slot pool step")
+            if t.dtype != torch.int64 or t.dim() != 1 or not t.is_contiguous():
+                raise ValueError(f"slot pool step: {what} must be contiguous int64 [n]")
+        if valid_markers.shape != out_cache_locs.shape:
+            raise ValueError("slot pool step: valid_markers and out_cache_locs differ in shape")
+        _lib.call("ls_slot_pool_step", self.free_slots.data_ptr(), self.capacity, self.state.data_ptr(),
+                  self.live.data_ptr(), slots.data_ptr(), slots.numel(), valid_markers.data_ptr(),
+                  valid_markers.numel(), out_cache_locs.data_ptr(), self._stream())
+
     def errors(self) -> int:
         """The error bits so far (one device read)."""
         return int(self.state[2].item())

@@ -263,3 +263,37 @@ def test_device_slot_pool_in_graph_replays(gpu):
         assert out.cpu().tolist() == want, rep
         prev = want
     assert pool.errors() == 0
+
+
+def test_device_slot_pool_step_is_release_then_allocate(gpu):
+    """The fused step against the reference pool's release-then-allocate, in
+    a replayed graph (the released IDs of a step are the previous step's)."""
+    cap, batch = 512, 96
+    markers = torch.from_numpy(np.where(np.arange(batch) % 5 == 3, -1, 0).astype(np.int64)).to(gpu)
+    n = int((markers >= 0).sum().item())
+    pool = DeviceSlotPool(cap, gpu)
+    pool.begin(20)
+    ref = og.DecodeSlotPool(cap)
+    ref.begin(20)
+    out = [torch.full((batch,), -1, dtype=torch.int64, device=gpu) for _ in range(2)]
+    pool.allocate(markers, out[1])
+    first = ref.allocate(n)
+    held = [first]
+    ids = [torch.empty(n, dtype=torch.int64, device=gpu) for _ in range(2)]
+    valid = (markers >= 0).nonzero().flatten()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("device slot pool fused step in a graph")
+    with torch.cuda.graph(g):
+        for i in range(2):
+            ids[i].copy_(out[1 - i][valid])
+            pool.step(ids[i], markers, out[i])
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            ref.release(held[-1])
+            want = ref.allocate(n)
+            held.append(want)
+            assert out[i].cpu().numpy()[markers.cpu().numpy() >= 0].tolist() == want, (rep, i)
+    assert pool.errors() == 0
