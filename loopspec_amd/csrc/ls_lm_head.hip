@@ -9,9 +9,9 @@
 //
 // Both operands are K-contiguous (hidden [M, H] row-major, weight [V, H] as
 // nn.Linear stores it), so each MFMA operand fragment is one 16-byte load.
-// One 512-lane workgroup computes a 320-row x 192-column tile with
-// v_mfma_f32_16x16x32_bf16: waves form a 2 (rows) x 4 (columns) grid, each
-// wave 10 x 3 tiles of 16 x 16 (120 accumulator registers). Both operands are
+// One 1024-lane workgroup computes a 320-row x 192-column tile with
+// v_mfma_f32_16x16x32_bf16: sixteen waves (four per SIMD) form a 4 (rows) x 4
+// (columns) grid, each wave 5 x 3 tiles of 16 x 16 (60 accumulator registers). Both operands are
 // staged through LDS in k-blocks of 64 (16-byte chunks XOR-swizzled by row):
 // the weight by direct global-to-LDS loads (global_load_lds_dwordx4) two
 // blocks ahead into a ring of three buffers, so two blocks of HBM reads are in
@@ -34,20 +34,18 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLmLanes = 512;
-constexpr int kLmMT = 10;                      // 16-row tiles per wave
+constexpr int kLmLanes = 1024;
+constexpr int kLmMT = 5;                       // 16-row tiles per wave
 constexpr int kLmNT = 3;                       // 16-column tiles per wave
-constexpr int kLmRowsPerWave = 16 * kLmMT;     // 160
+constexpr int kLmRowsPerWave = 16 * kLmMT;     // 80
 constexpr int kLmColsPerWave = 16 * kLmNT;     // 48
-constexpr int kLmBM = 2 * kLmRowsPerWave;      // 320 rows per workgroup
+constexpr int kLmBM = 4 * kLmRowsPerWave;      // 320 rows per workgroup
 constexpr int kLmBN = 4 * kLmColsPerWave;      // 192 columns per workgroup
 constexpr int kLmKB = 64;                      // k per LDS block
 constexpr int kLmRowBytes = kLmKB * 2;         // 128 bytes of a row's k-block
-constexpr int kLmChunks = kLmBM * kLmRowBytes / 16;         // 2560 16-byte chunks per A block
-constexpr int kLmChunksPerLane = kLmChunks / kLmLanes;      // 5
-constexpr int kLmBChunks = kLmBN * kLmRowBytes / 16;        // 1536 per B block
-constexpr int kLmBChunksPerLane = kLmBChunks / kLmLanes;    // 3
-static_assert(kLmChunks % kLmLanes == 0 && kLmBChunks % kLmLanes == 0, "block chunks spread evenly");
+constexpr int kLmARounds = 3;  // 40 x 1 KB per A block over 16 waves: rounds 0-1 all, round 2 waves 0-7
+static_assert(kLmBM * kLmRowBytes == 40 * 1024 && kLmBN * kLmRowBytes == 24 * 1024, "1 KB rounds per block");
+constexpr int kLmBRounds = 2;  // 24 x 1 KB per B block: round 0 all, round 1 waves 0-7
 
 struct LmParams {
   const char* hidden;   // [M, H] bf16, row stride hs elements
@@ -91,41 +89,47 @@ __global__ __launch_bounds__(kLmLanes) void lm_head_kernel(const LmParams p) {
   const int nkb = static_cast<int>(p.H / kLmKB);
 
   // Direct loads: round i of wave w puts lane l's 16 bytes at LDS chunk
-  // j = (8i + w) * 64 + l, i.e. row j/8 of the buffer, swizzled chunk l & 7,
-  // so the lane fetches logical chunk (l & 7) ^ (row & 7) of that row. Rows
-  // past the matrix are clamped into it (their results are never used).
-  // Byte offsets from the block's first row.
+  // j = (16i + w) * 64 + l, i.e. row j/8 of the buffer, swizzled chunk l & 7,
+  // so the lane fetches logical chunk (l & 7) ^ (row & 7) of that row. A block
+  // of hidden rows is 40 such 1 KB rounds (waves 0-7 do a third), one of
+  // weight rows 24 (waves 0-7 do a second). Rows past the matrix are clamped
+  // into it (their results are never used). Byte offsets from the block's
+  // first row (rounds a wave does not issue get an in-range dummy).
   const uint32_t lchunk = static_cast<uint32_t>(((lane & 7) ^ ((lane >> 3) & 7)) << 4);
   const char* abase = p.hidden + m_base * p.hs * 2;
-  uint32_t aoff[kLmChunksPerLane];
+  uint32_t aoff[kLmARounds];
 #pragma unroll
-  for (int i = 0; i < kLmChunksPerLane; ++i) {
-    const int r = (i * 8 + wid) * 8 + (lane >> 3);
+  for (int i = 0; i < kLmARounds; ++i) {
+    const int r = ((i * 16 + wid) * 8 + (lane >> 3)) % kLmBM;
     const int64_t rr = m_base + r < p.M ? r : p.M - 1 - m_base;
     aoff[i] = static_cast<uint32_t>(rr * p.hs * 2) + lchunk;
   }
   const char* bbase = p.weight + n_base * p.ws * 2;
-  uint32_t boff[kLmBChunksPerLane];
+  uint32_t boff[kLmBRounds];
 #pragma unroll
-  for (int i = 0; i < kLmBChunksPerLane; ++i) {
-    const int r = (i * 8 + wid) * 8 + (lane >> 3);
+  for (int i = 0; i < kLmBRounds; ++i) {
+    const int r = ((i * 16 + wid) * 8 + (lane >> 3)) % kLmBN;
     const int64_t rr = n_base + r < p.V ? r : p.V - 1 - n_base;
     boff[i] = static_cast<uint32_t>(rr * p.ws * 2) + lchunk;
   }
   auto dma_a = [&](int kb, uint8_t* dst) {
     const char* base = abase + static_cast<int64_t>(kb) * kLmRowBytes;
 #pragma unroll
-    for (int i = 0; i < kLmChunksPerLane; ++i) {
-      const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 8 + wid) * 1024;
-      dma16(base + aoff[i], __builtin_amdgcn_readfirstlane(lds));
+    for (int i = 0; i < kLmARounds; ++i) {
+      if (i * 16 + wid < 40) {
+        const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 16 + wid) * 1024;
+        dma16(base + aoff[i], __builtin_amdgcn_readfirstlane(lds));
+      }
     }
   };
   auto dma_b = [&](int kb, uint8_t* dst) {
     const char* base = bbase + static_cast<int64_t>(kb) * kLmRowBytes;
 #pragma unroll
-    for (int i = 0; i < kLmBChunksPerLane; ++i) {
-      const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 8 + wid) * 1024;
-      dma16(base + boff[i], __builtin_amdgcn_readfirstlane(lds));
+    for (int i = 0; i < kLmBRounds; ++i) {
+      if (i * 16 + wid < 24) {
+        const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)) + (i * 16 + wid) * 1024;
+        dma16(base + boff[i], __builtin_amdgcn_readfirstlane(lds));
+      }
     }
   };
 
@@ -140,19 +144,14 @@ __global__ __launch_bounds__(kLmLanes) void lm_head_kernel(const LmParams p) {
   // is an immediate offset)
   const int fr_a = (wm * kLmRowsPerWave + (lane & 15)) * kLmRowBytes;
   const int fr_b = (wn * kLmColsPerWave + (lane & 15)) * kLmRowBytes;
-  // One k-block: 2 k-steps x 5 pairs of row tiles. Each pair's fragments
-  // (and each k-step's column fragments) are read one pair ahead, before the
-  // current pair's MFMAs, so the LDS latency overlaps them; a scheduling fence
-  // after each pair keeps the compiler from hoisting every read (which would
-  // need some 50 more registers).
+  // One k-block: 2 k-steps x 5 row tiles. Each tile's fragment (and each
+  // k-step's column fragments) is read one tile ahead, before the current
+  // tile's MFMAs, so the LDS latency overlaps them; a scheduling fence after
+  // each tile keeps the compiler from hoisting every read.
   auto compute = [&](const uint8_t* abuf, const uint8_t* bbuf) {
-    constexpr int kPairs = kLmMT / 2;
     auto sw = [&](int ks) { return ((ks * 4 + (lane >> 4)) ^ (lane & 7)) << 4; };
-    auto read_a = [&](int ks, int mp, bf16x8 (&a)[2]) {
-      const uint8_t* const fa = abuf + fr_a + sw(ks);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        a[h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fa + (mp + h) * 16 * kLmRowBytes));
+    auto read_a = [&](int ks, int mt) {
+      return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(abuf + fr_a + sw(ks) + mt * 16 * kLmRowBytes));
     };
     auto read_b = [&](int ks, bf16x8 (&b)[kLmNT]) {
       const uint8_t* const fb = bbuf + fr_b + sw(ks);
@@ -160,46 +159,44 @@ __global__ __launch_bounds__(kLmLanes) void lm_head_kernel(const LmParams p) {
       for (int nt = 0; nt < kLmNT; ++nt)
         b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(fb + nt * 16 * kLmRowBytes));
     };
-    bf16x8 acur[2], anext[2], bcur[kLmNT], bnext[kLmNT];
+    bf16x8 acur, anext, bcur[kLmNT], bnext[kLmNT];
     read_b(0, bcur);
-    read_a(0, 0, acur);
+    acur = read_a(0, 0);
 #pragma unroll
-    for (int g = 0; g < 2 * kPairs; ++g) {
-      const int ks = g / kPairs, mp = 2 * (g % kPairs);
-      if (g + 1 < 2 * kPairs) {
-        const int ks1 = (g + 1) / kPairs, mp1 = 2 * ((g + 1) % kPairs);
+    for (int g = 0; g < 2 * kLmMT; ++g) {
+      const int ks = g / kLmMT, mt = g % kLmMT;
+      if (g + 1 < 2 * kLmMT) {
+        const int ks1 = (g + 1) / kLmMT, mt1 = (g + 1) % kLmMT;
         if (ks1 != ks) read_b(ks1, bnext);
-        read_a(ks1, mp1, anext);
+        anext = read_a(ks1, mt1);
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int nt = 0; nt < kLmNT; ++nt)
-          acc[mp + h][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(acur[h], bcur[nt], acc[mp + h][nt], 0, 0, 0);
-      }
+      for (int nt = 0; nt < kLmNT; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(acur, bcur[nt], acc[mt][nt], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      acur[0] = anext[0];
-      acur[1] = anext[1];
-      if (g + 1 == kPairs) {
+      acur = anext;
+      if (g + 1 == kLmMT) {
 #pragma unroll
         for (int nt = 0; nt < kLmNT; ++nt) bcur[nt] = bnext[nt];
       }
     }
   };
-  // End of block kb: every direct load but the newest weight block's
-  // (kLmBChunksPerLane of them, when issued) has landed in LDS, this lane's
-  // LDS reads are done, then the workgroup meets.
+  // End of block kb: every direct load but the newest weight block's (this
+  // wave's kLmBRounds or kLmBRounds - 1 of them, when issued) has landed in
+  // LDS, this lane's LDS reads are done, then the workgroup meets.
   auto block_end = [&](bool newest_in_flight) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (newest_in_flight) {
-      __builtin_amdgcn_s_waitcnt(0x0073);  // vmcnt(3) expcnt(7) lgkmcnt(0)
+    if (newest_in_flight && wid < 8) {
+      __builtin_amdgcn_s_waitcnt(0x0072);  // vmcnt(2) expcnt(7) lgkmcnt(0)
+    } else if (newest_in_flight) {
+      __builtin_amdgcn_s_waitcnt(0x0071);  // vmcnt(1)
     } else {
       __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7) lgkmcnt(0)
     }
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
-  static_assert(kLmBChunksPerLane == 3, "block_end's vmcnt counts the newest block's direct loads");
+
 
   // block kb: hidden rows in a[kb & 1], weight rows in b[kb % 3]; unrolled by
   // six so that every buffer is named statically. Per block, the hidden rows
