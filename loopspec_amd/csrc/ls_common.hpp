@@ -202,12 +202,14 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 }
 
 // Block-wide reductions; `smem` needs BLOCK/64 slots. Result broadcast to all.
+// block_max_u64 writes its slots without a barrier first: no other use of
+// `smem` may be in flight when it is called (one call per kernel, or a
+// barrier between calls).
 template <int BLOCK>
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* smem) {
   constexpr int kWaves = BLOCK / kWave;
   v = wave_max_u64(v);
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  __syncthreads();
   if (lane == 0) smem[wid] = v;
   __syncthreads();
   uint64_t r = smem[0];
