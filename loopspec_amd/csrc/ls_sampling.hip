@@ -48,7 +48,8 @@ constexpr int kRW = kRB / kWave;
 constexpr int kPerLane = kChunk / kWave;     // 32 elements per lane: one wave per chunk
 constexpr int kChunkCand = 64;               // candidate slots per chunk in the workspace
 constexpr int kOctBins = 16;                 // exponent bins of e
-constexpr int kHistStride = kOctBins + 1;    // lane-private bins, padded against bank conflicts
+constexpr int kHistStride = kOctBins + 1;    // bins of a lane pair, padded against bank conflicts
+constexpr int kHistRows = kWave / 2;         // lanes t and t + 32 share a row of bins
 constexpr int kRowCand = 2048;               // candidate slots of a row
 constexpr int kSlotsPerLane = kRowCand / kRB;
 constexpr int kMaxChunks = 128;              // vocab <= 262144
@@ -57,7 +58,9 @@ constexpr int kBins = 2048;                  // radix digits per round
 constexpr int kBinsPerLane = kBins / kRB;
 constexpr int kGather = kWave;               // bucket size finished by one wave
 constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
-constexpr int kChunkWavesPerCu = 12;         // resident chunk waves per CU (LDS-bound)
+// Resident chunk waves per CU: 15 fit the LDS, but 12 measured fastest on
+// MI355X (C3 and C4: 8, 10 and 15 all slower).
+constexpr int kChunkWavesPerCu = 12;
 constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
 constexpr uint32_t kNone = 0xffffffffu;
@@ -210,7 +213,10 @@ __device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
 // ---------------------------------------------------------------------------
 struct ChunkSh {
   float est[kChunk];                   // e of the chunk, 16-byte slots XOR-swizzled
-  uint32_t hist[kWave * kHistStride];  // lane-private exponent bins
+  // exponent bins, 16-bit counts: lane t < 32 counts bin b in the low half of
+  // word b of row t, lane t + 32 in the high half of word 15 - b of row t
+  // (the two lanes meet on one word only for bins 0 and 15, rarely together)
+  uint32_t hist[kHistRows * kHistStride];
 };
 
 // Physical float index of element v of the chunk in the e-store.
@@ -299,9 +305,12 @@ template <bool IN_ALL, int DT, int NVC>
 __device__ __forceinline__ void exp_bins(const SampParams& p, ChunkSh& cs, float (&x)[NVC * Elem<DT>::kPerVec],
                                          int t, int nvc, float nmc) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  // byte offset of this lane's bin 0 in the histogram
-  const int hbase4 = static_cast<int>(reinterpret_cast<uintptr_t>(&cs.hist[t * kHistStride]) -
-                                      reinterpret_cast<uintptr_t>(&cs.hist[0]));
+  // byte offset of this lane's bin-0 word, the step per -bin and the
+  // increment of its 16-bit half
+  const int hi = t >> 5;
+  const int hbase4 = ((t & 31) * kHistStride + (hi ? kOctBins - 1 : 0)) * 4;
+  const int hstep4 = hi ? 4 : -4;
+  const uint32_t hinc = hi ? 0x10000u : 1u;
   char* hist0 = reinterpret_cast<char*>(&cs.hist[0]);
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
@@ -312,7 +321,7 @@ __device__ __forceinline__ void exp_bins(const SampParams& p, ChunkSh& cs, float
       x[u * EPV + e] = exp2q_k(__builtin_fmaf(x[u * EPV + e], p.c, nmc), &ki);
       const int b = __builtin_elementwise_min(__builtin_elementwise_max(ki, -(kOctBins - 1)), 0);  // -bin
       if (in)
-        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(hist0 + (hbase4 - 4 * b)), 1u, __ATOMIC_RELAXED,
+        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(hist0 + (hbase4 + __mul24(hstep4, b))), hinc, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 #pragma unroll
@@ -385,18 +394,23 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
   const float mass = wave_tree_sum(lane_tree_sum(x));
   __syncthreads();
 
-  // 3. bin totals: lane (b, q) sums bin b of lanes 16q..16q+15 and clears it
+  // 3. bin totals: lane t < 32 (b = t & 15, q = t >> 4) sums word b of rows
+  //    16q..16q+15 and clears it (both 16-bit halves at once: a half sums to
+  //    at most 32 * 32); the low halves of word b count bin b of lanes 0..31,
+  //    the high halves of word 15 - b bin b of lanes 32..63
   uint32_t bc;
   {
-    const int b = t & (kOctBins - 1), q = t >> 4;
+    const int b = t & (kOctBins - 1), q = (t >> 4) & 1;
     uint32_t sb = 0;
+    if (t < kHistRows) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      sb += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int i = 0; i < 16; ++i)
+        sb += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     sb += __shfl_xor(sb, 16);
-    sb += __shfl_xor(sb, 32);
-    bc = t < kOctBins ? sb : 0u;
+    const uint32_t mirror = __shfl(sb, kOctBins - 1 - b);
+    bc = t < kOctBins ? (sb & 0xffffu) + (mirror >> 16) : 0u;
   }
   // lane-contiguous e: elements [32t, 32t + 32) (index order within the lane)
   float ec[kPerLane];
@@ -460,7 +474,7 @@ void chunk_kernel(const SampParams p) {
   constexpr int NVC = kChunk / (kWave * EPV);  // vectors per lane: 8 (f32) or 4
   __shared__ ChunkSh cs;
   const int t = threadIdx.x;
-  for (int i = t; i < kWave * kHistStride; i += kWave) cs.hist[i] = 0u;
+  for (int i = t; i < kHistRows * kHistStride; i += kWave) cs.hist[i] = 0u;
   __syncthreads();
   int item = blockIdx.x;
   if (item >= p.items) return;
