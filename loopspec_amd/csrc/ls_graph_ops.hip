@@ -338,6 +338,66 @@ __global__ __launch_bounds__(kScanBlock) void pool_step_kernel(int64_t* __restri
   }
 }
 
+// The same step when both lists fit one pass (n, batch <= kScanBlock), with
+// fewer dependent device round trips: the IDs the allocation can take are
+// ring[cursor, end) followed by this step's released IDs, so the first are
+// loaded at the start (beside the state, the released IDs and the markers)
+// and the second are placed beside them in LDS as the release ranks them.
+// Nothing is read back from the ring, and no lane waits for the ring writes.
+__global__ __launch_bounds__(kScanBlock) void pool_step_one_pass_kernel(int64_t* __restrict__ ring, int64_t capacity,
+                                                                        int64_t* st, uint32_t* live,
+                                                                        const int64_t* __restrict__ slots, int64_t n,
+                                                                        const int64_t* __restrict__ markers,
+                                                                        int64_t batch, int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kScanBlock / kWave];
+  __shared__ int64_t window[kScanBlock];  // ring[(cursor + j) % capacity] after the release, j < kScanBlock
+  const int t = static_cast<int>(threadIdx.x);
+  const int64_t cursor = st[0], end = st[1];
+  const int64_t slot = t < n ? slots[t] : 0;
+  const bool valid = t < batch && markers[t] >= 0;
+  const int64_t avail = end - cursor;  // IDs in the ring before the release
+  if (cursor >= 0 && t < avail) window[t] = ring[(cursor + t) % capacity];
+  // release: clear the live bits, append the IDs that were live in order
+  bool ok = false;
+  if (t < n && slot >= 1 && slot <= capacity) {
+    const uint32_t bit = 1u << (slot & 31);
+    ok = (atomicAnd(live + (slot >> 5), ~bit) & bit) != 0u;
+  }
+  const bool bad_rel = t < n && !ok;
+  uint32_t released;
+  const uint32_t rrank = block_excl_scan_u32(ok ? 1u : 0u, red, &released);
+  if (ok) {
+    ring[(end + rrank) % capacity] = slot;
+    const int64_t j = avail + rrank;
+    if (j >= 0 && j < kScanBlock) window[j] = slot;
+  }
+  const int64_t ne = end + released;
+  // allocate: valid row of rank r takes window[r] (r < count <= ne - cursor;
+  // the scan's barriers order the window writes before these reads)
+  uint32_t count;
+  const uint32_t arank = block_excl_scan_u32(valid ? 1u : 0u, red, &count);
+  const bool fit = cursor + count <= ne;
+  bool bad_live = false;
+  if (fit && valid) {
+    const int64_t s = window[arank];
+    out[t] = s;
+    if (s >= 1 && s <= capacity) {
+      const uint32_t bit = 1u << (s & 31);
+      bad_live = (atomicOr(live + (s >> 5), bit) & bit) != 0u;
+    } else {
+      bad_live = true;
+    }
+  }
+  if (bad_rel) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrUnowned);
+  if (bad_live) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrLive);
+  if (!fit && t == 0) atomicOr(reinterpret_cast<unsigned long long*>(st + 2), kPoolErrExhausted);
+  // every lane read st[0] and st[1] before the scans' barriers
+  if (t == 0) {
+    st[1] = ne;
+    if (fit) st[0] = cursor + count;
+  }
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -464,8 +524,13 @@ int ls_slot_pool_step(int64_t* ring, int64_t capacity, int64_t* state, uint32_t*
   if (count == 0 && batch == 0) return LS_OK;
   if (!ring || !state || !live || (count > 0 && !slots) || (batch > 0 && (!valid_markers || !out_cache_locs)))
     return fail(LS_ERR_VALUE, "slot_pool_step: NULL pointer");
-  hipLaunchKernelGGL(pool_step_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
-                     capacity, state, live, slots, count, valid_markers, batch, out_cache_locs);
+  if (count <= kScanBlock && batch <= kScanBlock) {
+    hipLaunchKernelGGL(pool_step_one_pass_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream),
+                       ring, capacity, state, live, slots, count, valid_markers, batch, out_cache_locs);
+  } else {
+    hipLaunchKernelGGL(pool_step_kernel, dim3(1), dim3(kScanBlock), 0, static_cast<hipStream_t>(stream), ring,
+                       capacity, state, live, slots, count, valid_markers, batch, out_cache_locs);
+  }
   return check_launch("slot_pool_step launch");
 }
 

@@ -297,3 +297,28 @@ def test_device_slot_pool_step_is_release_then_allocate(gpu):
             held.append(want)
             assert out[i].cpu().numpy()[markers.cpu().numpy() >= 0].tolist() == want, (rep, i)
     assert pool.errors() == 0
+
+
+@pytest.mark.parametrize("batch", [100, 1100])
+def test_device_slot_pool_step_takes_ids_it_releases(gpu, batch):
+    """A step whose allocation runs past the IDs free before it takes the IDs
+    it has just released, in release order, across the ring's wrap (batch 100:
+    the one-pass kernel; 1100: the multi-pass one)."""
+    cap = 2400
+    pool = DeviceSlotPool(cap, gpu)
+    pool.begin(0)
+    ref = og.DecodeSlotPool(cap)
+    ref.begin(0)
+    first_n = cap - batch // 2  # leaves batch // 2 IDs free
+    out0 = torch.empty(first_n, dtype=torch.int64, device=gpu)
+    pool.allocate(torch.zeros(first_n, dtype=torch.int64, device=gpu), out0)
+    want0 = ref.allocate(first_n)
+    assert out0.cpu().tolist() == want0
+    rel = want0[::-1][:batch]  # released in reverse allocation order
+    ref.release(rel)
+    want = ref.allocate(batch)
+    out = torch.full((batch,), -1, dtype=torch.int64, device=gpu)
+    announce(f"device slot pool step past the free IDs B={batch}")
+    pool.step(torch.tensor(rel, dtype=torch.int64, device=gpu), torch.zeros(batch, dtype=torch.int64, device=gpu), out)
+    assert pool.errors() == 0
+    assert out.cpu().tolist() == want
