@@ -24,6 +24,7 @@
 namespace ls {
 
 constexpr float kLog2e = 1.44269504f;          // 0x3FB8AA3B
+constexpr double kLog2eD = 1.4426950408889634; // log2(e) in binary64
 constexpr float kExp2Floor = -200.0f;
 constexpr float kExp2C0 = 1.0f;
 constexpr float kExp2C1 = 0x1.62e428p-1f;

@@ -1,38 +1,42 @@
 // (a) logit processing and (c) lossless speculative sampling for gfx950.
 //
-// Two launches per call (a third, first, with a repetition penalty; a last
-// one for dense outputs):
-//   bitmap_kernel    one workgroup per batch element turns its token history
-//                    into a vocabulary bitmap in the workspace.
-//   chunk_kernel     persistent, one wave per (row, chunk) item of kChunk =
-//                    2048 logits, items in row-major order, the next item's
-//                    loads in flight while the current one is processed. Per
-//                    item: the penalised chunk max m_j, mc_j = RN(m_j c) with
-//                    c = RN(log2e RN(1/T)), e = exp2q(fma(x, c, -mc_j)), the
-//                    chunk mass M_j (a fixed pairwise tree), a histogram of
-//                    exp2q's exponent (bins 0..15 below the chunk max) and the
-//                    chunk's candidates: every e >= kCandScale 2^-K, K the
-//                    number of leading bins holding at most cap entries
-//                    together, written in index order; then a 32-byte record
-//                    (mc_j, K, count, M_j, e of the row's draft token).
-//   spec_row_kernel  one 512-lane workgroup per (batch element, position i):
-//                    the target and the draft row of position i side by side
-//                    (the bonus row alone for i == k). S = sum_j f_j M_j with
-//                    f_j = exp2q(mc_j - max mc), g_j = RN(f_j / S),
-//                    p = RN(e g_j) for the candidates; the exact top-p cutoff
-//                    by a radix select on the binary32 bits of p with 2^-46
-//                    fixed-point masses (replacing sort + cumsum +
-//                    searchsorted, distributions.py:59-70), valid iff it
-//                    exceeds the bound on every p outside the candidates
-//                    (otherwise the row is re-read for an exact select); the
-//                    accept bit of x_i and the residual draw. The last of the
-//                    k+1 workgroups of a batch element writes its accepted
-//                    length and tokens.
-//   row_kernel       sample and dense modes: one workgroup per row, the same
-//                    finalisation, then a draw or the row statistics.
-//   dense_kernel     dense mode: p and/or the filtered, renormalised rows.
-// The arithmetic is the declared arithmetic of ls_numerics.hpp (restated by
-// oracle/sampling.py), so every output is bit-identical to the oracle's.
+// Launches per call: bitmap_kernel (with a repetition penalty: each batch
+// element's token history as a vocabulary bitmap), then fused_kernel, then,
+// for dense outputs only, dense_kernel.
+//
+// fused_kernel is persistent. A 256-lane workgroup (four waves) takes four
+// consecutive (row, 2048-element chunk) items per step -- the first ticket
+// by its block index, the rest from eight interleaved ticket counters -- and
+// each wave streams one chunk:
+//   * its logits staged in LDS, decoded, penalised tokens set aside;
+//   * chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk mass M_j in
+//     the declared pairwise order; the penalised tokens' own max and mass
+//     (pm_j, PM_j) from a sparse pass over them (x / r or x * r);
+//   * candidates: every element with e >= 2^-L, L from a binary search on
+//     the chunk's vector maxima (at most `cap` vectors reach it), lowered
+//     until at most `cap` elements remain,
+//     written as (index, processed logit); a 32-byte record per chunk.
+// Then the wave stores drain and it arrives on its unit's counter. A unit is
+// a pair (target row i, draft row i) of a batch element (spec, i < k), the
+// bonus target row (spec, i = k) or one row (sample / dense). The workgroup
+// that brings a unit's last chunk finalises it at once, all four waves
+// together, while the other workgroups keep streaming:
+//   * row constants from the records: mcmax, S, and per chunk the largest p a
+//     non-candidate can have (exact, because p is monotone in the logit);
+//   * every candidate's p = RN(exp2p(RN32(fma64(x, cd, -mcmax))) / S) into
+//     LDS, the exact top-p cutoff by a three-round radix select on the
+//     binary32 bits of p with 2^-46 fixed-point masses (the value semantics
+//     of sort + cumsum + searchsorted, distributions.py:59-70);
+//   * valid when the cutoff exceeds every chunk's non-candidate bound; else
+//     the chunks whose bound reaches it are re-read and their {p >= cutoff}
+//     replaces their candidates (exact, since that cutoff is a lower bound of
+//     the row's); else the whole row is selected by passes over it;
+//   * spec: the accept bit of x_i, the residual draw on rejection, the bonus
+//     draw for i = k; the last of the k+1 units of a batch element writes its
+//     accepted length and tokens. sample: the draw. dense: the statistics.
+// The arithmetic is the declared arithmetic of ls_numerics.hpp, restated by
+// oracle/sampling.py and oracle/native/ls_oracle.c, so every output is
+// bit-identical to the oracle's.
 #include "ls_common.hpp"
 #include "ls_numerics.hpp"
 #include "ls_runtime.hpp"
@@ -40,122 +44,153 @@
 namespace ls {
 namespace {
 
-constexpr int kChunk = 2048;                 // softmax chunk (declared arithmetic)
-constexpr int kChunkShift = 11;
-constexpr int kCB = 256;                     // dense kernel lanes
-constexpr int kRB = 512;                     // row kernel lanes
-constexpr int kRW = kRB / kWave;
-constexpr int kPerLane = kChunk / kWave;     // 32 elements per lane: one wave per chunk
-constexpr int kChunkCand = 64;               // candidate slots per chunk in the workspace
-constexpr int kOctBins = 16;                 // exponent bins of e
-constexpr int kHistStride = kOctBins + 1;    // bins of a lane pair, padded against bank conflicts
-constexpr int kHistRows = kWave / 2;         // lanes t and t + 32 share a row of bins
-constexpr int kRowCand = 2048;               // candidate slots of a row
-constexpr int kSlotsPerLane = kRowCand / kRB;
-constexpr int kMaxChunks = 128;              // vocab <= 262144
+constexpr int kChunk = 2048;               // softmax chunk (declared arithmetic)
+constexpr int kWG = 256;                   // fused workgroup
+constexpr int kNW = kWG / kWave;           // waves per workgroup
+constexpr int kMaxChunks = 128;            // vocab <= 262144
 constexpr int kMaxVocab = kMaxChunks * kChunk;
-constexpr int kBins = 2048;                  // radix digits per round
-constexpr int kBinsPerLane = kBins / kRB;
-constexpr int kGather = kWave;               // bucket size finished by one wave
-constexpr int kCounterStride = 16;           // arrival counters one 64-byte line apart
-// Resident chunk waves per CU: 15 fit the LDS, but 12 measured fastest on
-// MI355X (C3 and C4: 8, 10 and 15 all slower).
-constexpr int kChunkWavesPerCu = 12;
+constexpr int kRowCap = 2048;              // LDS entries per row in the finaliser
+constexpr int kRadixBits = 10;
+constexpr int kBins = 1 << kRadixBits;     // radix digits per round
+constexpr int kMaxLevel = 31;              // candidate levels: e >= 2^-L, L in [0, 31]
+constexpr int kTickets = 8;                // ticket counters, one 64-byte line each
+constexpr int kLineU32 = 16;
+constexpr int kWgPerCu = 3;
 constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
+constexpr int64_t kMaxK = 64;
+// unit counters at a fixed place, sized for the largest call (spec: B (k+1))
+constexpr int64_t kMaxUnits = kMaxSpecBatch * (kMaxK + 1);
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
-// kFlagRebuilt: the candidates of some chunks were replaced (same slot layout)
-enum RowFlag : uint32_t { kFlagUnfiltered = 1u, kFlagDense = 2u, kFlagSlow = 4u, kFlagRebuilt = 8u };
-enum ChunkFlag : uint32_t { kChunkComplete = 1u, kChunkHasTok = 2u };
+enum ChunkFlag : uint32_t { kChunkOverflow = 1u, kChunkHasTok = 2u };
+enum RowFlag : uint32_t { kRowFiltered = 1u, kRowList = 2u, kRowEmpty = 4u, kRowSlow = 8u, kRowRefilled = 16u };
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// Per-chunk result, published by the chunk's workgroup.
+// Per-chunk result of the streaming pass.
 struct ChunkRec {
-  float mc;         // RN(chunk max * c)
-  int32_t K;        // candidates are the e >= 2^(1-K) (every e > 0 when complete)
+  float m;          // max of the non-penalised x (-inf if none)
+  float mass;       // M_j
+  float pm;         // max of the penalised x (-inf if none)
+  float pmass;      // PM_j
+  int32_t level;    // candidates: e >= 2^-level relative to max(mc_j, pmc_j); -1 with kChunkOverflow
   uint32_t n;       // candidates written
+  float xtok;       // processed logit of the row's draft token (kChunkHasTok)
   uint32_t flags;
-  float mass;       // chunk mass M_j
-  float e_tok;      // e of the row's draft token when it lies in this chunk
-  uint32_t pad0, pad1;
 };
 static_assert(sizeof(ChunkRec) == 32, "ChunkRec layout");
 
-// Published per-row statistics.
+// Published per-row statistics (dense mode).
 struct RowStat {
-  float mcmax;      // row max of mc_j
-  float s;          // normaliser S
-  float cutoff;     // top-p cutoff value (0 when unfiltered)
-  float mass;       // binary32 retained mass (renormaliser; 1 when unfiltered)
-  uint32_t flags;
-  float p_tok;      // filtered probability of the row's draft token
-  uint64_t mass_fx; // exact retained mass
+  float mcmax, s, cutoff, mass;  // mass: binary32 retained mass (1 when unfiltered)
+  uint32_t flags, pad;
+  uint64_t mass_fx;
 };
 static_assert(sizeof(RowStat) == 32, "RowStat layout");
 
-struct SampParams {
+struct Params {
   const char* base0;           // target / row logits
   int64_t bstride0, pstride0;  // bytes
-  const char* base1;           // draft logits (spec mode)
+  const char* base1;           // draft logits (spec)
   int64_t bstride1, pstride1;
-  int rpg;                     // rows per group: spec 2k+1, else 1
-  int k;                       // spec: draft positions; 0 otherwise
-  int vocab;
-  int nch;                     // chunks per row
-  int cap, cap_log2;           // candidates kept per chunk (a power of two)
-  int bm_words;                // penalty bitmap words per group
-  int items;                   // rows * nch
-  float c;                     // exponent scale RN(log2e * RN(1/T))
-  float pen, inv_pen;
+  int mode, k, rpg;            // rpg: rows per group (spec 2k+1, else 1)
+  int vocab, nch, cap;         // chunks per row, candidate slots per chunk
+  int items, tickets, groups, units;
+  float c;                     // RN32(cd)
+  double cd;                   // RN64(log2(e) / T)
+  float pen;                   // repetition penalty
   int use_pen;
   float top_p;                 // >= 1: unfiltered
   const float* top_p_rows;     // optional per-row top_p (dense mode)
   const int32_t* hist;
   int64_t hist_stride;
   const int32_t* hist_len;
-  // spec mode
+  int bm_words;                // bitmap words per group (nch * 64)
+  // spec
   const int64_t* draft_tokens;  // [B, k]
   const float* uniforms;        // [B, 2k+1]
   int32_t* accept_len;
   int64_t* tokens;              // [B, k+1]
-  // sample mode
-  const float* row_uniforms;    // [rows]
-  int64_t* row_tokens;          // [rows]
-  // dense mode
+  // sample
+  const float* row_uniforms;
+  int64_t* row_tokens;
+  // dense
   float* probs_out;
-  int64_t probs_stride;         // elements
+  int64_t probs_stride;
   float* filt_out;
   int64_t filt_stride;
   float* cutoff_out;
   float* mass_out;
   // workspace
-  ChunkRec* chunks;             // [rows, nch]
-  uint64_t* cands;              // [rows, nch, kChunkCand] of (idx << 32 | bits(e))
-  RowStat* stats;               // [rows]
-  uint32_t* grp_cnt;            // [kMaxSpecBatch * kCounterStride]
-  uint32_t* bitmap;             // [groups, bm_words] penalty bits
-  int64_t* draws;               // spec: [B, k+1] residual draws, then the bonus draw
+  uint32_t* ctl;       // ticket counters [kTickets lines], exit counter [1 line]
+  uint32_t* unit_cnt;  // [units]
+  uint32_t* grp_cnt;   // [groups] (spec)
+  ChunkRec* recs;      // [rows * nch]
+  uint64_t* cands;     // [rows * nch * cap] of (index << 32 | bits(x))
+  RowStat* stats;      // [rows]
+  uint64_t* words;     // [groups * (k+1)] (spec)
+  uint32_t* bitmap;    // [groups * bm_words]
 };
 
-// Row jr of group g: spec rows are target positions 0..k, then draft 0..k-1.
-__device__ __forceinline__ const char* row_of(const SampParams& p, int64_t g, int jr) {
-  if (jr <= p.k) return p.base0 + g * p.bstride0 + jr * p.pstride0;
-  return p.base1 + g * p.bstride1 + (jr - p.k - 1) * p.pstride1;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Declared arithmetic pieces
+// ---------------------------------------------------------------------------
+
+// 2^t for probabilities: the exp2q reduction with the polynomial in binary64,
+// rounded once (monotone over every binary32 t).
+constexpr double kP1 = 0x1.62e42920369e4p-1;
+constexpr double kP2 = 0x1.ebf9bb8a817edp-3;
+constexpr double kP3 = 0x1.c6b752e01b730p-5;
+constexpr double kP4 = 0x1.3cea874a3c256p-7;
+constexpr double kP5 = 0x1.5bba1349df24ap-10;
+
+__device__ __forceinline__ float exp2p(float t) {
+  const float tc = __builtin_fmaxf(t, kExp2Floor);
+  const float kf = __builtin_rintf(tc);
+  const double r = static_cast<double>(tc - kf);
+  double q = kP5;
+  q = __builtin_fma(q, r, kP4);
+  q = __builtin_fma(q, r, kP3);
+  q = __builtin_fma(q, r, kP2);
+  q = __builtin_fma(q, r, kP1);
+  q = __builtin_fma(q, r, 1.0);
+  return __builtin_ldexpf(static_cast<float>(q), static_cast<int>(kf));
 }
 
-// The draft token whose probability row jr of group g contributes to the
-// accept test (target position i and draft position i both test x_i); -1 for
-// the bonus row and outside spec mode.
-__device__ __forceinline__ int64_t row_token(const SampParams& p, int64_t g, int jr) {
-  if (p.k == 0 || jr == p.k) return -1;
-  const int i = jr < p.k ? jr : jr - p.k - 1;
-  return p.draft_tokens[g * p.k + i];
+// The exponent of p: RN32(fma64(x, cd, -mcmax)).
+__device__ __forceinline__ float p_exponent(float x, double cd, float mcmax) {
+  return static_cast<float>(__builtin_fma(static_cast<double>(x), cd, -static_cast<double>(mcmax)));
 }
 
-__device__ __forceinline__ bool bit_of(const uint32_t* bm, int idx) { return (bm[idx >> 5] >> (idx & 31)) & 1u; }
+// p(x) = S > 0 ? RN(exp2p(t) / S) : 0 (correctly rounded division).
+__device__ __forceinline__ float p_of(float x, double cd, float mcmax, float s) {
+  if (!(s > 0.0f)) return 0.0f;
+  return exp2p(p_exponent(x, cd, mcmax)) / s;
+}
+
+// Repetition penalty of one logit (transformers' closed form).
+__device__ __forceinline__ float penalise(float x, float pen) { return x < 0.0f ? x * pen : x / pen; }
+
+// Row constants of one processed row.
+struct RowK {
+  float mcmax, s;
+  double cd;
+};
+
+__device__ __forceinline__ float pval(const RowK& k, float x) { return p_of(x, k.cd, k.mcmax, k.s); }
+
+__device__ __forceinline__ uint64_t pack_u32(uint32_t lo, uint32_t hi) {
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
+// The next binary32 value above t (t finite).
+__device__ __forceinline__ float next_up(float t) {
+  const uint32_t b = __float_as_uint(t);
+  if (b == 0x80000000u || b == 0u) return __uint_as_float(1u);
+  return __uint_as_float((b & 0x80000000u) ? b - 1u : b + 1u);
+}
 
 // ---------------------------------------------------------------------------
 // Wave sums in the declared pairwise order (lanes 2i and 2i+1 first, then
@@ -173,28 +208,15 @@ __device__ __forceinline__ float dpp_add(float v) {
   return __uint_as_float(dpp32<CTRL, ROWS>(0u, __float_as_uint(v))) + v;
 }
 
-// Pairwise sum over the 16 lanes of each row (every lane of the row gets it).
-__device__ __forceinline__ float row_tree_sum(float v) {
+// Pairwise sum over the 64 lanes (wave-uniform result).
+__device__ __forceinline__ float wave_tree_sum(float v) {
   v = dpp_add<kDppQuadXor1, 0xf>(v);
   v = dpp_add<kDppQuadXor2, 0xf>(v);
   v = dpp_add<kDppRowHalfMirror, 0xf>(v);
   v = dpp_add<kDppRowMirror, 0xf>(v);
-  return v;
-}
-
-// Pairwise sum over the 64 lanes (wave-uniform result).
-__device__ __forceinline__ float wave_tree_sum(float v) {
-  v = row_tree_sum(v);
   v = dpp_add<kDppRowBcast15, 0xa>(v);  // rows 1, 3: r0 + r1, r2 + r3
   v = dpp_add<kDppRowBcast31, 0xc>(v);  // row 3: (r0 + r1) + (r2 + r3)
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), kWave - 1));
-}
-
-// Pairwise sum over lanes 0..31 (wave-uniform result).
-__device__ __forceinline__ float half_tree_sum(float v) {
-  v = row_tree_sum(v);
-  v = dpp_add<kDppRowBcast15, 0xa>(v);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 31));
 }
 
 // Pairwise sum of N values held by one lane, adjacent pairs first.
@@ -209,35 +231,142 @@ __device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
 }
 
 // ---------------------------------------------------------------------------
-// Shared memory: the chunk phase and the row / tail phases share one region.
+// Shared memory: the streaming phase and the finaliser share one region.
 // ---------------------------------------------------------------------------
-struct ChunkSh {
-  float est[kChunk];                   // e of the chunk, 16-byte slots XOR-swizzled
-  // exponent bins, 16-bit counts: lane t < 32 counts bin b in the low half of
-  // word b of row t, lane t + 32 in the high half of word 15 - b of row t
-  // (the two lanes meet on one word only for bins 0 and 15, rarely together)
-  uint32_t hist[kHistRows * kHistStride];
+struct StreamSh {
+  u32x4 stage[kNW][kChunk / 4];  // each wave's chunk as loaded (8 KB for 4-byte logits)
 };
 
-// Physical float index of element v of the chunk in the e-store.
-__device__ __forceinline__ int est_index(int v) {
-  const int s = v >> 2;
-  return ((s ^ ((s >> 3) & 7)) << 2) | (v & 3);
+struct RowAux {
+  float mcmax, s, cut, mass_f;   // cutoff (0 unfiltered), binary32 retained mass
+  uint64_t mass_fx;
+  float bmax;                    // largest non-candidate bound
+  float xtok;
+  uint32_t n;                    // LDS entries
+  uint32_t flags;
+  uint32_t has_tok;
+  float top_p;
+};
+
+struct FinSh {
+  union {
+    ChunkRec recs[2][kMaxChunks];  // records of the unit's rows
+    uint64_t bins[kBins];          // radix bins
+    uint64_t csum[kMaxChunks];     // per-chunk weight sums of a draw
+  } u;
+  uint32_t cstart[2][kMaxChunks];  // each chunk's entries in the LDS list
+  uint32_t ccount[2][kMaxChunks];
+  float bound[2][kMaxChunks];      // per-chunk bound on the p of non-candidates
+  struct Entries {
+    uint32_t pbits[kRowCap];       // bits of p
+    uint32_t eidx[kRowCap];        // vocabulary index
+  } ent[2];                        // slot 1's 16 KB double as a draw's u64 weights
+  RowAux aux[2];
+  uint64_t red[2 * kNW];
+  uint64_t red2[2 * kNW];
+  uint32_t sel[4];
+  uint64_t sel64[4];
+  uint32_t list[kWG];              // a draw's entries of one chunk
+  uint32_t nlist;
+  uint32_t nadd;
+  int64_t token;
+};
+
+struct Sh {
+  union {
+    StreamSh st;
+    FinSh fin;
+  };
+  uint32_t pcount[kNW];
+  int32_t ready[2][kNW];
+  uint32_t ticket[3];
+};
+
+// ---------------------------------------------------------------------------
+// Items
+// ---------------------------------------------------------------------------
+struct Item {
+  int unit, row, chunk, group;
+  int64_t tok;
+  const char* rowp;
+};
+
+__device__ __forceinline__ Item item_of(const Params& p, int it) {
+  Item r;
+  if (p.mode == kModeSpec) {
+    const int per_g = p.rpg * p.nch;
+    const int g = it / per_g;
+    const int q = it - g * per_g;
+    const int two = 2 * p.nch;
+    int i, slot, chunk;
+    if (q < p.k * two) {
+      i = q / two;
+      const int w = q - i * two;
+      slot = w >= p.nch ? 1 : 0;
+      chunk = w - slot * p.nch;
+    } else {
+      i = p.k;
+      slot = 0;
+      chunk = q - p.k * two;
+    }
+    r.unit = g * (p.k + 1) + i;
+    r.group = g;
+    r.chunk = chunk;
+    r.row = g * p.rpg + (slot == 0 ? i : p.k + 1 + i);
+    r.rowp = slot == 0 ? p.base0 + g * p.bstride0 + i * p.pstride0 : p.base1 + g * p.bstride1 + i * p.pstride1;
+    r.tok = i < p.k ? p.draft_tokens[static_cast<int64_t>(g) * p.k + i] : -1;
+  } else {
+    const int row = it / p.nch;
+    r.unit = row;
+    r.group = row;
+    r.row = row;
+    r.chunk = it - row * p.nch;
+    r.rowp = p.base0 + static_cast<int64_t>(row) * p.bstride0;
+    r.tok = -1;
+  }
+  return r;
 }
 
-__device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) {
-  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+__device__ __forceinline__ int unit_items(const Params& p, int unit) {
+  if (p.mode == kModeSpec) return (unit % (p.k + 1)) < p.k ? 2 * p.nch : p.nch;
+  return p.nch;
 }
-__device__ __forceinline__ uint64_t pack2f(float lo, float hi) { return pack2(__float_as_uint(lo), __float_as_uint(hi)); }
-__device__ __forceinline__ float lo_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
-__device__ __forceinline__ float hi_f(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
+
+// Logits row of row id r (spec rows: targets 0..k, then drafts 0..k-1).
+__device__ __forceinline__ const char* row_ptr(const Params& p, int r) {
+  if (p.mode != kModeSpec) return p.base0 + static_cast<int64_t>(r) * p.bstride0;
+  const int g = r / p.rpg, jr = r - g * p.rpg;
+  if (jr <= p.k) return p.base0 + g * p.bstride0 + jr * p.pstride0;
+  return p.base1 + g * p.bstride1 + (jr - p.k - 1) * p.pstride1;
+}
+
+__device__ __forceinline__ const uint32_t* row_bitmap(const Params& p, int r) {
+  return p.use_pen ? p.bitmap + static_cast<int64_t>(r / p.rpg) * p.bm_words : nullptr;
+}
+
+__device__ __forceinline__ float row_top_p(const Params& p, int r) {
+  return p.top_p_rows ? p.top_p_rows[r] : p.top_p;
+}
+
+template <int DT>
+__device__ __forceinline__ float decode_bits(uint32_t b) {
+  return bits_to_float<DT>(b);
+}
+
+// Processed logit of element i of a row read from global memory.
+template <int DT>
+__device__ __forceinline__ float load_x(const Params& p, const char* rowp, const uint32_t* bm, int64_t i) {
+  float x = decode_bits<DT>(load_bits<DT>(rowp, i));
+  if (bm && ((bm[i >> 5] >> (i & 31)) & 1u)) x = penalise(x, p.pen);
+  return x;
+}
 
 // ===========================================================================
 // bitmap_kernel: the penalty bitmap of each group's token history
 // ===========================================================================
 constexpr int kBmB = 1024;
 
-__global__ __launch_bounds__(kBmB) void bitmap_kernel(const SampParams p) {
+__global__ __launch_bounds__(kBmB) void bitmap_kernel(const Params p) {
   __shared__ uint32_t bm[kMaxVocab / 32];
   const int t = threadIdx.x;
   const int64_t g = blockIdx.x;
@@ -257,115 +386,92 @@ __global__ __launch_bounds__(kBmB) void bitmap_kernel(const SampParams p) {
 }
 
 // ===========================================================================
-// Chunk phase
+// Streaming pass
 // ===========================================================================
 
-// Loads of one chunk (lanes past the chunk end re-read its last vector), plus,
-// with a penalty, the bitmap word of each vector (the bits of a 16-byte vector
-// always sit in one 32-bit word).
+// Loads of one item (lanes past the chunk end re-read its last vector), plus,
+// with a penalty, the chunk's bitmap word t for lane t.
 template <int DT, int NVC>
-__device__ __forceinline__ void load_chunk(const SampParams& p, int item, u32x4 (&d)[NVC], uint32_t (&pw)[NVC]) {
+__device__ __forceinline__ void load_item(const Params& p, int it, u32x4 (&d)[NVC], uint32_t& pw) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  const int r = item / p.nch;
-  const int cj = item - r * p.nch;
-  const int g = r / p.rpg;
-  const int jr = r - g * p.rpg;
-  const int c0 = cj * kChunk;
+  const Item I = item_of(p, it);
+  const int c0 = I.chunk * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
-  const u32x4* src = reinterpret_cast<const u32x4*>(row_of(p, g, jr)) + c0 / EPV;
+  const u32x4* src = reinterpret_cast<const u32x4*>(I.rowp) + c0 / EPV;
+  const int t = threadIdx.x & (kWave - 1);
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
-    const int v = u * kWave + static_cast<int>(threadIdx.x);
+    const int v = u * kWave + t;
     d[u] = __builtin_nontemporal_load(src + (v < nvc ? v : nvc - 1));
   }
-  if (p.use_pen) {
-    const uint32_t* bm = p.bitmap + static_cast<int64_t>(g) * p.bm_words + c0 / 32;
-#pragma unroll
-    for (int u = 0; u < NVC; ++u) pw[u] = bm[((u * kWave + static_cast<int>(threadIdx.x)) * EPV) >> 5];
+  pw = 0u;
+  if (p.use_pen) pw = p.bitmap[static_cast<int64_t>(I.group) * p.bm_words + I.chunk * (kChunk / 32) + t];
+}
+
+// Element li of the chunk staged in LDS, decoded.
+template <int DT>
+__device__ __forceinline__ float staged(const u32x4* st, int li) {
+  if constexpr (DT == F32) {
+    return __uint_as_float(reinterpret_cast<const uint32_t*>(st)[li]);
+  } else {
+    return decode_bits<DT>(reinterpret_cast<const uint16_t*>(st)[li]);
   }
 }
 
-__device__ __forceinline__ int64_t item_token(const SampParams& p, int item) {
-  if (p.k == 0) return -1;
-  const int r = item / p.nch;
-  const int g = r / p.rpg;
-  return row_token(p, g, r - g * p.rpg);
-}
-
-// Bins and candidates: bin b = min(-k, 15) counts the elements whose
-// exponent scaling in exp2q is 2^k = 2^-b (e in [2^-b / sqrt2, 2^-b * sqrt2)),
-// the last bin also everything smaller; lanes past the row end are not
-// counted. With K the number of leading bins holding at most cap entries,
-// the candidates are the e >= kCandScale * 2^-K, all inside those bins since
-// e <= kCandScale * 2^k for every k (K == kOctBins: every e > 0; K == 0: none).
-constexpr float kCandScale = 1.41422f;  // > max of exp2q's polynomial over [-1/2, 1/2]
-
-template <bool IN_ALL, int DT, int NVC>
-__device__ __forceinline__ void exp_bins(const SampParams& p, ChunkSh& cs, float (&x)[NVC * Elem<DT>::kPerVec],
-                                         int t, int nvc, float nmc) {
+// One chunk item, processed by wave w. Returns the unit id if this wave's
+// arrival completed the unit, else -1 (wave-uniform).
+template <int DT, bool PEN>
+__device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int it, const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4],
+                           uint32_t pw) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  // byte offset of this lane's bin-0 word, the step per -bin and the
-  // increment of its 16-bit half
-  const int hi = t >> 5;
-  const int hbase4 = ((t & 31) * kHistStride + (hi ? kOctBins - 1 : 0)) * 4;
-  const int hstep4 = hi ? 4 : -4;
-  const uint32_t hinc = hi ? 0x10000u : 1u;
-  char* hist0 = reinterpret_cast<char*>(&cs.hist[0]);
-#pragma unroll
-  for (int u = 0; u < NVC; ++u) {
-    const bool in = IN_ALL || u * kWave + t < nvc;
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      int ki;
-      x[u * EPV + e] = exp2q_k(__builtin_fmaf(x[u * EPV + e], p.c, nmc), &ki);
-      const int b = __builtin_elementwise_min(__builtin_elementwise_max(ki, -(kOctBins - 1)), 0);  // -bin
-      if (in)
-        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(hist0 + (hbase4 + __mul24(hstep4, b))), hinc, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-#pragma unroll
-    for (int h = 0; h < EPV / 4; ++h) {
-      const int s = (u * kWave + t) * (EPV / 4) + h;
-      const int ps = s ^ ((s >> 3) & 7);
-      f32x4 v;
-      v.x = x[u * EPV + 4 * h + 0];
-      v.y = x[u * EPV + 4 * h + 1];
-      v.z = x[u * EPV + 4 * h + 2];
-      v.w = x[u * EPV + 4 * h + 3];
-      *reinterpret_cast<f32x4*>(&cs.est[ps * 4]) = v;
-    }
-  }
-}
-
-// One chunk, processed by one wave: no workgroup barriers (the wave's LDS
-// accesses are ordered; s_barrier of a one-wave workgroup only fences).
-template <int DT, int NVC, bool PEN>
-__device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, int item, const u32x4 (&d)[NVC],
-                                              const uint32_t (&pw)[NVC], int64_t tok) {
-  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int NVC = kChunk / (kWave * EPV);
   constexpr int NE = NVC * EPV;
-  static_assert(NE == kPerLane, "32 elements per lane");
-  // lane-derived values are recomputed per item (not hoisted out of the
-  // persistent loop)
-  int t = threadIdx.x;
+  static_assert(NE == 32, "32 elements per lane");
+  int t = threadIdx.x & (kWave - 1);
   asm volatile("" : "+v"(t));
-  const int r = item / p.nch;
-  const int cj = item - r * p.nch;
-  const int c0 = cj * kChunk;
+  const Item I = item_of(p, it);
+  const int c0 = I.chunk * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
-  const bool full = nvc == NVC * kWave;  // only a row's last chunk can be partial
+  const bool full = nvc == NVC * kWave;
 
-  // 1. penalised logits (-inf past the row end) and the chunk max
+  // 1. stage the chunk as loaded
+  u32x4* st = sh.st.stage[w];
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) st[u * kWave + t] = d[u];
+
+  // 2. penalised elements of this lane's vectors (bits of the chunk's
+  //    bitmap words, which lane t loaded as word t)
+  uint32_t hb[NVC];
+  bool any_hit = false;
+  if constexpr (PEN) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      const int i0 = (u * kWave + t) * EPV;
+      const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), i0 >> 5));
+      hb[u] = (u * kWave + t < nvc) ? (word >> (i0 & 31)) & ((1u << EPV) - 1u) : 0u;
+    }
+    uint32_t a = 0;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) a |= hb[u];
+    any_hit = __ballot(a != 0) != 0;
+  } else {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) hb[u] = 0;
+  }
+
+  // 3. decoded logits, penalised ones and lanes past the row end at -inf
   float x[NE];
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
-      float l = vec_elem<DT>(d[u], e);
-      if (PEN && ((pw[u] >> ((((u * kWave + t) * EPV) & 31) + e)) & 1u)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
-      x[u * EPV + e] = l;
+      float v = vec_elem<DT>(d[u], e);
+      if constexpr (PEN) {
+        if ((hb[u] >> e) & 1u) v = -__builtin_inff();
+      }
+      x[u * EPV + e] = v;
     }
   }
   if (!full) {
@@ -377,1133 +483,1036 @@ __device__ __forceinline__ void process_chunk(const SampParams& p, ChunkSh& cs, 
       }
     }
   }
-  float mx = x[0];
-#pragma unroll
-  for (int i = 1; i < NE; ++i) mx = nmax(mx, x[i]);
-  const float m = wave_max_f32(mx);
-  const float mc = m * p.c;
-  const float nmc = -mc;
 
-  // 2. e in place, exponent bins, e-store
-  if (full) {
-    exp_bins<true, DT, NVC>(p, cs, x, t, nvc, nmc);
-  } else {
-    exp_bins<false, DT, NVC>(p, cs, x, t, nvc, nmc);
+  // 4. vector maxima and the chunk max (NaN-propagating first; a NaN chunk
+  //    is redone ignoring NaN)
+  float vm[NVC];
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) {
+    float mv = x[u * EPV];
+#pragma unroll
+    for (int e = 1; e < EPV; ++e) mv = nmax(mv, x[u * EPV + e]);
+    vm[u] = mv;
   }
-  // chunk mass: each lane's 32 e pairwise, then the lanes pairwise
-  const float mass = wave_tree_sum(lane_tree_sum(x));
-  __syncthreads();
-
-  // 3. bin totals: lane t < 32 (b = t & 15, q = t >> 4) sums word b of rows
-  //    16q..16q+15 and clears it (both 16-bit halves at once: a half sums to
-  //    at most 32 * 32); the low halves of word b count bin b of lanes 0..31,
-  //    the high halves of word 15 - b bin b of lanes 32..63
-  uint32_t bc;
-  {
-    const int b = t & (kOctBins - 1), q = (t >> 4) & 1;
-    uint32_t sb = 0;
-    if (t < kHistRows) {
+  float mx = vm[0];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        sb += __hip_atomic_exchange(&cs.hist[(16 * q + i) * kHistStride + b], 0u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int u = 1; u < NVC; ++u) mx = nmax(mx, vm[u]);
+  float m = wave_max_f32(mx);
+  if (m != m) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      float mv = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) mv = x[u * EPV + e] > mv ? x[u * EPV + e] : mv;
+      vm[u] = mv;
     }
-    sb += __shfl_xor(sb, 16);
-    const uint32_t mirror = __shfl(sb, kOctBins - 1 - b);
-    bc = t < kOctBins ? (sb & 0xffffu) + (mirror >> 16) : 0u;
-  }
-  // lane-contiguous e: elements [32t, 32t + 32) (index order within the lane)
-  float ec[kPerLane];
+    mx = vm[0];
 #pragma unroll
-  for (int q = 0; q < kPerLane / 4; ++q) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(&cs.est[(8 * t + (q ^ (t & 7))) * 4]);
-    ec[4 * q + 0] = v.x;
-    ec[4 * q + 1] = v.y;
-    ec[4 * q + 2] = v.z;
-    ec[4 * q + 3] = v.w;
+    for (int u = 1; u < NVC; ++u) mx = mx > vm[u] ? mx : vm[u];
+    m = wave_max_f32(mx);
   }
-  const bool has_tok = tok >= c0 && tok < c0 + nel;
-  float e_tok = 0.0f;
-  if (has_tok) e_tok = cs.est[est_index(static_cast<int>(tok - c0))];
+  const float c = p.c;
+  const float mc = m * c;
 
-  // 4. K: the number of leading exponent bins holding at most cap entries
-  const uint32_t binc = wave_scan_add_u32(bc);
-  const int K = __builtin_popcountll(__ballot(t < kOctBins && binc <= static_cast<uint32_t>(p.cap)));
-  const float th = K >= kOctBins ? __uint_as_float(1u) : (K == 0 ? __builtin_inff() : __builtin_ldexpf(kCandScale, -K));
-  // 5. candidate mask (bit 31 - i <-> element 32t + i), offsets
-  uint32_t mask = 0;
+  // 5. penalised sub-chunk: max of the penalised logits
+  float pm = -__builtin_inff();
+  if constexpr (PEN) {
+    if (any_hit) {
+      float lm = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
-    // mask = 2 mask + (ec[i] >= th): a compare into VCC and one add with carry
-    asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc" : "+v"(mask) : "v"(ec[i]), "v"(th) : "vcc");
+      for (int u = 0; u < NVC; ++u) {
+        uint32_t bits = hb[u];
+        while (bits) {
+          const int e = __builtin_ctz(bits);
+          bits &= bits - 1u;
+          const float xp = penalise(staged<DT>(st, (u * kWave + t) * EPV + e), p.pen);
+          lm = xp > lm ? xp : lm;
+        }
+      }
+      pm = wave_max_f32(lm);
+    }
   }
-  const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(mask));
-  const uint32_t incl = wave_scan_add_u32(cnt);
-  const uint32_t total = lane_bcast_u32(incl, kWave - 1);
-  uint32_t pos = incl - cnt;
-  // 6. candidates, in index order
-  uint64_t* out = p.cands + (static_cast<int64_t>(r) * p.nch + cj) * kChunkCand;
-  const uint32_t ibase = static_cast<uint32_t>(c0 + kPerLane * t);
-  while (mask) {
-    const int i = __builtin_clz(mask);
-    const uint32_t eb = __float_as_uint(cs.est[(8 * t + ((i >> 2) ^ (t & 7))) * 4 + (i & 3)]);
-    out[pos] = (static_cast<uint64_t>(ibase + static_cast<uint32_t>(i)) << 32) | eb;
-    ++pos;
-    mask &= 0x7fffffffu >> i;
+  const float pmc = pm * c;
+
+  // 6. e and the chunk mass (e replaces x)
+  const float nmc = -mc;
+#pragma unroll
+  for (int i = 0; i < NE; ++i) x[i] = exp2q(__builtin_fmaf(x[i], c, nmc));
+  float ea[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) ea[i] = x[i];
+  const float mass = wave_tree_sum(lane_tree_sum(ea));
+
+  // 7. the level L: candidates are the e >= 2^-L relative to mref = max(mc, pmc)
+  const float mref = mc > pmc ? mc : pmc;
+  const bool same = mref == mc && mc > -__builtin_inff();
+  const int cap = p.cap;
+  int L = -1;
+  uint32_t mask = 0;  // bit 31 - i <-> element i (A elements)
+  uint32_t cnt = 0;
+  if (mref > -__builtin_inff()) {
+    // a start from the vector maxima: the largest L in [0, kMaxLevel] at
+    // which at most cap of the lane vectors hold a candidate (binary search;
+    // the count only grows with L)
+    const float nref = -mref;
+    float tv[NVC];
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) tv[u] = __builtin_fmaf(vm[u], c, nref);
+    int lo = 0, hi = kMaxLevel;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      const float th = -static_cast<float>(mid);
+      uint32_t nv = 0;
+#pragma unroll
+      for (int u = 0; u < NVC; ++u) nv += __builtin_popcountll(__ballot(tv[u] >= th));
+      if (nv <= static_cast<uint32_t>(cap)) lo = mid; else hi = mid - 1;
+    }
+    const int Ls = lo;
+    for (L = Ls; L >= 0; --L) {
+      mask = 0;
+      if (same) {
+        const float th = __builtin_ldexpf(1.0f, -L);
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          // mask = 2 mask + (e >= th): a compare into VCC and one add with carry
+          asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
+              : "+v"(mask) : "v"(x[i]), "v"(th) : "vcc");
+        }
+      } else {
+        // the penalised maximum lies above the rest (a penalty below 1, or
+        // no other finite logit): test the exponent against mref directly
+        const float th = -static_cast<float>(L);
+#pragma unroll
+        for (int u = 0; u < NVC; ++u) {
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) {
+            float v = vec_elem<DT>(d[u], e);
+            if (((hb[u] >> e) & 1u) || (!full && u * kWave + t >= nvc)) v = -__builtin_inff();
+            mask = 2u * mask + (__builtin_fmaf(v, c, nref) >= th ? 1u : 0u);
+          }
+        }
+      }
+      cnt = static_cast<uint32_t>(__builtin_popcount(mask));
+      const uint32_t tot = wave_sum_u64(cnt);
+      if (tot <= static_cast<uint32_t>(cap)) {
+        cnt = tot;
+        break;
+      }
+    }
+    if (L < 0) {
+      mask = 0;
+      cnt = 0;
+    }
   }
+
+  // 8. A candidates, lane-major order: (chunk index << 32 | bits(x))
+  uint64_t* out = p.cands + (static_cast<int64_t>(I.row) * p.nch + I.chunk) * p.cap;
+  uint32_t nA = 0;
+  if (L >= 0) {
+    const uint32_t own = static_cast<uint32_t>(__builtin_popcount(mask));
+    const uint32_t incl = wave_scan_add_u32(own);
+    nA = lane_bcast_u32(incl, kWave - 1);
+    uint32_t pos = incl - own;
+    while (mask) {
+      const int i = __builtin_clz(mask);
+      mask &= ~(0x80000000u >> i);
+      const int li = ((i / EPV) * kWave + t) * EPV + (i % EPV);
+      const float xv = staged<DT>(st, li);
+      store_sc64(out + pos, (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv));
+      ++pos;
+    }
+  }
+
+  // 9. penalised sub-chunk: its mass (lane-sequential in (u, element) order,
+  //    then the lanes pairwise) and its candidates (appended, any order)
+  float pmass = 0.0f;
+  bool overflow = L < 0 && mref > -__builtin_inff();
+  if constexpr (PEN) {
+    if (any_hit) {
+      if (t == 0) sh.pcount[w] = 0;
+      const float npmc = -pmc;
+      const float nref = -mref;
+      const float th = -static_cast<float>(L);
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NVC; ++u) {
+        uint32_t bits = hb[u];
+        while (bits) {
+          const int e = __builtin_ctz(bits);
+          bits &= bits - 1u;
+          const int li = (u * kWave + t) * EPV + e;
+          const float xp = penalise(staged<DT>(st, li), p.pen);
+          acc = acc + exp2q(__builtin_fmaf(xp, c, npmc));
+          if (L >= 0 && __builtin_fmaf(xp, c, nref) >= th) {
+            const uint32_t q = __hip_atomic_fetch_add(&sh.pcount[w], 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (nA + q < static_cast<uint32_t>(cap))
+              store_sc64(out + nA + q, (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp));
+          }
+        }
+      }
+      pmass = wave_tree_sum(acc);
+      const uint32_t nB = __hip_atomic_load(&sh.pcount[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (nA + nB > static_cast<uint32_t>(cap)) overflow = true;
+      nA += nB;
+    }
+  }
+
+  // 10. the row's draft token, processed
+  float xtok = 0.0f;
+  const bool has_tok = I.tok >= c0 && I.tok < c0 + nel;
+  if (has_tok) {
+    const int li = static_cast<int>(I.tok - c0);
+    float xv = staged<DT>(st, li);
+    if constexpr (PEN) {
+      const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), li >> 5));
+      if ((word >> (li & 31)) & 1u) xv = penalise(xv, p.pen);
+    }
+    xtok = xv;
+  }
+
+  // 11. the record, then drain every store and arrive on the unit
   if (t == 0) {
-    ChunkRec rec;
-    rec.mc = mc;
-    rec.K = K;
-    rec.n = total;
-    rec.flags = (K >= kOctBins ? kChunkComplete : 0u) | (has_tok ? kChunkHasTok : 0u);
-    rec.mass = mass;
-    rec.e_tok = e_tok;
-    rec.pad0 = rec.pad1 = 0;
-    p.chunks[static_cast<int64_t>(r) * p.nch + cj] = rec;
+    ChunkRec* rec = p.recs + static_cast<int64_t>(I.row) * p.nch + I.chunk;
+    uint64_t* r64 = reinterpret_cast<uint64_t*>(rec);
+    const uint32_t flags = (overflow ? kChunkOverflow : 0u) | (has_tok ? kChunkHasTok : 0u);
+    store_sc64(r64 + 0, pack_u32(__float_as_uint(m), __float_as_uint(mass)));
+    store_sc64(r64 + 1, pack_u32(__float_as_uint(pm), __float_as_uint(pmass)));
+    store_sc64(r64 + 2, pack_u32(static_cast<uint32_t>(overflow ? -1 : L), overflow ? 0u : nA));
+    store_sc64(r64 + 3, pack_u32(__float_as_uint(xtok), flags));
   }
-  __syncthreads();  // the e-store and bins are rewritten by the next item
+  drain_stores();
+  int done = -1;
+  if (t == 0) {
+    const uint32_t old = atomic_arrive(p.unit_cnt + I.unit);
+    if (old + 1u == static_cast<uint32_t>(unit_items(p, I.unit))) done = I.unit;
+  }
+  return __shfl(done, 0);
 }
 
-// Persistent over (row, chunk) items in row-major order, double-buffered: the
-// next item's loads are in flight while the current one is processed.
-template <int DT, bool PEN>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(kChunkWavesPerCu / 4)))
-void chunk_kernel(const SampParams p) {
-  constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int NVC = kChunk / (kWave * EPV);  // vectors per lane: 8 (f32) or 4
-  __shared__ ChunkSh cs;
-  const int t = threadIdx.x;
-  for (int i = t; i < kHistRows * kHistStride; i += kWave) cs.hist[i] = 0u;
+// ===========================================================================
+// Finaliser
+// ===========================================================================
+
+// Block-wide inclusive scan of one u64 per thread; tot receives the total.
+// red must not be in use by another scan still being read (callers alternate
+// between two buffers).
+__device__ __forceinline__ uint64_t block_incl_scan(uint64_t v, uint64_t* red, uint64_t* tot) {
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const uint64_t inc = wave_scan_add_u64(v);
+  if (lane == kWave - 1) red[wid] = inc;
   __syncthreads();
-  int item = blockIdx.x;
-  if (item >= p.items) return;
-  u32x4 cur[NVC], nxt[NVC];
-  uint32_t pcur[NVC] = {}, pnxt[NVC] = {};
-  load_chunk<DT, NVC>(p, item, cur, pcur);
-  int64_t tcur = item_token(p, item), tnxt = -1;
-  while (true) {
-    const int next = item + static_cast<int>(gridDim.x);
-    if (next < p.items) {
-      load_chunk<DT, NVC>(p, next, nxt, pnxt);
-      tnxt = item_token(p, next);
+  uint64_t base = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < kNW; ++i) {
+    const uint64_t x = red[i];
+    base += i < wid ? x : 0;
+    all += x;
+  }
+  *tot = all;
+  return base + inc;
+}
+
+__device__ __forceinline__ uint64_t block_sum(uint64_t v, uint64_t* red) {
+  uint64_t tot;
+  block_incl_scan(v, red, &tot);
+  return tot;
+}
+
+// Row constants and per-chunk data of row slot s from the unit's records;
+// wave s runs it (lane l holds chunks 2l and 2l+1).
+__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, int row) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int nch = p.nch;
+  const float c = p.c;
+  ChunkRec ra{}, rb{};
+  const int ja = 2 * lane, jb = ja + 1;
+  const bool ia = ja < nch, ib = jb < nch;
+  const uint64_t* base = reinterpret_cast<const uint64_t*>(p.recs + static_cast<int64_t>(row) * nch);
+  uint64_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0};
+  if (ia) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wa[q] = load_sc64(base + 4 * ja + q);
+  }
+  if (ib) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wb[q] = load_sc64(base + 4 * jb + q);
+  }
+  __builtin_memcpy(&ra, wa, 32);
+  __builtin_memcpy(&rb, wb, 32);
+  const float ninf = -__builtin_inff();
+  const float mca = ia ? ra.m * c : ninf, pmca = ia ? ra.pm * c : ninf;
+  const float mcb = ib ? rb.m * c : ninf, pmcb = ib ? rb.pm * c : ninf;
+  float lm = mca;
+  lm = pmca > lm ? pmca : lm;
+  lm = mcb > lm ? mcb : lm;
+  lm = pmcb > lm ? pmcb : lm;
+  const float mcmax = wave_max_f32(lm);
+  // slots 4l..4l+3 = (A, B) of chunks 2l and 2l+1: the first two pairwise
+  // levels of the normaliser's sum
+  const float sa = ia ? exp2q(mca - mcmax) * ra.mass : 0.0f;
+  const float sb = ia ? exp2q(pmca - mcmax) * ra.pmass : 0.0f;
+  const float sc = ib ? exp2q(mcb - mcmax) * rb.mass : 0.0f;
+  const float sd = ib ? exp2q(pmcb - mcmax) * rb.pmass : 0.0f;
+  const float S = wave_tree_sum((sa + sb) + (sc + sd));
+  // largest p of a non-candidate: candidates are RN32(x c - mref) >= -L, so
+  // every other x has x c < mref - L and p(x) <= p at the exponent
+  // (mref - L) cd / c - mcmax, rounded up
+  auto bound = [&](const ChunkRec& r, float mcj, float pmcj) -> float {
+    if (r.flags & kChunkOverflow) return __builtin_inff();
+    const float mref = mcj > pmcj ? mcj : pmcj;
+    if (!(mref > ninf) || !(S > 0.0f)) return 0.0f;
+    const double a = static_cast<double>(mref) - static_cast<double>(r.level);
+    const double tb = a * (p.cd / static_cast<double>(c)) - static_cast<double>(mcmax);
+    const float tf = next_up(static_cast<float>(tb));
+    return exp2p(tf) / S;
+  };
+  const float ba = ia ? bound(ra, mca, pmca) : 0.0f;
+  const float bb = ib ? bound(rb, mcb, pmcb) : 0.0f;
+  // counts read back from the workspace never exceed the chunk's slots
+  const uint32_t capu = static_cast<uint32_t>(p.cap);
+  const uint32_t na = ia ? (ra.n < capu ? ra.n : capu) : 0u, nb = ib ? (rb.n < capu ? rb.n : capu) : 0u;
+  const uint32_t own = na + nb;
+  const uint32_t incl = wave_scan_add_u32(own);
+  if (ia) {
+    f.bound[s][ja] = ba;
+    f.cstart[s][ja] = incl - own;
+    f.ccount[s][ja] = na;
+  }
+  if (ib) {
+    f.bound[s][jb] = bb;
+    f.cstart[s][jb] = incl - own + na;
+    f.ccount[s][jb] = nb;
+  }
+  const float bmax = wave_max_f32(ba > bb ? ba : bb);
+  const bool ta = ia && (ra.flags & kChunkHasTok), tb2 = ib && (rb.flags & kChunkHasTok);
+  const uint64_t tk = __ballot(ta || tb2);
+  float xt = ta ? ra.xtok : (tb2 ? rb.xtok : 0.0f);
+  const int tl = tk ? __builtin_ctzll(tk) : 0;
+  xt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(xt), tl));
+  if (lane == 0) {
+    RowAux& a = f.aux[s];
+    a.mcmax = mcmax;
+    a.s = S;
+    a.bmax = bmax;
+    a.n = lane_bcast_u32(incl, kWave - 1);
+    a.has_tok = tk != 0;
+    a.xtok = xt;
+    a.flags = S > 0.0f ? 0u : kRowEmpty;
+    a.cut = 0.0f;
+    a.mass_f = 1.0f;
+    a.mass_fx = 0;
+  } else {
+    (void)lane_bcast_u32(incl, kWave - 1);
+  }
+}
+
+// Candidates of row slot s into the LDS entries (p bits, index).
+__device__ __forceinline__ void load_entries(const Params& p, FinSh& f, int s, int row, const RowK& K) {
+  const int t = threadIdx.x;
+  const uint32_t n = f.aux[s].n;
+  const int nch = p.nch;
+  const uint64_t* cb = p.cands + static_cast<int64_t>(row) * nch * p.cap;
+  for (uint32_t e = t; e < n; e += kWG) {
+    // the chunk holding entry e: the last j with cstart[j] <= e
+    int lo = 0, hi = nch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (f.cstart[s][mid] <= e) lo = mid; else hi = mid - 1;
     }
-    process_chunk<DT, NVC, PEN>(p, cs, item, cur, pcur, tcur);
-    if (next >= p.items) break;
-    // register moves (the empty asm keeps the copy from becoming a memcpy of
-    // the arrays, which would put them in scratch)
+    const uint64_t v = load_sc64(cb + static_cast<int64_t>(lo) * p.cap + (e - f.cstart[s][lo]));
+    const float x = __uint_as_float(static_cast<uint32_t>(v));
+    const uint32_t idx = static_cast<uint32_t>(v >> 32);
+    const bool ok = idx < static_cast<uint32_t>(p.vocab);  // always, for a well-formed workspace
+    f.ent[s].pbits[e] = ok ? __float_as_uint(pval(K, x)) : 0u;
+    f.ent[s].eidx[e] = ok ? idx : 0u;
+  }
+}
+
+// Exact top-p cutoff over the LDS entries of slot s: c = max{v : sum over
+// entries with p >= v of fx46(p) >= thr}, by three radix rounds on the bits of
+// p (10 bits each; p <= 1, so bits >> 20 < 1024). Returns false when the
+// entries hold less than thr. Uses f.u.bins.
+__device__ __forceinline__ bool select_entries(FinSh& f, int s, uint64_t thr, float* cut, uint64_t* mass) {
+  const int t = threadIdx.x;
+  const uint32_t n = f.aux[s].n;
+  uint32_t prefix = 0;
+  uint64_t above = 0;
+  constexpr int kPer = kBins / kWG;  // bins per thread
+  for (int round = 0; round < 3; ++round) {
+    const int shift = 20 - round * kRadixBits;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) f.u.bins[kPer * t + q] = 0;
+    __syncthreads();
+    for (uint32_t e = t; e < n; e += kWG) {
+      const uint32_t b = f.ent[s].pbits[e];
+      if ((b >> (shift + kRadixBits)) == prefix) {
+        __hip_atomic_fetch_add(&f.u.bins[(b >> shift) & (kBins - 1)], fx46(__uint_as_float(b)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    __syncthreads();
+    // thread t holds the bins of digits 4(255 - t) .. +3: its inclusive scan is
+    // the mass at digits >= 4(255 - t)
+    const int g0 = kPer * (kWG - 1 - t);
+    uint64_t own = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) own += f.u.bins[g0 + q];
+    uint64_t tot;
+    const uint64_t incl = block_incl_scan(own, f.red + (round & 1) * kNW, &tot);
+    const uint64_t need = thr > above ? thr - above : 0;
+    if (t == 0) f.sel[0] = kNone;
+    __syncthreads();
+    if (incl >= need && incl - own < need) {
+      // the crossing digit inside this thread's group, from the top
+      uint64_t acc = incl - own;
+      int d = g0;
+      for (int q = kPer - 1; q >= 0; --q) {
+        acc += f.u.bins[g0 + q];
+        if (acc >= need) {
+          d = g0 + q;
+          acc -= f.u.bins[g0 + q];
+          break;
+        }
+      }
+      f.sel[0] = static_cast<uint32_t>(d);
+      f.sel64[0] = above + acc;  // mass strictly above digit d
+      f.sel64[1] = f.u.bins[d];
+    }
+    __syncthreads();
+    const uint32_t d = f.sel[0];
+    if (d == kNone) return false;
+    above = f.sel64[0];
+    prefix = (prefix << kRadixBits) | d;
+    if (round == 2) {
+      *cut = __uint_as_float(prefix);
+      *mass = above + f.sel64[1];
+    }
+    __syncthreads();
+  }
+  return true;
+}
+
+// Passes over a whole row for the slow path: fn(index, x) for every element,
+// 16-byte vectors spread over the workgroup.
+template <int DT, typename Fn>
+__device__ __forceinline__ void row_pass(const Params& p, const char* rowp, const uint32_t* bm, int64_t i0, int64_t i1,
+                                         Fn fn) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  const u32x4* src = reinterpret_cast<const u32x4*>(rowp);
+  for (int64_t v = i0 / EPV + threadIdx.x; v < i1 / EPV; v += kWG) {
+    const u32x4 d = src[v];
+    uint32_t word = bm ? bm[(v * EPV) >> 5] : 0u;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t i = v * EPV + e;
+      float x = vec_elem<DT>(d, e);
+      if (bm && ((word >> (i & 31)) & 1u)) x = penalise(x, p.pen);
+      fn(i, x);
+    }
+  }
+}
+
+// Whole-row exact cutoff by three radix passes over the row (slow path).
+template <int DT>
+__device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, const RowK& K, uint64_t thr, float* cut, uint64_t* mass) {
+  const int t = threadIdx.x;
+  const char* rowp = row_ptr(p, row);
+  const uint32_t* bm = row_bitmap(p, row);
+  uint32_t prefix = 0;
+  uint64_t above = 0;
+  constexpr int kPer = kBins / kWG;
+  for (int round = 0; round < 3; ++round) {
+    const int shift = 20 - round * kRadixBits;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) f.u.bins[kPer * t + q] = 0;
+    __syncthreads();
+    row_pass<DT>(p, rowp, bm, 0, p.vocab, [&](int64_t, float x) {
+      const uint32_t b = __float_as_uint(pval(K, x));
+      if ((b >> (shift + kRadixBits)) == prefix)
+        __hip_atomic_fetch_add(&f.u.bins[(b >> shift) & (kBins - 1)], fx46(__uint_as_float(b)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    });
+    __syncthreads();
+    const int g0 = kPer * (kWG - 1 - t);
+    uint64_t own = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) own += f.u.bins[g0 + q];
+    uint64_t tot;
+    const uint64_t incl = block_incl_scan(own, f.red + (round & 1) * kNW, &tot);
+    const uint64_t need = thr > above ? thr - above : 0;
+    if (t == 0) f.sel[0] = kNone;
+    __syncthreads();
+    if (incl >= need && incl - own < need) {
+      uint64_t acc = incl - own;
+      int d = g0;
+      for (int q = kPer - 1; q >= 0; --q) {
+        acc += f.u.bins[g0 + q];
+        if (acc >= need) {
+          d = g0 + q;
+          acc -= f.u.bins[g0 + q];
+          break;
+        }
+      }
+      f.sel[0] = static_cast<uint32_t>(d);
+      f.sel64[0] = above + acc;
+      f.sel64[1] = f.u.bins[d];
+    }
+    __syncthreads();
+    const uint32_t d = f.sel[0];
+    if (d == kNone) {
+      // the row holds less than thr: the reference clamps to the last sorted
+      // value, the row minimum, and keeps everything
+      if (round != 0) return false;  // cannot happen: later rounds include the crossing
+      float mn = __builtin_inff();
+      row_pass<DT>(p, rowp, bm, 0, p.vocab, [&](int64_t, float x) {
+        const float v = pval(K, x);
+        mn = v < mn ? v : mn;
+      });
+      uint64_t key = static_cast<uint64_t>(__float_as_uint(mn));
+      key = ~block_max_u64<kWG>(~key, f.red2);  // min via max of complements
+      __syncthreads();
+      *cut = __uint_as_float(static_cast<uint32_t>(key));
+      *mass = tot;
+      return true;
+    }
+    above = f.sel64[0];
+    prefix = (prefix << kRadixBits) | d;
+    if (round == 2) {
+      *cut = __uint_as_float(prefix);
+      *mass = above + f.sel64[1];
+    }
+    __syncthreads();
+  }
+  return true;
+}
+
+// Appends the elements of chunk j with p >= cut to slot s's entries, in
+// index order, as the chunk's new range. Returns false if they do not fit.
+template <int DT>
+__device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, int row, const RowK& K, int j, float cut) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int EPT = kChunk / kWG;  // elements per thread, contiguous
+  const int t = threadIdx.x;
+  const char* rowp = row_ptr(p, row);
+  const uint32_t* bm = row_bitmap(p, row);
+  const int64_t c0 = static_cast<int64_t>(j) * kChunk;
+  const int64_t nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
+  float pv[EPT];
+  uint32_t keep = 0;
+#pragma unroll
+  for (int q = 0; q < EPT / EPV; ++q) {
+    const int64_t i0 = c0 + static_cast<int64_t>(t) * EPT + q * EPV;
+    u32x4 d{0, 0, 0, 0};
+    if (i0 < c0 + nel) d = reinterpret_cast<const u32x4*>(rowp)[i0 / EPV];
+    const uint32_t word = (bm && i0 < c0 + nel) ? bm[i0 >> 5] : 0u;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t i = i0 + e;
+      float v = 0.0f;
+      if (i < c0 + nel) {
+        float x = vec_elem<DT>(d, e);
+        if (bm && ((word >> (i & 31)) & 1u)) x = penalise(x, p.pen);
+        v = pval(K, x);
+      }
+      pv[q * EPV + e] = v;
+      if (i < c0 + nel && v >= cut) keep |= 1u << (q * EPV + e);
+    }
+  }
+  const uint32_t own = static_cast<uint32_t>(__builtin_popcount(keep));
+  uint64_t tot;
+  const uint64_t incl = block_incl_scan(own, f.red, &tot);
+  const uint32_t base = f.aux[s].n;
+  if (base + tot > static_cast<uint64_t>(kRowCap)) {
+    __syncthreads();
+    return false;
+  }
+  uint32_t pos = base + static_cast<uint32_t>(incl) - own;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    if ((keep >> i) & 1u) {
+      f.ent[s].pbits[pos] = __float_as_uint(pv[i]);
+      f.ent[s].eidx[pos] = static_cast<uint32_t>(c0 + static_cast<int64_t>(t) * EPT + i);
+      ++pos;
+    }
+  }
+  // the chunk's old entries drop out of the select (p = 0 cannot reach the cutoff)
+  const uint32_t os = f.cstart[s][j], oc = f.ccount[s][j];
+  for (uint32_t e = os + t; e < os + oc; e += kWG) f.ent[s].pbits[e] = 0u;
+  __syncthreads();
+  if (t == 0) {
+    f.cstart[s][j] = base;
+    f.ccount[s][j] = static_cast<uint32_t>(tot);
+    f.aux[s].n = base + static_cast<uint32_t>(tot);
+    f.bound[s][j] = 0.0f;
+  }
+  __syncthreads();
+  return true;
+}
+
+// Collects the whole support {p >= cut} of a row into slot s's entries,
+// chunk by chunk (slow path); false if it does not fit.
+template <int DT>
+__device__ __forceinline__ bool collect_support(const Params& p, FinSh& f, int s, int row, const RowK& K, float cut) {
+  if (threadIdx.x == 0) f.aux[s].n = 0;
+  __syncthreads();
+  for (int j = 0; j < p.nch; ++j) {
+    if (threadIdx.x == 0) {
+      f.cstart[s][j] = f.aux[s].n;
+      f.ccount[s][j] = 0;
+    }
+    __syncthreads();
+    if (!refill_chunk<DT>(p, f, s, row, K, j, cut)) return false;
+  }
+  return true;
+}
+
+// Resolves the cutoff of row slot s: list mode (kRowList: the support is in
+// the LDS entries) or dense (the support is {p >= cut} of the whole row).
+template <int DT>
+__device__ __forceinline__ void resolve_row(const Params& p, FinSh& f, int s, int row, const RowK& K) {
+  RowAux& a = f.aux[s];
+  const float top_p = row_top_p(p, row);
+  const uint32_t empty = a.flags & kRowEmpty;
+  if (top_p >= 1.0f || empty) {
+    // unfiltered: P = p over the whole row (an empty row has p = 0 everywhere)
+    if (threadIdx.x == 0) {
+      a.flags = empty;
+      a.cut = 0.0f;
+      a.mass_f = 1.0f;
+      a.top_p = top_p;
+    }
+    __syncthreads();
+    return;
+  }
+  const uint64_t thr = fx46(top_p);
+  float cut = 0.0f;
+  uint64_t mass = 0;
+  bool ok = select_entries(f, s, thr, &cut, &mass);
+  uint32_t flags = kRowFiltered | kRowList;
+  if (ok && !(cut > a.bmax)) {
+    // re-read the chunks whose non-candidates may reach the cutoff
+    flags |= kRowRefilled;
+    for (int j = 0; j < p.nch && ok; ++j) {
+      if (f.bound[s][j] >= cut) ok = refill_chunk<DT>(p, f, s, row, K, j, cut);
+    }
+    if (ok) ok = select_entries(f, s, thr, &cut, &mass);
+  }
+  if (!ok) {
+    flags = kRowFiltered | kRowSlow;
+    select_row<DT>(p, f, row, K, thr, &cut, &mass);
+    if (collect_support<DT>(p, f, s, row, K, cut)) flags |= kRowList;
+  }
+  if (threadIdx.x == 0) {
+    a.flags = flags;
+    a.cut = cut;
+    a.mass_fx = mass;
+    a.mass_f = mass_to_f32(mass);
+    a.top_p = top_p;
+  }
+  __syncthreads();
+}
+
+// Filtered probability of a row at p (P = p when unfiltered).
+__device__ __forceinline__ float filtered_of(const RowAux& a, float pv) {
+  if (!(a.flags & kRowFiltered)) return pv;
+  if (a.mass_fx == 0) return 0.0f;
+  return pv >= a.cut ? pv / a.mass_f : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Draws: the first index j (in vocabulary order) with
+// sum_{i <= j} W_i > floor(u * sum W), W_i = fx46 of the normalised weight;
+// index 0 at zero total (categorical_pick).
+// ---------------------------------------------------------------------------
+
+// Chunk j* holding the target, from f.u.csum: lane l of wave 0 holds chunks
+// 2l and 2l+1. Writes f.sel64[0] = target - mass before j*, f.sel[0] = j*
+// (kNone at zero total). Ends with a barrier.
+__device__ __forceinline__ void pick_chunk(const Params& p, FinSh& f, float u) {
+  const int t = threadIdx.x;
+  if (t < kWave) {
+    const int ja = 2 * t, jb = ja + 1;
+    const uint64_t a = ja < p.nch ? f.u.csum[ja] : 0, b = jb < p.nch ? f.u.csum[jb] : 0;
+    const uint64_t incl = wave_scan_add_u64(a + b);
+    const uint64_t total = lane_bcast_u64(incl, kWave - 1);
+    const uint64_t target = floor_u_times(u, total);
+    const uint64_t ex = incl - a - b;
+    // the first chunk whose inclusive mass exceeds the target
+    const bool in_a = ja < p.nch && ex <= target && ex + a > target;
+    const bool in_b = jb < p.nch && ex + a <= target && ex + a + b > target;
+    if (total == 0) {
+      if (t == 0) f.sel[0] = kNone;
+    } else if (in_a) {
+      f.sel[0] = static_cast<uint32_t>(ja);
+      f.sel64[0] = target - ex;
+    } else if (in_b) {
+      f.sel[0] = static_cast<uint32_t>(jb);
+      f.sel64[0] = target - ex - a;
+    }
+  }
+  __syncthreads();
+}
+
+// Within a chunk of 2048 positions: thread t owns positions 8t..8t+7 with
+// weights w[0..7]; the first position whose inclusive mass exceeds `rem`
+// (the target minus the mass before the chunk) goes to f.token as c0 + pos.
+__device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64_t (&w)[8], uint64_t rem) {
+  const int t = threadIdx.x;
+  uint64_t own = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) own += w[q];
+  uint64_t tot;
+  const uint64_t incl = block_incl_scan(own, f.red, &tot);
+  const uint64_t ex = incl - own;
+  if (ex <= rem && incl > rem) {
+    uint64_t acc = ex;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (acc + w[q] > rem) {
+        f.token = c0 + 8 * t + q;
+        break;
+      }
+      acc += w[q];
+    }
+  }
+  __syncthreads();
+}
+
+// List-mode draw over slot 0's entries with weights wts[e] (u64, held in the
+// slot-1 region); the entries of chunk j are f.cstart/ccount[0][j].
+__device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t* wts, float u) {
+  const int t = threadIdx.x;
+  const uint32_t n = f.aux[0].n;
+  for (int j = t; j < p.nch; j += kWG) f.u.csum[j] = 0;
+  if (t == 0) f.token = 0;
+  __syncthreads();
+  for (uint32_t e = t; e < n; e += kWG) {
+    const uint64_t w = wts[e];
+    if (w) __hip_atomic_fetch_add(&f.u.csum[f.ent[0].eidx[e] >> 11], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  pick_chunk(p, f, u);
+  const uint32_t js = f.sel[0];
+  if (js == kNone) return 0;
+  const uint64_t rem = f.sel64[0];
+  const uint32_t s0 = f.cstart[0][js], sc = f.ccount[0][js];
+  const int64_t c0 = static_cast<int64_t>(js) * kChunk;
+  // thread t gathers the weights of the chunk's positions 8t..8t+7
+  uint64_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (uint32_t e = s0; e < s0 + sc; ++e) {
+    const int pos = static_cast<int>(f.ent[0].eidx[e] - c0);
+    const uint64_t we = wts[e];
+    if ((pos >> 3) == t) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) w[q] += (pos & 7) == q ? we : 0;
+    }
+  }
+  pick_in_chunk(f, c0, w, rem);
+  return f.token;
+}
+
+// Dense-mode draw over the whole vocabulary with weights wfn(i) (slow path).
+template <int DT, typename WFn>
+__device__ __forceinline__ int64_t draw_dense(const Params& p, FinSh& f, const char* rowp, const uint32_t* bm, float u, WFn wfn) {
+  const int t = threadIdx.x;
+  for (int j = t; j < p.nch; j += kWG) f.u.csum[j] = 0;
+  if (t == 0) f.token = 0;
+  __syncthreads();
+  row_pass<DT>(p, rowp, bm, 0, p.vocab, [&](int64_t i, float x) {
+    const uint64_t w = wfn(i, x);
+    if (w) __hip_atomic_fetch_add(&f.u.csum[i >> 11], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  });
+  __syncthreads();
+  pick_chunk(p, f, u);
+  const uint32_t js = f.sel[0];
+  if (js == kNone) return 0;
+  const int64_t c0 = static_cast<int64_t>(js) * kChunk;
+  uint64_t w[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int64_t i = c0 + 8 * t + q;
+    w[q] = i < p.vocab ? wfn(i, load_x<DT>(p, rowp, bm, i)) : 0;
+  }
+  pick_in_chunk(f, c0, w, f.sel64[0]);
+  return f.token;
+}
+
+// Filtered draft probability Q at vocabulary index x (slot 1).
+template <int DT>
+__device__ __forceinline__ float q_at(const Params& p, const FinSh& f, const RowK& K1, int row1, uint32_t x) {
+  const RowAux& a = f.aux[1];
+  if (a.flags & kRowEmpty) return 0.0f;
+  if (a.flags & kRowList) {
+    const int j = static_cast<int>(x >> 11);
+    const uint32_t s0 = f.cstart[1][j], sc = f.ccount[1][j];
+    for (uint32_t e = s0; e < s0 + sc; ++e) {
+      if (f.ent[1].eidx[e] == x) return filtered_of(a, __uint_as_float(f.ent[1].pbits[e]));
+    }
+    return 0.0f;  // every draft element with q >= its cutoff is an entry
+  }
+  return filtered_of(a, pval(K1, load_x<DT>(p, row_ptr(p, row1), row_bitmap(p, row1), x)));
+}
+
+// Draw from slot 0's filtered distribution P (bonus / sample).
+template <int DT>
+__device__ __forceinline__ int64_t draw_target(const Params& p, FinSh& f, int row0, const RowK& K0, float u) {
+  const RowAux& a = f.aux[0];
+  if (a.flags & kRowList) {
+    uint64_t* wts = reinterpret_cast<uint64_t*>(&f.ent[1]);
+    uint64_t wl[kRowCap / kWG];
+    const uint32_t n = a.n;
+#pragma unroll
+    for (int q = 0; q < kRowCap / kWG; ++q) {
+      const uint32_t e = threadIdx.x + q * kWG;
+      wl[q] = e < n ? fx46(filtered_of(a, __uint_as_float(f.ent[0].pbits[e]))) : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kRowCap / kWG; ++q) wts[threadIdx.x + q * kWG] = wl[q];
+    __syncthreads();
+    return draw_list(p, f, wts, u);
+  }
+  return draw_dense<DT>(p, f, row_ptr(p, row0), row_bitmap(p, row0), u,
+                        [&](int64_t, float x) { return fx46(filtered_of(a, pval(K0, x))); });
+}
+
+// Residual draw at a rejected position: normalize(max(P - Q, 0)), falling
+// back to normalize(P) at zero mass (rejection.py:60-69).
+template <int DT>
+__device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int row0, int row1, const RowK& K0, const RowK& K1,
+                                 float u) {
+  const int t = threadIdx.x;
+  const RowAux& a = f.aux[0];
+  if (a.flags & kRowList) {
+    constexpr int kPer = kRowCap / kWG;
+    const uint32_t n = a.n;
+    float dl[kPer], pl[kPer];
+    uint64_t dsum = 0, psum = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const uint32_t e = t + q * kWG;
+      float P = 0.0f, d = 0.0f;
+      if (e < n) {
+        P = filtered_of(a, __uint_as_float(f.ent[0].pbits[e]));
+        if (P > 0.0f) {
+          const float Q = q_at<DT>(p, f, K1, row1, f.ent[0].eidx[e]);
+          d = P - Q;
+          d = d > 0.0f ? d : 0.0f;
+        }
+      }
+      dl[q] = d;
+      pl[q] = P;
+      dsum += fx46(d);
+      psum += fx46(P);
+    }
+    const uint64_t dtot = block_sum(dsum, f.red);
+    const uint64_t ptot = block_sum(psum, f.red2);
+    float den;
+    bool use_d = dtot > 0;
+    if (use_d) {
+      den = mass_to_f32(dtot);
+    } else {
+      den = ptot > 0 ? mass_to_f32(ptot) : 1.0f;
+    }
+    uint64_t wl[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) wl[q] = fx46((use_d ? dl[q] : pl[q]) / den);
+    __syncthreads();  // slot 1's entries are no longer read
+    uint64_t* wts = reinterpret_cast<uint64_t*>(&f.ent[1]);
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) wts[t + q * kWG] = wl[q];
+    __syncthreads();
+    return draw_list(p, f, wts, u);
+  }
+  // dense target support: passes over both rows
+  const char* r0 = row_ptr(p, row0);
+  const char* r1 = row_ptr(p, row1);
+  const uint32_t* bm0 = row_bitmap(p, row0);
+  const uint32_t* bm1 = row_bitmap(p, row1);
+  const RowAux a1 = f.aux[1];
+  auto dval = [&](int64_t i, float x0) -> float {
+    const float P = filtered_of(a, pval(K0, x0));
+    if (!(P > 0.0f)) return 0.0f;
+    const float Q = (a1.flags & kRowEmpty) ? 0.0f : filtered_of(a1, pval(K1, load_x<DT>(p, r1, bm1, i)));
+    const float d = P - Q;
+    return d > 0.0f ? d : 0.0f;
+  };
+  uint64_t dsum = 0, psum = 0;
+  row_pass<DT>(p, r0, bm0, 0, p.vocab, [&](int64_t i, float x0) {
+    dsum += fx46(dval(i, x0));
+    psum += fx46(filtered_of(a, pval(K0, x0)));
+  });
+  const uint64_t dtot = block_sum(dsum, f.red);
+  const uint64_t ptot = block_sum(psum, f.red2);
+  const bool use_d = dtot > 0;
+  const float den = use_d ? mass_to_f32(dtot) : (ptot > 0 ? mass_to_f32(ptot) : 1.0f);
+  __syncthreads();
+  return draw_dense<DT>(p, f, r0, bm0, u, [&](int64_t i, float x0) -> uint64_t {
+    const float w = use_d ? dval(i, x0) : filtered_of(a, pval(K0, x0));
+    return fx46(w / den);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Unit finalisation
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ void finalize_unit(const Params& p, Sh& sh, int unit) {
+  FinSh& f = sh.fin;
+  const int t = threadIdx.x, w = t / kWave;
+  int g, i, nr;
+  int rows[2];
+  if (p.mode == kModeSpec) {
+    g = unit / (p.k + 1);
+    i = unit - g * (p.k + 1);
+    nr = i < p.k ? 2 : 1;
+    rows[0] = g * p.rpg + i;
+    rows[1] = g * p.rpg + p.k + 1 + i;
+  } else {
+    g = unit;
+    i = 0;
+    nr = 1;
+    rows[0] = unit;
+    rows[1] = unit;
+  }
+  if (t == 0) atomic_store_u32(p.unit_cnt + unit, 0u);
+  if (w < nr) row_setup(p, f, w, rows[w]);
+  __syncthreads();
+  RowK K[2];
+  for (int s = 0; s < 2; ++s) K[s] = RowK{f.aux[s < nr ? s : 0].mcmax, f.aux[s < nr ? s : 0].s, p.cd};
+  for (int s = 0; s < nr; ++s) load_entries(p, f, s, rows[s], K[s]);
+  __syncthreads();
+  for (int s = 0; s < nr; ++s) resolve_row<DT>(p, f, s, rows[s], K[s]);
+
+  if (p.mode == kModeSpec) {
+    const int k = p.k;
+    const float* ug = p.uniforms + static_cast<int64_t>(g) * (2 * k + 1);
+    int64_t token;
+    bool acc = false;
+    if (i == k) {
+      token = draw_target<DT>(p, f, rows[0], K[0], ug[2 * k]);
+    } else {
+      const RowAux& a0 = f.aux[0];
+      const RowAux& a1 = f.aux[1];
+      const float P = a0.has_tok ? filtered_of(a0, pval(K[0], a0.xtok)) : 0.0f;
+      const float Q = a1.has_tok ? filtered_of(a1, pval(K[1], a1.xtok)) : 0.0f;
+      acc = accept_draw(ug[i], P, Q);
+      const int64_t x = p.draft_tokens[static_cast<int64_t>(g) * k + i];
+      token = acc ? x : draw_residual<DT>(p, f, rows[0], rows[1], K[0], K[1], ug[k + i]);
+    }
+    // publish, then the last of the group's k+1 units writes the outputs
+    if (t == 0) {
+      store_sc64(p.words + static_cast<int64_t>(g) * (k + 1) + i,
+                 static_cast<uint64_t>(token) | (acc ? (1ull << 63) : 0ull));
+      drain_stores();
+      const uint32_t old = atomic_arrive(p.grp_cnt + g);
+      sh.fin.sel[1] = old == static_cast<uint32_t>(k) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (sh.fin.sel[1] && t < kWave) {
+      // accepted length: the first rejected position (k if none), 64 positions per pass
+      const uint64_t* wg = p.words + static_cast<int64_t>(g) * (k + 1);
+      int a = k;
+      for (int b0 = 0; b0 < k && a == k; b0 += kWave) {
+        const int pos = b0 + t;
+        const uint64_t wd = pos < k ? load_sc64(wg + pos) : (1ull << 63);
+        const uint64_t rej = __ballot(!(wd >> 63));
+        if (rej) a = b0 + __builtin_ctzll(rej);
+      }
+      for (int b0 = 0; b0 <= k; b0 += kWave) {
+        const int pos = b0 + t;
+        if (pos <= k) {
+          const int64_t tokv = pos <= a ? static_cast<int64_t>(load_sc64(wg + pos) & 0x7fffffffffffffffull) : -1;
+          p.tokens[static_cast<int64_t>(g) * (k + 1) + pos] = tokv;
+        }
+      }
+      if (t == 0) {
+        p.accept_len[g] = a;
+        atomic_store_u32(p.grp_cnt + g, 0u);
+      }
+    }
+  } else if (p.mode == kModeSample) {
+    const int64_t token = draw_target<DT>(p, f, rows[0], K[0], p.row_uniforms[rows[0]]);
+    if (t == 0) p.row_tokens[rows[0]] = token;
+  } else {
+    if (t == 0) {
+      const RowAux& a = f.aux[0];
+      RowStat st;
+      st.mcmax = a.mcmax;
+      st.s = a.s;
+      st.cutoff = a.cut;
+      st.mass = a.mass_f;
+      st.flags = a.flags;
+      st.pad = 0;
+      st.mass_fx = a.mass_fx;
+      p.stats[rows[0]] = st;
+      const bool filt = a.flags & kRowFiltered;
+      if (p.cutoff_out) p.cutoff_out[rows[0]] = filt ? a.cut : 0.0f;
+      if (p.mass_out) p.mass_out[rows[0]] = filt ? a.mass_f : 1.0f;
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// The persistent kernel
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t next_ticket(const Params& p) {
+  const uint32_t x = blockIdx.x & (kTickets - 1);
+  const uint32_t n = atomic_arrive(p.ctl + x * kLineU32);
+  return gridDim.x + x + kTickets * n;
+}
+
+template <int DT, bool PEN>
+__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(kWgPerCu)))
+void fused_kernel(const Params p) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int NVC = kChunk / (kWave * EPV);
+  __shared__ Sh sh;
+  const int t = threadIdx.x, w = t / kWave, lane = t & (kWave - 1);
+  uint32_t q = blockIdx.x;
+  u32x4 cur[NVC], nxt[NVC];
+  uint32_t cpw = 0, npw = 0;
+  if (4 * q + w < static_cast<uint32_t>(p.items)) load_item<DT, NVC>(p, 4 * q + w, cur, cpw);
+  if (t == 0) sh.ticket[2] = next_ticket(p);
+  __syncthreads();
+  uint32_t qn = sh.ticket[2];
+  for (int step = 0;; ++step) {
+    const bool has_next = qn < static_cast<uint32_t>(p.tickets);
+    if (has_next && 4 * qn + w < static_cast<uint32_t>(p.items)) load_item<DT, NVC>(p, 4 * qn + w, nxt, npw);
+    uint32_t tk = 0;
+    if (t == 0 && has_next) tk = next_ticket(p);
+    int done = -1;
+    if (4 * q + w < static_cast<uint32_t>(p.items)) done = stream_item<DT, PEN>(p, sh, w, 4 * q + w, cur, cpw);
+    if (lane == 0) sh.ready[step & 1][w] = done;
+    if (t == 0) sh.ticket[step & 1] = tk;
+    __syncthreads();
+    const uint32_t qnn = sh.ticket[step & 1];
+    int rdy[kNW];
+#pragma unroll
+    for (int r = 0; r < kNW; ++r) rdy[r] = sh.ready[step & 1][r];
+#pragma unroll
+    for (int r = 0; r < kNW; ++r) {
+      if (rdy[r] >= 0) finalize_unit<DT>(p, sh, rdy[r]);
+    }
+    if (!has_next) break;
+    q = qn;
+    qn = qnn;
 #pragma unroll
     for (int u = 0; u < NVC; ++u) {
       u32x4 v = nxt[u];
       asm volatile("" : "+v"(v));
       cur[u] = v;
-      pcur[u] = pnxt[u];
     }
-    tcur = tnxt;
-    item = next;
+    cpw = npw;
   }
-}
-
-// ===========================================================================
-// Row phase
-// ===========================================================================
-
-// Shared memory of the row kernels: up to two rows (spec: the target and the
-// draft row of one draft position) finalised side by side.
-struct RowSh {
-  uint64_t slot[2][kRowCand];          // candidate slots (idx << 32 | bits(p))
-  union {
-    uint64_t H[2][kBins];              // radix bins of each row
-    float w[kRowCand];                 // draw weights per slot
-  };
-  float g[2][kMaxChunks];
-  float mcj[2][kMaxChunks];
-  uint32_t n[2][kMaxChunks];
-  uint8_t kb[2][kMaxChunks];           // K of each chunk (kOctBins: complete)
-  uint32_t gbits[2][kGather];
-  uint64_t gw[2][kGather];
-  uint32_t gcount[2];
-  uint32_t sel32[2][2];
-  uint64_t sel64[2][3];
-  uint64_t red[2 * kRW];
-  uint64_t red2[2 * kRW];              // block_sum_n's own buffer
-  uint64_t red3[2 * kRW];              // the radix selects' own scan buffer
-  uint64_t u64s[8];
-  uint32_t u32s[8];
-  float f32s[2][4];
-  float slow_cut[2];
-  float wmin[kRW];                     // per-wave minima (negated) of the slow path
-  uint64_t slow_mass[2];
-  uint64_t draws[64 + 1];
-};
-
-// Exclusive scans in lane order over the workgroup of NS values at once;
-// tot receives the sums. smem holds NS * kRW words. LEAD = false drops the
-// leading barrier, for a caller whose smem has a barrier between this and its
-// previous use.
-template <int NS, bool LEAD = true>
-__device__ __forceinline__ void block_excl_scan_n(const uint64_t (&v)[NS], uint64_t* smem, uint64_t (&ex)[NS],
-                                                  uint64_t (&tot)[NS]) {
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  uint64_t inc[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) inc[s] = wave_scan_add_u64(v[s]);
-  if constexpr (LEAD) __syncthreads();
-  if (lane == kWave - 1) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) smem[s * kRW + wid] = inc[s];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    uint64_t base = 0, t = 0;
-#pragma unroll
-    for (int i = 0; i < kRW; ++i) {
-      const uint64_t x = smem[s * kRW + i];
-      base += i < wid ? x : 0;
-      t += x;
-    }
-    ex[s] = base + inc[s] - v[s];
-    tot[s] = t;
-  }
-}
-
-// Sums over the workgroup of NS values at once, with one barrier. smem (NS *
-// kRW words) must not be read by a wave still inside a previous use: the
-// callers give it a buffer of its own.
-template <int NS>
-__device__ __forceinline__ void block_sum_n(const uint64_t (&v)[NS], uint64_t* smem, uint64_t (&tot)[NS]) {
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint64_t w = wave_scan_add_u64(v[s]);
-    if (lane == kWave - 1) smem[s * kRW + wid] = w;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    uint64_t t = 0;
-#pragma unroll
-    for (int i = 0; i < kRW; ++i) t += smem[s * kRW + i];
-    tot[s] = t;
-  }
-}
-
-__device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t* smem, uint64_t* total) {
-  const uint64_t vv[1] = {v};
-  uint64_t ex[1], tot[1];
-  block_excl_scan_n<1>(vv, smem, ex, tot);
-  *total = tot[0];
-  return ex[0];
-}
-
-// Wave w: from the chunk records of row-set `set` (lane l holds records 2l
-// and 2l+1) compute the row max, S and g_j (kept in sh.g / sh.mcj / sh.n),
-// the bound on every p outside the candidates, and p of the draft token.
-struct RowScale {
-  float mcmax, s, p_bound, p_tok;
-  bool has_tok;
-};
-
-__device__ __forceinline__ float chunk_bound(const ChunkRec& rec, float gj) {
-  if (rec.flags & kChunkComplete) return 0.0f;
-  return rec.K > 0 ? __builtin_ldexpf(kCandScale, -rec.K) * gj : __builtin_inff();
-}
-
-__device__ __forceinline__ RowScale row_scale(RowSh& sh, int set, const ChunkRec& ra, const ChunkRec& rb, int nch) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int ja = 2 * lane, jb = ja + 1;
-  const bool ia = ja < nch, ib = jb < nch;
-  RowScale rs;
-  rs.mcmax = wave_max_f32(nmax(ia ? ra.mc : -__builtin_inff(), ib ? rb.mc : -__builtin_inff()));
-  const float fa = ia ? exp2q(ra.mc - rs.mcmax) : 0.0f;
-  const float fb = ib ? exp2q(rb.mc - rs.mcmax) : 0.0f;
-  // slots 2l and 2l+1 are the first pairwise level of the normaliser's sum
-  rs.s = wave_tree_sum((ia ? fa * ra.mass : 0.0f) + (ib ? fb * rb.mass : 0.0f));
-  const float ga = fa / rs.s, gb = fb / rs.s;
-  if (ia) {
-    sh.g[set][ja] = ga;
-    sh.mcj[set][ja] = ra.mc;
-    sh.n[set][ja] = ra.n;
-    sh.kb[set][ja] = static_cast<uint8_t>((ra.flags & kChunkComplete) ? kOctBins : ra.K);
-  }
-  if (ib) {
-    sh.g[set][jb] = gb;
-    sh.mcj[set][jb] = rb.mc;
-    sh.n[set][jb] = rb.n;
-    sh.kb[set][jb] = static_cast<uint8_t>((rb.flags & kChunkComplete) ? kOctBins : rb.K);
-  }
-  rs.p_bound = wave_max_f32(__builtin_fmaxf(ia ? chunk_bound(ra, ga) : 0.0f, ib ? chunk_bound(rb, gb) : 0.0f));
-  const bool ta = ia && (ra.flags & kChunkHasTok), tb = ib && (rb.flags & kChunkHasTok);
-  rs.has_tok = __ballot(ta || tb) != 0;
-  rs.p_tok = wave_max_f32(ta ? ra.e_tok * ga : (tb ? rb.e_tok * gb : -1.0f));
-  return rs;
-}
-
-// Chunk records 2l and 2l+1 of row r for lane l.
-__device__ __forceinline__ void load_recs(const SampParams& p, int64_t r, ChunkRec* ra, ChunkRec* rb) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int ja = 2 * lane, jb = ja + 1;
-  if (ja < p.nch) *ra = p.chunks[r * p.nch + ja];
-  if (jb < p.nch) *rb = p.chunks[r * p.nch + jb];
-}
-
-__device__ __forceinline__ uint32_t digit_of(uint32_t bits, int shift, uint32_t dmask) {
-  const uint32_t d = (bits >> shift) & dmask;
-  return d < kBins ? d : kBins - 1;
-}
-
-// Exact top-p cutoffs of NS sets at once (sets s0 .. s0+NS-1 of sh), each
-// visited by visit(s, f), which passes f(bits, w) for its elements (bits of
-// p > 0, w = fx46(p)): c = max{v : sum_{p >= v} w >= thr}, and the mass
-// kept. Up to three radix rounds on the bits of p (12, 11 and 8 bits from the
-// top; sh.H[s] zero on entry); after each round a bucket of at most kGather
-// entries is finished by one wave (wave s for set s). found[s] is false when
-// the set's total mass is below thr. The sets advance in lockstep, so NS rows
-// cost the barriers of one. after_r0(d) runs on every lane once round 0 has
-// found set 0's crossing digit d (the top 12 bits, bits >> kRound0Shift; kNone
-// if the set holds less than thr): every element of p >= the cutoff has a
-// digit >= d, so loads issued there for those elements overlap the rest.
-constexpr int kRound0Shift = 19;
-
-template <int NS, typename Visit, typename AfterR0>
-__device__ void radix_select_n(RowSh& sh, int s0, const uint64_t (&thr)[NS], Visit visit, bool (&found)[NS],
-                               float (&cut)[NS], uint64_t (&mass)[NS], AfterR0 after_r0) {
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  uint32_t prefix[NS], pmask[NS];
-  uint64_t above[NS];
-  bool done[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    prefix[s] = pmask[s] = 0;
-    above[s] = 0;
-    done[s] = false;
-    found[s] = false;
-  }
-  for (int round = 0; round < 3; ++round) {
-    const int shift = round == 0 ? kRound0Shift : (round == 1 ? 8 : 0);
-    const uint32_t dmask = round == 0 ? 0xfffu : (round == 1 ? 0x7ffu : 0xffu);
-    if (round > 0) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        if (!done[s]) {
-#pragma unroll
-          for (int q = 0; q < kBinsPerLane; ++q) sh.H[s0 + s][kBinsPerLane * t + q] = 0;
-        }
-      }
-      __syncthreads();
-    }
-    // this round's crossing digit and gather count start empty (the barrier
-    // below orders these stores before any use)
-    if (t < NS) {
-      sh.sel32[t][0] = kNone;
-      sh.gcount[t] = 0;
-    }
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (!done[s]) {
-        uint64_t* H = sh.H[s0 + s];
-        const uint32_t pm = pmask[s], pf = prefix[s];
-        visit(s, [&](uint32_t bits, uint64_t w) {
-          if ((bits & pm) == pf && w)
-            __hip_atomic_fetch_add(&H[digit_of(bits, shift, dmask)], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        });
-      }
-    }
-    __syncthreads();
-    // lane t owns digits kBins-1 - (kBinsPerLane*t + q), q = 0.. (descending)
-    uint64_t v[NS][kBinsPerLane], sum[NS], ex[NS], tot[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      sum[s] = 0;
-#pragma unroll
-      for (int q = 0; q < kBinsPerLane; ++q) {
-        v[s][q] = done[s] ? 0 : sh.H[s0 + s][kBins - 1 - (kBinsPerLane * t + q)];
-        sum[s] += v[s][q];
-      }
-    }
-    block_excl_scan_n<NS, false>(sum, sh.red3, ex, tot);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      uint64_t before = above[s] + ex[s];
-      if (!done[s] && before < thr[s] && before + sum[s] >= thr[s]) {
-#pragma unroll
-        for (int q = 0; q < kBinsPerLane; ++q) {
-          if (before < thr[s] && before + v[s][q] >= thr[s]) {
-            sh.sel32[s][0] = static_cast<uint32_t>(kBins - 1 - (kBinsPerLane * t + q));
-            sh.sel64[s][0] = before;
-            sh.sel64[s][1] = v[s][q];
-          }
-          before += v[s][q];
-        }
-      }
-    }
-    __syncthreads();
-    uint64_t binmass[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      binmass[s] = 0;
-      if (!done[s]) {
-        const uint32_t digit = sh.sel32[s][0];
-        if (digit == kNone) {
-          done[s] = true;
-        } else {
-          prefix[s] |= digit << shift;
-          pmask[s] |= dmask << shift;
-          above[s] = sh.sel64[s][0];
-          binmass[s] = sh.sel64[s][1];
-        }
-      }
-    }
-    if (round == 0) after_r0(sh.sel32[0][0]);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (!done[s]) {
-        const uint32_t pm = pmask[s], pf = prefix[s];
-        uint32_t* gb = sh.gbits[s];
-        uint64_t* gw = sh.gw[s];
-        uint32_t* gc = &sh.gcount[s];
-        visit(s, [&](uint32_t bits, uint64_t w) {
-          if ((bits & pm) == pf && w) {
-            const uint32_t k = __hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (k < kGather) {
-              gb[k] = bits;
-              gw[k] = w;
-            }
-          }
-        });
-      }
-    }
-    __syncthreads();
-    bool finish[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      finish[s] = false;
-      if (!done[s]) {
-        const uint32_t cnt = sh.gcount[s];
-        if (cnt > kGather && round == 2) {
-          // every entry of the bucket has the same bits
-          cut[s] = __uint_as_float(prefix[s]);
-          mass[s] = above[s] + binmass[s];
-          found[s] = true;
-          done[s] = true;
-        } else if (cnt <= kGather) {
-          finish[s] = true;
-          if (wid == s) {
-            const uint32_t b = lane < static_cast<int>(cnt) ? sh.gbits[s][lane] : 0u;
-            uint64_t A = above[s];
-            for (int j = 0; j < static_cast<int>(cnt); ++j) {
-              const uint32_t bj = sh.gbits[s][j];
-              const uint64_t wj = sh.gw[s][j];
-              A += bj >= b ? wj : 0;
-            }
-            const bool ok = lane < static_cast<int>(cnt) && A >= thr[s];
-            const uint64_t best = wave_max_u64(ok ? b : 0u);
-            const uint64_t at = wave_max_u64(ok && b == static_cast<uint32_t>(best) ? A : 0);
-            if (lane == 0) {
-              sh.sel32[s][1] = static_cast<uint32_t>(best);
-              sh.sel64[s][2] = at;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-    bool all = true;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (finish[s]) {
-        cut[s] = __uint_as_float(sh.sel32[s][1]);
-        mass[s] = sh.sel64[s][2];
-        found[s] = true;
-        done[s] = true;
-      }
-      all = all && done[s];
-    }
-    if (all) break;
-  }
-}
-
-// p of element i of a row recomputed from its logit.
-template <int DT>
-__device__ __forceinline__ float p_elem(const char* rowp, const uint32_t* bm, float c, float pen, float inv_pen,
-                                        const float* mcj, const float* gj, int i) {
-  float l = load_elem<DT>(rowp, i);
-  if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
-  const int j = i >> kChunkShift;
-  return exp2q(__builtin_fmaf(l, c, -mcj[j])) * gj[j];
-}
-
-// Index-ordered inverse-CDF pick over the first n slots; weight(s) is an
-// exact fx46 mass. Lane t owns slots [8t, 8t+8). Returns the winning slot, or
-// -1 at zero total mass.
-template <typename W>
-__device__ int pick_slot(RowSh& sh, int n, float u, W weight) {
-  const int t = threadIdx.x;
-  const int s0 = kSlotsPerLane * t;
-  uint64_t sum = 0;
-#pragma unroll
-  for (int q = 0; q < kSlotsPerLane; ++q) sum += s0 + q < n ? weight(s0 + q) : 0;
-  // the scan's barrier publishes this before any lane can set it
-  if (t == 0) sh.u32s[3] = kNone;
-  const uint64_t vv[1] = {sum};
-  uint64_t exv[1], totv[1];
-  // no leading barrier: every caller reaches this through a barrier after
-  // its last other use of sh.red
-  block_excl_scan_n<1, false>(vv, sh.red, exv, totv);
-  const uint64_t ex = exv[0], total = totv[0];
-  if (total > 0) {
-    const uint64_t target = floor_u_times(u, total);
-    if (ex <= target && target < ex + sum) {
-      uint64_t run = ex;
-      for (int q = 0; q < kSlotsPerLane; ++q) {
-        if (s0 + q >= n) break;
-        run += weight(s0 + q);
-        if (run > target) {
-          sh.u32s[3] = static_cast<uint32_t>(s0 + q);
-          break;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  const uint32_t s = sh.u32s[3];
-  return s == kNone ? -1 : static_cast<int>(s);
-}
-
-// Dense inverse-CDF pick over a whole row whose masses weight(idx) are
-// computed on the fly. Lane t owns a contiguous index range.
-template <typename W>
-__device__ int64_t pick_dense(RowSh& sh, int vocab, float u, W weight) {
-  const int t = threadIdx.x;
-  const int per = (vocab + kRB - 1) / kRB;
-  const int a = t * per < vocab ? t * per : vocab;
-  const int b = a + per < vocab ? a + per : vocab;
-  uint64_t sum = 0;
-  for (int i = a; i < b; ++i) sum += weight(i);
-  uint64_t total;
-  const uint64_t ex = block_excl_scan(sum, sh.red, &total);
-  if (t == 0) sh.u64s[3] = 0;
-  __syncthreads();
-  if (total > 0) {
-    const uint64_t target = floor_u_times(u, total);
-    if (ex <= target && target < ex + sum) {
-      uint64_t run = ex;
-      for (int i = a; i < b; ++i) {
-        run += weight(i);
-        if (run > target) {
-          sh.u64s[3] = static_cast<uint64_t>(i);
-          break;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  return static_cast<int64_t>(sh.u64s[3]);
-}
-
-// The candidates' cutoff cut of the row of set `set` did not clear the
-// worst-case bound on the p outside the candidates. Re-reads only the chunks
-// whose bound reaches cut and checks their non-candidates exactly: true iff
-// every p outside the candidates is below cut, in which case cut and the
-// candidates' mass are the row's (no element outside the candidates can
-// reach a value >= cut). Runs inside slow_select.
-template <int DT>
-__device__ __forceinline__ bool bound_repair(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c,
-                                             float pen, float inv_pen, int vocab, int nch, float cut) {
-  const int t = threadIdx.x;
-  bool bad = false;
-  for (int j = 0; j < nch; ++j) {
-    const int K = sh.kb[set][j];
-    if (K >= kOctBins) continue;
-    const float gj = sh.g[set][j];
-    const float th = K > 0 ? __builtin_ldexpf(kCandScale, -K) : __builtin_inff();
-    if (K > 0 && !(th * gj >= cut)) continue;  // chunk_bound below cut
-    const float nmc = -sh.mcj[set][j];
-    const int c0 = j * kChunk;
-#pragma unroll
-    for (int q = 0; q < kChunk / kRB; ++q) {
-      const int i = c0 + t + q * kRB;
-      if (i < vocab) {
-        float l = load_elem<DT>(rowp, i);
-        if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
-        const float e = exp2q(__builtin_fmaf(l, c, nmc));
-        bad = bad || (!(e >= th) && e * gj >= cut);
-      }
-    }
-  }
-  // block-wide OR through LDS (no device-library call)
-  if (t == 0) sh.u32s[6] = 0u;
-  __syncthreads();
-  if (bad) sh.u32s[6] = 1u;
-  __syncthreads();
-  const bool any = sh.u32s[6] != 0u;
-  __syncthreads();
-  return !any;
-}
-
-// Chunk rebuild, when the bound repair found a non-candidate p >= cut (the
-// candidates' cutoff): the candidates of every chunk whose bound reaches cut
-// become {p >= cut} of that chunk, in index order, if they fit its cap slots.
-// cut is a lower bound of the row's cutoff (the candidates alone hold top_p
-// at p >= cut), and the other chunks hold no p >= cut, so afterwards the
-// slots hold every element of p >= the row's cutoff and their select is exact.
-// Returns false (slots partly rewritten) if some chunk does not fit. Out of
-// line, like slow_select.
-template <int DT, int OCC>
-__device__ __noinline__ bool rebuild_chunks(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c,
-                                               float pen, float inv_pen, int vocab, int nch, int cap, float cut) {
-  constexpr int kQ = kChunk / kRB;
-  static_assert(kQ * kRW <= kGather, "per-(q, wave) counts fit sh.gbits[0]");
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  // at fixed offsets (sets are rebuilt one at a time), so the count reads
-  // take immediate offsets rather than per-read addresses
-  uint32_t* cnt = sh.gbits[0];
-#pragma nounroll
-  for (int j = 0; j < nch; ++j) {
-    const int K = sh.kb[set][j];
-    if (K >= kOctBins) continue;
-    const float gj = sh.g[set][j];
-    const float th = K > 0 ? __builtin_ldexpf(kCandScale, -K) : __builtin_inff();
-    if (K > 0 && !(th * gj >= cut)) continue;  // chunk_bound below cut
-    const float nmc = -sh.mcj[set][j];
-    const int c0 = j * kChunk;
-    float pq[kQ];
-    uint64_t mq[kQ];
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      // element c0 + q*kRB + t: (q, t) order is index order
-      const int i = c0 + t + q * kRB;
-      pq[q] = 0.0f;
-      if (i < vocab) {
-        float l = load_elem<DT>(rowp, i);
-        if (bm && bit_of(bm, i)) l = l < 0.0f ? l * pen : l * inv_pen;
-        pq[q] = exp2q(__builtin_fmaf(l, c, nmc)) * gj;
-      }
-      mq[q] = __ballot(pq[q] > 0.0f && pq[q] >= cut);
-      if (lane == 0) cnt[q * kRW + wid] = static_cast<uint32_t>(__builtin_popcountll(mq[q]));
-    }
-    __syncthreads();
-    // lane l < kQ*kRW holds count l = (q, w) in (q, t) order; an inclusive
-    // scan over the lanes gives each wave base[q], the flagged elements
-    // before its own of round q
-    int incl = lane < kQ * kRW ? static_cast<int>(cnt[lane]) : 0;
-#pragma unroll
-    for (int d = 1; d < kQ * kRW; d <<= 1) {
-      const int o = __shfl_up(incl, d);
-      incl += lane >= d ? o : 0;
-    }
-    const int total = __shfl(incl, kQ * kRW - 1);
-    int base[kQ];
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int l = q * kRW + wid;
-      base[q] = __shfl(incl, l) - static_cast<int>(cnt[l]);
-    }
-    if (total > cap) {
-      __syncthreads();  // every wave is past its reads of cnt
-      return false;
-    }
-    uint64_t* slots = sh.slot[set] + j * cap;
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      if ((mq[q] >> lane) & 1u) {
-        const int pos = base[q] + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                      static_cast<uint32_t>(mq[q] >> 32),
-                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mq[q]), 0u)));
-        slots[pos] = (static_cast<uint64_t>(c0 + t + q * kRB) << 32) | __float_as_uint(pq[q]);
-      }
-    }
-    if (t >= total && t < cap) slots[t] = 0;
-    if (t == 0) {
-      sh.n[set][j] = static_cast<uint32_t>(total);
-      sh.kb[set][j] = static_cast<uint8_t>(kOctBins);
-    }
-    __syncthreads();  // slots written; cnt free for the next chunk
-  }
-  return true;
-}
-
-// Cutoff of the row of set `set` when its candidates' cutoff did not pass the
-// bound. mode kSlowCand: the candidates' select again; if they hold top_p,
-// the bound repair returns kRepaired when their cutoff stands, else
-// kNeedRebuild (for the chunk rebuild, then mode kSlowRebuilt: the select over
-// the rebuilt slots, exact, returns kRebuilt). Otherwise (and in mode
-// kSlowRow) the exact select over every element of the row, p recomputed from
-// the re-read logits with the set's g_j; when keep is set, it leaves the
-// support {p >= c} in index order in sh.slot[set] (as idx << 32 | bits(p))
-// and returns its size, or -1 if it does not fit. The cutoff and its fx46
-// mass go to sh.slow_cut / sh.slow_mass. Out of line, with plain arguments
-// and no pointers into the caller's frame, so the common path's registers are
-// unaffected.
-constexpr int kRepaired = -2;     // the candidates' cutoff stands
-constexpr int kRebuilt = -3;      // the rebuilt slots' cutoff
-constexpr int kNeedRebuild = -4;  // the candidates hold top_p but a non-candidate reaches their cutoff
-enum SlowMode : int { kSlowCand = 0, kSlowRebuilt = 1, kSlowRow = 2 };
-
-template <int DT, int OCC>
-__device__ __noinline__ int slow_select(RowSh& sh, int set, const char* rowp, const uint32_t* bm, float c, float pen,
-                                        float inv_pen, int vocab, int nch, int nslots, uint64_t thr, bool keep,
-                                        int mode) {
-  const int t = threadIdx.x, wid = t / kWave;
-  const float* mcj = sh.mcj[set];
-  const float* gj = sh.g[set];
-  auto pval = [&](int i) { return p_elem<DT>(rowp, bm, c, pen, inv_pen, mcj, gj, i); };
-  const uint64_t thr1[1] = {thr};
-  bool found[1];
-  float cc1[1];
-  uint64_t mfx1[1];
-  // 1. the select over the slots (the candidates' p are still in
-  //    sh.slot[set], or the rebuilt chunks')
-  if (mode != kSlowRow) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
-    __syncthreads();
-    radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
-      for (int sl = t; sl < nslots; sl += kRB) {
-        const uint32_t bits = static_cast<uint32_t>(sh.slot[set][sl]);
-        const float x = __uint_as_float(bits);
-        if (x > 0.0f) f(bits, fx46(x));
-      }
-    }, found, cc1, mfx1, [](uint32_t) {});
-    if (found[0]) {
-      if (mode == kSlowCand && !bound_repair<DT>(sh, set, rowp, bm, c, pen, inv_pen, vocab, nch, cc1[0])) {
-        if (t == 0) sh.slow_cut[set] = cc1[0];
-        __syncthreads();
-        return kNeedRebuild;
-      }
-      if (t == 0) {
-        sh.slow_cut[set] = cc1[0];
-        sh.slow_mass[set] = mfx1[0];
-      }
-      __syncthreads();
-      return mode == kSlowCand ? kRepaired : kRebuilt;
-    }
-  }
-  // 2. exact select over the whole row
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < kBinsPerLane; ++q) sh.H[set][kBinsPerLane * t + q] = 0;
-  __syncthreads();
-  radix_select_n<1>(sh, set, thr1, [&](int, auto f) {
-    for (int i = t; i < vocab; i += kRB) {
-      const float pv = pval(i);
-      f(__float_as_uint(pv), fx46(pv));
-    }
-  }, found, cc1, mfx1, [](uint32_t) {});
-  float cc = cc1[0];
-  uint64_t mfx = mfx1[0];
-  if (!found[0]) {
-    // Total mass below the threshold: keep the whole row (cutoff = min p).
-    float mn = __builtin_inff();
-    uint64_t tot = 0;
-    for (int i = t; i < vocab; i += kRB) {
-      const float pv = pval(i);
-      mn = fminf(mn, pv);
-      tot += fx46(pv);
-    }
-    mn = wave_max_f32(-mn);
-    if ((t & (kWave - 1)) == 0) sh.wmin[wid] = mn;
-    uint64_t all;
-    (void)block_excl_scan(tot, sh.red, &all);  // its barriers also publish wmin
-    float m = sh.wmin[0];
-#pragma unroll
-    for (int w = 1; w < kRW; ++w) m = nmax(m, sh.wmin[w]);
-    cc = -m;
-    mfx = all;
-    __syncthreads();
-  }
+  // the last workgroup out resets the ticket counters for the next call
   if (t == 0) {
-    sh.slow_cut[set] = cc;
-    sh.slow_mass[set] = mfx;
-  }
-  __syncthreads();
-  if (!keep) return -1;
-  const int per = (vocab + kRB - 1) / kRB;
-  const int a = t * per < vocab ? t * per : vocab;
-  const int b = a + per < vocab ? a + per : vocab;
-  uint64_t cnt = 0;
-  for (int i = a; i < b; ++i) cnt += pval(i) >= cc ? 1 : 0;
-  uint64_t total;
-  const uint64_t ex = block_excl_scan(cnt, sh.red, &total);
-  if (total > static_cast<uint64_t>(kRowCand)) {
-    __syncthreads();  // every wave is past its reads of sh.red
-    return -1;
-  }
-  int pos = static_cast<int>(ex);
-  for (int i = a; i < b; ++i) {
-    const float pv = pval(i);
-    if (pv >= cc) sh.slot[set][pos++] = (static_cast<uint64_t>(i) << 32) | __float_as_uint(pv);
-  }
-  __syncthreads();
-  return static_cast<int>(total);
-}
-
-// Candidate slot s of row r: (idx << 32 | bits(e)); stale beyond n_j.
-__device__ __forceinline__ uint64_t load_slot(const SampParams& p, int64_t r, int s) {
-  return p.cands[(r * p.nch + (s >> p.cap_log2)) * kChunkCand + (s & (p.cap - 1))];
-}
-
-__device__ __forceinline__ bool slot_valid(const RowSh& sh, int set, const SampParams& p, int s) {
-  return (s & (p.cap - 1)) < static_cast<int>(sh.n[set][s >> p.cap_log2]);
-}
-
-// Finalisation of NS rows side by side (set s = row r[s]): scales, p of the
-// candidates into sh.slot[s] (idx << 32 | bits(p), 0 for empty slots), the
-// exact top-p cutoff (candidates, or the re-streamed row when they do not hold
-// it). after_r0 is the candidates' select's round-0 hook (set 0's crossing
-// digit). Outputs the row statistics, the filtered probability of each row's
-// draft token (-1 if the row has none) and, for a row that took the slow path
-// with keep_support, the size of its support.
-template <int DT, int NS, int OCC, typename AfterR0>
-__device__ void finalize_rows(const SampParams& p, RowSh& sh, const int64_t (&r)[NS], bool keep_support,
-                              RowStat (&st)[NS], float (&P_tok)[NS], int (&n_sup)[NS], AfterR0 after_r0) {
-  const int t = threadIdx.x, wid = t / kWave;
-  const int nch = p.nch;
-  const int nslots = nch * p.cap;
-  float top_p[NS];
-  bool unf[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    top_p[s] = p.top_p_rows ? p.top_p_rows[r[s]] : p.top_p;
-    unf[s] = !(top_p[s] < 1.0f);
-  }
-  // 1. chunk records (wave s: row s) and candidate slots (strided), in flight together
-  ChunkRec ra{}, rb{};
-  if (wid < NS) load_recs(p, wid == 0 ? r[0] : r[NS - 1], &ra, &rb);
-  uint64_t cv[NS][kSlotsPerLane];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int sl = t + q * kRB;
-      cv[s][q] = (!unf[s] && sl < nslots) ? load_slot(p, r[s], sl) : 0;
-    }
-#pragma unroll
-    for (int q = 0; q < kBinsPerLane; ++q) sh.H[s][kBinsPerLane * t + q] = 0;
-  }
-  // 2. row scales (wave s: row s)
-  if (wid < NS) {
-    const RowScale rs = row_scale(sh, wid, ra, rb, nch);
-    if ((t & (kWave - 1)) == 0) {
-      sh.f32s[wid][0] = rs.mcmax;
-      sh.f32s[wid][1] = rs.s;
-      sh.f32s[wid][2] = rs.p_bound;
-      sh.f32s[wid][3] = rs.has_tok ? rs.p_tok : -1.0f;
-    }
-  }
-  __syncthreads();
-  // 3. p of the candidates, kept in registers and in sh.slot
-  float pv[NS][kSlotsPerLane];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int sl = t + q * kRB;
-      pv[s][q] = 0.0f;
-      if (!unf[s] && sl < nslots && slot_valid(sh, s, p, sl))
-        pv[s][q] = __uint_as_float(static_cast<uint32_t>(cv[s][q])) * sh.g[s][sl >> p.cap_log2];
-      if (sl < nslots) sh.slot[s][sl] = ((cv[s][q] >> 32) << 32) | __float_as_uint(pv[s][q]);
-    }
-  }
-  // 4. cutoffs
-  uint64_t thr[NS];
-  bool found[NS];
-  float cut[NS];
-  uint64_t mfx[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) thr[s] = unf[s] ? 0 : fx46(top_p[s]);
-  bool any = false;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) any = any || !unf[s];
-  if (any) {
-    radix_select_n<NS>(sh, 0, thr, [&](int s, auto f) {
-#pragma unroll
-      for (int q = 0; q < kSlotsPerLane; ++q) {
-        const float x = pv[s][q];
-        if (x > 0.0f) f(__float_as_uint(x), fx46(x));
-      }
-    }, found, cut, mfx, after_r0);
-  }
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    st[s].mcmax = sh.f32s[s][0];
-    st[s].s = sh.f32s[s][1];
-    st[s].flags = unf[s] ? (kFlagUnfiltered | kFlagDense) : 0u;
-    st[s].cutoff = 0.0f;
-    st[s].mass_fx = 0;
-    n_sup[s] = nslots;
-    const float p_bound = sh.f32s[s][2];
-    if (!unf[s]) {
-      if (found[s] && cut[s] > p_bound) {
-        st[s].cutoff = cut[s];
-        st[s].mass_fx = mfx[s];
-      } else {
-        const int64_t g = r[s] / p.rpg;
-        const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
-        const char* rowp = row_of(p, g, static_cast<int>(r[s] - g * p.rpg));
-        int n = slow_select<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
-                                kSlowCand);
-        if (n == kNeedRebuild) {
-          // the deficient chunks' candidates become {p >= the candidates' cutoff}
-          const bool fits = rebuild_chunks<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, p.cap,
-                                               sh.slow_cut[s]);
-          n = slow_select<DT, OCC>(sh, s, rowp, bm, p.c, p.pen, p.inv_pen, p.vocab, nch, nslots, thr[s], keep_support,
-                              fits ? kSlowRebuilt : kSlowRow);
-        }
-        st[s].cutoff = sh.slow_cut[s];
-        st[s].mass_fx = sh.slow_mass[s];
-        const bool rep = n == kRepaired, reb = n == kRebuilt;
-        st[s].flags |= rep ? 0u : (reb ? kFlagRebuilt : (kFlagSlow | ((!keep_support || n < 0) ? kFlagDense : 0u)));
-        n_sup[s] = rep || reb ? nslots : n;
-      }
-    }
-    st[s].mass = unf[s] ? 1.0f : mass_to_f32(st[s].mass_fx);
-    const float pt = sh.f32s[s][3];
-    P_tok[s] = pt < 0.0f ? -1.0f : (unf[s] ? pt : (pt >= st[s].cutoff ? pt / st[s].mass : 0.0f));
-    st[s].p_tok = P_tok[s] < 0.0f ? 0.0f : P_tok[s];
-  }
-}
-
-// Inverse-CDF draw over the row of set `set` (its slots hold idx | bits(p),
-// n of them, sh.g / sh.mcj its scales): weights fx46(P), P the filtered,
-// renormalised probability; the whole row when it is dense.
-template <int DT>
-__device__ int64_t own_draw(const SampParams& p, RowSh& sh, int set, const RowStat& st, int n, float u,
-                            const char* rowp, const uint32_t* bm) {
-  const bool unf = st.flags & kFlagUnfiltered;
-  const float cc = st.cutoff, mass = st.mass;
-  if (!(st.flags & kFlagDense)) {
-    const int win = pick_slot(sh, n, u, [&](int s) {
-      const float x = __uint_as_float(static_cast<uint32_t>(sh.slot[set][s]));
-      return x >= cc && x > 0.0f ? fx46(x / mass) : 0ull;
-    });
-    return win < 0 ? 0 : static_cast<int64_t>(sh.slot[set][win] >> 32);
-  }
-  return pick_dense(sh, p.vocab, u, [&](int i) {
-    const float x = p_elem<DT>(rowp, bm, p.c, p.pen, p.inv_pen, sh.mcj[set], sh.g[set], i);
-    return fx46(unf ? x : (x >= cc ? x / mass : 0.0f));
-  });
-}
-
-// Publish draw word w of group g and arrive on its counter; the last of the
-// k+1 arrivals runs the accept chain: a = the first position whose accept
-// bit (bit 63) is clear, tokens = the accepted drafts, draw a, then -1.
-__device__ void publish_draw(const SampParams& p, RowSh& sh, int64_t g, int i, uint64_t word) {
-  const int k = p.k;
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-  if (t == 0) {
-    store_sc64(reinterpret_cast<uint64_t*>(p.draws) + g * (k + 1) + i, word);
-    drain_stores();
-    uint32_t* ctr = p.grp_cnt + g * kCounterStride;
-    const uint32_t prev = atomic_arrive(ctr);
-    const bool last = prev == static_cast<uint32_t>(k);
-    if (last) store_sc(ctr, 0u);
-    sh.u32s[7] = last ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!sh.u32s[7] || wid != 0) return;
-  // wave 0 alone: lane l holds draw l (lane 0 also draw 64 when k == 64)
-  const uint64_t* dw = reinterpret_cast<const uint64_t*>(p.draws) + g * (k + 1);
-  const uint64_t d = lane <= k ? load_sc64(dw + lane) : 0;
-  const uint64_t d64 = (k >= kWave && lane == 0) ? load_sc64(dw + kWave) : 0;
-  const int64_t x = lane < k ? p.draft_tokens[g * k + lane] : -1;
-  const uint64_t bad = __ballot(lane < k && !(d >> 63));
-  const int a = bad ? __builtin_ctzll(bad) : k;
-  const uint64_t wa = a < kWave ? __shfl(d, a) : __shfl(d64, 0);
-  const int64_t da = static_cast<int64_t>(wa & ~(1ull << 63));
-  int64_t* out = p.tokens + g * (k + 1);
-  if (lane < a) out[lane] = x;
-  if (lane == a) out[lane] = da;
-  if (lane > a && lane <= k) out[lane] = -1;
-  if (k >= kWave && lane == 0) out[k] = a == k ? da : -1;
-  if (lane == 0) p.accept_len[g] = a;
-}
-
-// Spec mode: one workgroup per (batch element g, position i). i < k: the
-// target row i and the draft row i, finalised side by side; the accept bit
-// of draft token x_i (u < min(1, P/Q), sampler.py:451-452) and the residual
-// draw normalize(max(P - Q, 0)) (fallback normalize(P), rejection.py:60-69)
-// with u[g, k+i]. i == k: the bonus row's draw with u[g, 2k].
-// OCC = 4: built for two workgroups per CU (at most 128 registers, the
-// out-of-line slow path in its own copies), launched when the workgroups
-// outnumber the CUs; OCC = 0 otherwise (no spills).
-template <int DT, int OCC>
-__global__ __launch_bounds__(kRB) __attribute__((amdgpu_waves_per_eu(OCC > 0 ? OCC : 1)))
-void spec_row_kernel(const SampParams p) {
-  __shared__ RowSh sh;
-  const int k = p.k, rpg = 2 * k + 1;
-  const int64_t g = blockIdx.x / (k + 1);
-  const int i = static_cast<int>(blockIdx.x - g * (k + 1));
-  const int t = threadIdx.x;
-  const int nslots = p.nch * p.cap;
-  const uint32_t* bm = p.use_pen ? p.bitmap + g * p.bm_words : nullptr;
-  // this workgroup's scalars, loaded before the row work so that their latency
-  // is not paid after it
-  const float u_acc = p.uniforms[g * rpg + i];        // i < k: acceptance draw
-  const float u_draw = p.uniforms[g * rpg + k + i];   // residual draw (bonus draw u[2k] when i == k)
-  const int64_t x = i < k ? p.draft_tokens[g * k + i] : -1;
-  const bool bonus = i == k;
-  const int64_t r[2] = {g * rpg + (bonus ? k : i), g * rpg + (bonus ? k : k + 1 + i)};
-  const char* trow = row_of(p, g, bonus ? k : i);
-  const char* drow = row_of(p, g, bonus ? k : k + 1 + i);
-  // the draft logits' bits at the target's candidates that can be in its
-  // support (digit >= the target select's round-0 crossing digit d0), gathered
-  // during the rest of the select and decoded at their use (the bonus
-  // workgroup has no draft row)
-  uint32_t lq[kSlotsPerLane] = {};
-  auto gather = [&](uint32_t d0) {
-    if (bonus || d0 == kNone) return;
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int sl = t + q * kRB;
-      if (sl < nslots) {
-        const uint64_t v = sh.slot[0][sl];
-        const uint32_t bits = static_cast<uint32_t>(v);
-        if (bits != 0u && (bits >> kRound0Shift) >= d0) {
-          const int idx = static_cast<int>(v >> 32);
-          lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
-        }
-      }
-    }
-  };
-  RowStat st[2];
-  float P_tok[2];
-  int n_sup[2];
-  // keep_support: a row whose cutoff needed the whole-row select keeps its
-  // support (if it fits the slots) in index order, so its draw stays on slots
-  finalize_rows<DT, 2, OCC>(p, sh, r, true, st, P_tok, n_sup, gather);
-  // target slots: the candidates, or the kept support of a slow row
-  const int nt = (st[0].flags & kFlagSlow) ? n_sup[0] : nslots;
-  if (bonus) {
-    const int64_t tok = own_draw<DT>(p, sh, 0, st[0], nt, u_draw, trow, bm);
-    publish_draw(p, sh, g, k, static_cast<uint64_t>(tok));
-    return;
-  }
-  if ((st[0].flags & kFlagRebuilt) || (st[0].flags & (kFlagSlow | kFlagDense)) == kFlagSlow) {
-    // the support or rebuilt chunks replaced candidates: gather the draft
-    // logits again (slots with p > 0 hold token indices)
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int sl = t + q * kRB;
-      lq[q] = 0u;
-      if (sl < nt) {
-        const uint64_t v = sh.slot[0][sl];
-        if (static_cast<uint32_t>(v) != 0u) {
-          const int idx = static_cast<int>(v >> 32);
-          lq[q] = load_bits<DT>(drow, idx < p.vocab ? idx : 0);
-        }
-      }
-    }
-  }
-  const RowStat& st_t = st[0];
-  const RowStat& st_d = st[1];
-  // accept bit of x_i
-  const bool acc = x >= 0 && x < p.vocab && accept_draw(u_acc, P_tok[0] < 0.0f ? 0.0f : P_tok[0],
-                                                        P_tok[1] < 0.0f ? 0.0f : P_tok[1]);
-  const float u = u_draw;
-  const bool unf_t = st_t.flags & kFlagUnfiltered;
-  const bool unf_d = st_d.flags & kFlagUnfiltered;
-  auto Qof = [&](float l, int idx) {
-    if (bm && bit_of(bm, idx)) l = l < 0.0f ? l * p.pen : l * p.inv_pen;
-    const int j = idx >> kChunkShift;
-    const float q = exp2q(__builtin_fmaf(l, p.c, -sh.mcj[1][j])) * sh.g[1][j];
-    return unf_d ? q : (q >= st_d.cutoff ? q / st_d.mass : 0.0f);
-  };
-  int64_t token;
-  if (!(st_t.flags & kFlagDense)) {
-    float P[kSlotsPerLane], D[kSlotsPerLane];
-    uint64_t sums[2] = {0, 0};  // fx46 masses of D and of P
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      const int sl = t + q * kRB;
-      P[q] = D[q] = 0.0f;
-      if (sl < nt) {
-        const uint64_t v = sh.slot[0][sl];
-        const float pv = __uint_as_float(static_cast<uint32_t>(v));
-        if (pv > 0.0f && pv >= st_t.cutoff) {
-          P[q] = pv / st_t.mass;
-          const float dv = P[q] - Qof(bits_to_float<DT>(lq[q]), static_cast<int>(v >> 32));
-          D[q] = dv > 0.0f ? dv : 0.0f;
-          sums[0] += fx46(D[q]);
-          sums[1] += fx46(P[q]);
-        }
-      }
-    }
-    uint64_t tot[2];
-    block_sum_n<2>(sums, sh.red2, tot);
-    const bool use_d = tot[0] > 0;
-    const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
-#pragma unroll
-    for (int q = 0; q < kSlotsPerLane; ++q) {
-      // both values in registers first: a select of the two arrays would
-      // otherwise become a select of their addresses, on the stack
-      float dq = D[q], pq = P[q];
-      asm volatile("" : "+v"(dq), "+v"(pq));
-      const int sl = t + q * kRB;
-      if (sl < nt) sh.w[sl] = (use_d ? dq : pq) / den;
-    }
-    __syncthreads();
-    const int win = pick_slot(sh, nt, u, [&](int s) { return fx46(sh.w[s]); });
-    token = win < 0 ? 0 : static_cast<int64_t>(sh.slot[0][win] >> 32);
-  } else {
-    // dense target row: the whole vocabulary
-    auto Pof = [&](int y) {
-      const float pv = p_elem<DT>(trow, bm, p.c, p.pen, p.inv_pen, sh.mcj[0], sh.g[0], y);
-      return unf_t ? pv : (pv >= st_t.cutoff ? pv / st_t.mass : 0.0f);
-    };
-    auto Qat = [&](int y) { return Qof(load_elem<DT>(drow, y), y); };
-    uint64_t sums[2] = {0, 0};
-    {
-      const int per = (p.vocab + kRB - 1) / kRB;
-      const int i0 = t * per < p.vocab ? t * per : p.vocab;
-      const int i1 = i0 + per < p.vocab ? i0 + per : p.vocab;
-      for (int y = i0; y < i1; ++y) {
-        const float pj = Pof(y);
-        const float dj = pj - Qat(y);
-        sums[0] += fx46(dj > 0.0f ? dj : 0.0f);
-        sums[1] += fx46(pj);
-      }
-    }
-    uint64_t ex[2], tot[2];
-    block_excl_scan_n<2>(sums, sh.red, ex, tot);
-    const bool use_d = tot[0] > 0;
-    const float den = use_d ? mass_to_f32(tot[0]) : (tot[1] > 0 ? mass_to_f32(tot[1]) : 1.0f);
-    token = pick_dense(sh, p.vocab, u, [&](int y) {
-      const float pj = Pof(y);
-      float v = pj;
-      if (use_d) {
-        const float dj = pj - Qat(y);
-        v = dj > 0.0f ? dj : 0.0f;
-      }
-      return fx46(v / den);
-    });
-  }
-  publish_draw(p, sh, g, i, static_cast<uint64_t>(token) | (acc ? 1ull << 63 : 0ull));
-}
-
-// Sample and dense modes: one workgroup per row.
-template <int DT, int MODE>
-__global__ __launch_bounds__(kRB) void row_kernel(const SampParams p) {
-  __shared__ RowSh sh;
-  const int64_t r[1] = {blockIdx.x};
-  const int t = threadIdx.x;
-  RowStat st[1];
-  float P_tok[1];
-  int n_sup[1];
-  finalize_rows<DT, 1, 0>(p, sh, r, MODE == kModeSample, st, P_tok, n_sup, [](uint32_t) {});
-  if constexpr (MODE == kModeSample) {
-    const uint32_t* bm = p.use_pen ? p.bitmap + r[0] * p.bm_words : nullptr;
-    const int64_t token = own_draw<DT>(p, sh, 0, st[0], (st[0].flags & kFlagSlow) ? n_sup[0] : p.nch * p.cap,
-                                       p.row_uniforms[r[0]], row_of(p, r[0], 0), bm);
-    if (t == 0) p.row_tokens[r[0]] = token;
-  } else {
-    if (t == 0) {
-      p.stats[r[0]] = st[0];
-      const bool unf = st[0].flags & kFlagUnfiltered;
-      if (p.cutoff_out) p.cutoff_out[r[0]] = unf ? 0.0f : st[0].cutoff;
-      if (p.mass_out) p.mass_out[r[0]] = st[0].mass;
+    const uint32_t old = atomic_arrive(p.ctl + kTickets * kLineU32);
+    if (old + 1u == gridDim.x) {
+      for (int x = 0; x < kTickets; ++x) atomic_store_u32(p.ctl + x * kLineU32, 0u);
+      atomic_store_u32(p.ctl + kTickets * kLineU32, 0u);
     }
   }
 }
@@ -1511,23 +1520,28 @@ __global__ __launch_bounds__(kRB) void row_kernel(const SampParams p) {
 // ===========================================================================
 // dense_kernel: p and the filtered distribution for one (row, chunk) item
 // ===========================================================================
+constexpr int kCB = 256;
+
 template <int DT>
-__global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
+__global__ __launch_bounds__(kCB) void dense_kernel(const Params p) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kCB * EPV);
   const int t = threadIdx.x;
   const int item = blockIdx.x;
   const int64_t r = item / p.nch;
   const int cj = item - static_cast<int>(r) * p.nch;
-  const char* rowp = row_of(p, r, 0);
+  const char* rowp = p.base0 + r * p.bstride0;
   const int c0 = cj * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
   const u32x4* src = reinterpret_cast<const u32x4*>(rowp) + c0 / EPV;
   const RowStat st = p.stats[r];
-  const float mc = p.chunks[r * p.nch + cj].mc;
-  const float gj = exp2q(mc - st.mcmax) / st.s;
-  const bool unf = st.flags & kFlagUnfiltered;
+  const RowK K{st.mcmax, st.s, p.cd};
+  RowAux a{};
+  a.flags = st.flags;
+  a.cut = st.cutoff;
+  a.mass_f = st.mass;
+  a.mass_fx = st.mass_fx;
 #pragma unroll
   for (int u = 0; u < NVC; ++u) {
     const int v = u * kCB + t;
@@ -1536,9 +1550,8 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
       float pv[EPV], fv[EPV];
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
-        const float x = exp2q(__builtin_fmaf(vec_elem<DT>(d, e), p.c, -mc)) * gj;
-        pv[e] = x;
-        fv[e] = unf ? x : (x >= st.cutoff ? x / st.mass : 0.0f);
+        pv[e] = pval(K, vec_elem<DT>(d, e));
+        fv[e] = filtered_of(a, pv[e]);
       }
       const int64_t i = c0 + static_cast<int64_t>(v) * EPV;
 #pragma unroll
@@ -1554,84 +1567,81 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const SampParams p) {
 // Host side
 // ===========================================================================
 struct Layout {
-  uint64_t grp_cnt, chunks, cands, stats, draws, bitmap, total;
+  uint64_t ctl, unit_cnt, grp_cnt, recs, cands, stats, words, bitmap, total;
 };
 
-// Workspace: [group arrival counters, one 64-byte line each, for up to
-// kMaxSpecBatch batch elements] (at a fixed place, so calls of any shape find
-// them zero) [chunk records] [candidates] [row statistics] [draws] [penalty
-// bitmaps, one per group].
-Layout ws_layout(int64_t rows, int64_t groups, int nch) {
+int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChunk); }
+int cap_for(int nch) { return nch <= 32 ? 64 : (nch <= 64 ? 32 : 16); }
+
+// Workspace: [ticket + exit counters] [unit counters] [group counters] --
+// every counter at a fixed place sized for the largest call, so that calls of
+// any shape on one workspace find them zero (each call leaves them zero) --
+// then, shaped by the call, [chunk records] [candidates] [row statistics]
+// [published words] [penalty bitmaps].
+Layout ws_layout(int64_t rows, int64_t words, int64_t groups, int nch) {
   auto al = [](uint64_t x) { return (x + 255u) & ~255ull; };
   Layout l{};
-  l.grp_cnt = 0;
-  uint64_t off = al(l.grp_cnt + static_cast<uint64_t>(kMaxSpecBatch) * kCounterStride * 4u);
-  l.chunks = off;
+  uint64_t off = 0;
+  l.ctl = off;
+  off = al(off + (kTickets + 1) * kLineU32 * 4u);
+  l.unit_cnt = off;
+  off = al(off + static_cast<uint64_t>(kMaxUnits) * 4u);
+  l.grp_cnt = off;
+  off = al(off + static_cast<uint64_t>(kMaxSpecBatch) * 4u);
+  l.recs = off;
   off = al(off + static_cast<uint64_t>(rows) * nch * sizeof(ChunkRec));
   l.cands = off;
-  off = al(off + static_cast<uint64_t>(rows) * nch * kChunkCand * 8u);
+  off = al(off + static_cast<uint64_t>(rows) * nch * cap_for(nch) * 8u);
   l.stats = off;
   off = al(off + static_cast<uint64_t>(rows) * sizeof(RowStat));
-  l.draws = off;
-  off = al(off + static_cast<uint64_t>(rows) * 8u);
+  l.words = off;
+  off = al(off + static_cast<uint64_t>(words) * 8u);
   l.bitmap = off;
   off = al(off + static_cast<uint64_t>(groups) * nch * (kChunk / 32) * 4u);
   l.total = off;
   return l;
 }
 
-void bind_workspace(SampParams& p, void* ws, const Layout& l) {
+void bind_workspace(Params& p, void* ws, const Layout& l) {
   char* b = static_cast<char*>(ws);
+  p.ctl = reinterpret_cast<uint32_t*>(b + l.ctl);
+  p.unit_cnt = reinterpret_cast<uint32_t*>(b + l.unit_cnt);
   p.grp_cnt = reinterpret_cast<uint32_t*>(b + l.grp_cnt);
-  p.chunks = reinterpret_cast<ChunkRec*>(b + l.chunks);
+  p.recs = reinterpret_cast<ChunkRec*>(b + l.recs);
   p.cands = reinterpret_cast<uint64_t*>(b + l.cands);
   p.stats = reinterpret_cast<RowStat*>(b + l.stats);
-  p.draws = reinterpret_cast<int64_t*>(b + l.draws);
+  p.words = reinterpret_cast<uint64_t*>(b + l.words);
   p.bitmap = reinterpret_cast<uint32_t*>(b + l.bitmap);
 }
 
-int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChunk); }
-
-template <int DT, int MODE>
-void launch_dt(const SampParams& p, int64_t groups, int64_t rows, hipStream_t st) {
-  if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(groups)), dim3(kBmB), 0, st, p);
-  const int wgs = static_cast<int>(device_cu_count()) * kChunkWavesPerCu;
-  const dim3 grid(p.items < wgs ? p.items : wgs);
+template <int DT>
+void launch_dt(const Params& p, hipStream_t st) {
+  if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(p.groups)), dim3(kBmB), 0, st, p);
+  const int cap_wgs = device_cu_count() * kWgPerCu;
+  const dim3 grid(p.tickets < cap_wgs ? p.tickets : cap_wgs);
   if (p.use_pen) {
-    hipLaunchKernelGGL((chunk_kernel<DT, true>), grid, dim3(kWave), 0, st, p);
+    hipLaunchKernelGGL((fused_kernel<DT, true>), grid, dim3(kWG), 0, st, p);
   } else {
-    hipLaunchKernelGGL((chunk_kernel<DT, false>), grid, dim3(kWave), 0, st, p);
+    hipLaunchKernelGGL((fused_kernel<DT, false>), grid, dim3(kWG), 0, st, p);
   }
-  if constexpr (MODE == kModeSpec) {
-    const int64_t wgs_row = groups * (p.k + 1);
-    if (wgs_row > static_cast<int64_t>(device_cu_count())) {
-      hipLaunchKernelGGL((spec_row_kernel<DT, 4>), dim3(static_cast<unsigned>(wgs_row)), dim3(kRB), 0, st, p);
-    } else {
-      hipLaunchKernelGGL((spec_row_kernel<DT, 0>), dim3(static_cast<unsigned>(wgs_row)), dim3(kRB), 0, st, p);
-    }
-  } else {
-    hipLaunchKernelGGL((row_kernel<DT, MODE>), dim3(static_cast<unsigned>(rows)), dim3(kRB), 0, st, p);
-  }
-  if constexpr (MODE == kModeDense) {
-    hipLaunchKernelGGL((dense_kernel<DT>), dim3(p.items), dim3(kCB), 0, st, p);
+  if (p.mode == kModeDense && (p.probs_out || p.filt_out)) {
+    hipLaunchKernelGGL((dense_kernel<DT>), dim3(static_cast<unsigned>(p.items)), dim3(kCB), 0, st, p);
   }
 }
 
-template <int MODE>
-int launch_mode(const SampParams& p, int dtype, int64_t groups, int64_t rows, hipStream_t st) {
+int launch(const Params& p, int dtype, hipStream_t st) {
   switch (dtype) {
-    case LS_DTYPE_F32: launch_dt<F32, MODE>(p, groups, rows, st); break;
-    case LS_DTYPE_BF16: launch_dt<BF16, MODE>(p, groups, rows, st); break;
-    case LS_DTYPE_F16: launch_dt<F16, MODE>(p, groups, rows, st); break;
+    case LS_DTYPE_F32: launch_dt<F32>(p, st); break;
+    case LS_DTYPE_BF16: launch_dt<BF16>(p, st); break;
+    case LS_DTYPE_F16: launch_dt<F16>(p, st); break;
     default: return fail(LS_ERR_VALUE, "unsupported logits dtype");
   }
   return check_launch("sampling kernel launch");
 }
 
 // Shared argument validation / setup for the processing options.
-int setup_common(SampParams& p, int dtype, int64_t rows, int64_t vocab, float temperature, float top_p,
-                 int64_t top_k, float penalty, const int32_t* history, int64_t history_stride,
-                 const int32_t* history_len) {
+int setup_common(Params& p, int dtype, int64_t rows, int64_t vocab, float temperature, float top_p, int64_t top_k,
+                 float penalty, const int32_t* history, int64_t history_stride, const int32_t* history_len) {
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(LS_ERR_VALUE, "unsupported logits dtype");
   if (vocab <= 0 || vocab > kMaxVocab) return fail(LS_ERR_VALUE, "vocabulary size must be in [1, 262144]");
@@ -1645,15 +1655,14 @@ int setup_common(SampParams& p, int dtype, int64_t rows, int64_t vocab, float te
     return fail(LS_ERR_VALUE, "repetition penalty needs a token history");
   p.vocab = static_cast<int>(vocab);
   p.nch = nch_for(vocab);
-  p.cap_log2 = p.nch <= kRowCand / kChunkCand ? 6 : (p.nch <= 2 * kRowCand / kChunkCand ? 5 : 4);
-  p.cap = 1 << p.cap_log2;  // nch * cap <= kRowCand
+  p.cap = cap_for(p.nch);
   p.bm_words = p.nch * (kChunk / 32);
   p.items = static_cast<int>(rows * p.nch);
-  const float inv_t = 1.0f / temperature;
-  p.c = kLog2e * inv_t;
+  p.tickets = (p.items + kNW - 1) / kNW;
+  p.cd = kLog2eD / static_cast<double>(temperature);
+  p.c = static_cast<float>(p.cd);
   p.use_pen = penalty != 1.0f;
   p.pen = penalty;
-  p.inv_pen = 1.0f / penalty;
   p.top_p = top_p;
   p.hist = history;
   p.hist_stride = history_stride;
@@ -1670,7 +1679,7 @@ extern "C" {
 
 uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab) {
   if (batch <= 0 || k < 1 || vocab <= 0) return 0;
-  return ws_layout(batch * (2 * k + 1), batch, nch_for(vocab)).total;
+  return ws_layout(batch * (2 * k + 1), batch * (k + 1), batch, nch_for(vocab)).total;
 }
 
 int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64_t target_pos_stride,
@@ -1684,7 +1693,7 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64
   if (batch == 0) return LS_OK;
   if (!target_logits || !draft_logits || !draft_tokens || !uniforms || !accept_len || !tokens)
     return fail(LS_ERR_VALUE, "spec_verify: NULL pointer");
-  SampParams p{};
+  Params p{};
   const int64_t rows = batch * (2 * k + 1);
   int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, penalty, history, history_stride,
                         history_len);
@@ -1699,21 +1708,24 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64
   if (!aligned16(target_logits) || !aligned16(draft_logits) || p.bstride0 % 16 || p.pstride0 % 16 ||
       p.bstride1 % 16 || p.pstride1 % 16)
     return fail(LS_ERR_VALUE, "spec_verify: logits rows must be 16-byte aligned");
+  p.mode = kModeSpec;
   p.k = static_cast<int>(k);
   p.rpg = static_cast<int>(2 * k + 1);
+  p.groups = static_cast<int>(batch);
+  p.units = static_cast<int>(batch * (k + 1));
   p.draft_tokens = draft_tokens;
   p.uniforms = uniforms;
   p.accept_len = accept_len;
   p.tokens = tokens;
-  const Layout l = ws_layout(rows, batch, p.nch);
+  const Layout l = ws_layout(rows, batch * (k + 1), batch, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "spec_verify: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeSpec>(p, dtype, batch, rows, static_cast<hipStream_t>(stream));
+  return launch(p, dtype, static_cast<hipStream_t>(stream));
 }
 
 uint64_t ls_sample_logits_workspace(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
-  return ws_layout(rows, rows, nch_for(vocab)).total;
+  return ws_layout(rows, 0, rows, nch_for(vocab)).total;
 }
 
 int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows, int64_t vocab,
@@ -1723,7 +1735,7 @@ int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   if (rows < 0 || rows > kMaxRows) return fail(LS_ERR_VALUE, "sample_logits: need 0 <= rows <= 65536");
   if (rows == 0) return LS_OK;
   if (!logits || !uniforms || !out_tokens) return fail(LS_ERR_VALUE, "sample_logits: NULL pointer");
-  SampParams p{};
+  Params p{};
   int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, penalty, history, history_stride,
                         history_len);
   if (rc) return rc;
@@ -1731,19 +1743,22 @@ int ls_sample_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   p.base0 = static_cast<const char*>(logits);
   p.bstride0 = row_stride * eb;
   if (!aligned16(logits) || p.bstride0 % 16) return fail(LS_ERR_VALUE, "sample_logits: rows must be 16-byte aligned");
+  p.mode = kModeSample;
   p.rpg = 1;
   p.k = 0;
+  p.groups = static_cast<int>(rows);
+  p.units = static_cast<int>(rows);
   p.row_uniforms = uniforms;
   p.row_tokens = out_tokens;
-  const Layout l = ws_layout(rows, rows, p.nch);
+  const Layout l = ws_layout(rows, 0, rows, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "sample_logits: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeSample>(p, dtype, rows, rows, static_cast<hipStream_t>(stream));
+  return launch(p, dtype, static_cast<hipStream_t>(stream));
 }
 
 uint64_t ls_filter_logits_workspace(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
-  return ws_layout(rows, rows, nch_for(vocab)).total;
+  return ws_layout(rows, 0, rows, nch_for(vocab)).total;
 }
 
 int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t rows, int64_t vocab,
@@ -1753,15 +1768,18 @@ int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   if (rows < 0 || rows > kMaxRows) return fail(LS_ERR_VALUE, "filter_logits: need 0 <= rows <= 65536");
   if (rows == 0) return LS_OK;
   if (!logits) return fail(LS_ERR_VALUE, "filter_logits: NULL logits");
-  SampParams p{};
+  Params p{};
   int rc = setup_common(p, dtype, rows, vocab, temperature, top_p, top_k, 1.0f, nullptr, 0, nullptr);
   if (rc) return rc;
   const int eb = dtype_bytes(dtype);
   p.base0 = static_cast<const char*>(logits);
   p.bstride0 = row_stride * eb;
   if (!aligned16(logits) || p.bstride0 % 16) return fail(LS_ERR_VALUE, "filter_logits: rows must be 16-byte aligned");
+  p.mode = kModeDense;
   p.rpg = 1;
   p.k = 0;
+  p.groups = static_cast<int>(rows);
+  p.units = static_cast<int>(rows);
   p.top_p_rows = top_p < 1.0f ? top_p_rows : nullptr;
   p.probs_out = probs_out;
   p.probs_stride = probs_stride;
@@ -1769,10 +1787,10 @@ int ls_filter_logits(const void* logits, int64_t row_stride, int dtype, int64_t 
   p.filt_stride = filtered_stride;
   p.cutoff_out = cutoff_out;
   p.mass_out = mass_out;
-  const Layout l = ws_layout(rows, rows, p.nch);
+  const Layout l = ws_layout(rows, 0, rows, p.nch);
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "filter_logits: workspace too small");
   bind_workspace(p, workspace, l);
-  return launch_mode<kModeDense>(p, dtype, rows, rows, static_cast<hipStream_t>(stream));
+  return launch(p, dtype, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -10,9 +10,11 @@ import it; the product package ``loopspec_amd`` never does.
 Modules:
 - ``greedy``:   argmax and greedy chain verification (exact; numpy).
 - ``numerics``: the declared arithmetic shared by oracle and kernels (fp32 FMA
-                emulation, the EXP function, 2^-46 fixed-point masses).
+                emulation, the exp2m / exp2p functions, 2^-46 fixed-point masses).
+- ``native``:   the C core (native/ls_oracle.c): exp2m, exp2p and the row
+                softmax, which need binary64 fused multiply-add.
 - ``sampling``: softmax, top-p cutoff, categorical CDF sampling, speculative
-                verification, residuals (declared arithmetic; numpy).
+                verification, residuals (declared arithmetic; numpy + C core).
 - ``graph_ops``: KV slot allocation, request-mapping update, state-row copy
                 and the paged KV commit (integer; numpy).
 - ``torch_ref``: literal torch-CPU restatements of the reference's code

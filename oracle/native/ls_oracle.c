@@ -1,0 +1,320 @@
+/* CPU oracle core of the sampling path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Plain C restatement of the library's declared arithmetic for the softmax
+ * of one processed-logit row (the parts numpy cannot state exactly: binary64
+ * fused multiply-add and the order of binary32 sums). Loaded through ctypes
+ * by oracle/numerics.py and oracle/sampling.py; never linked into the
+ * product library.
+ *
+ * Declared arithmetic (binary32 unless stated; RN = round to nearest even):
+ *
+ *   exp2m(t)  chunk-mass exponential: tc = fmax(t, -200) (NaN -> -200),
+ *             k = rint(tc), r = tc - k (exact), P = degree-5 Horner in
+ *             binary32 with fma (coefficients EXP2M_C), result ldexp(P, k).
+ *   exp2p(t)  probability exponential: same reduction, the polynomial
+ *             evaluated in binary64 with fma (coefficients EXP2P_C) and
+ *             rounded once to binary32, then ldexp(., k). Monotone
+ *             non-decreasing over every binary32 t (checked exhaustively by
+ *             ls_o_exp2p_check), within 2.5 ulp of 2^t.
+ *
+ *   Temperature scale: cd = RN64(log2(e) / T) in binary64 (T the binary32
+ *   temperature), c = RN32(cd).
+ *   Row of V processed logits x (penalised tokens already divided /
+ *   multiplied by the penalty), chunks of 2048 elements; in chunk j the penalised tokens form the set B_j, the
+ *   others A_j:
+ *     m_j  = max of x over A_j (NaN ignored; -inf if none),  mc_j  = RN(m_j c)
+ *     pm_j = max of x over B_j,                             pmc_j = RN(pm_j c)
+ *     e_i  = exp2m(fma(x_i, c, -mc_j)) on A_j (0 on B_j),   M_j  = tree_j(e)
+ *     e'_i = exp2m(fma(x_i, c, -pmc_j)) on B_j,             PM_j = seq_j(e')
+ *   tree_j: lane t of 64 owns the 16-byte vectors u*64 + t of the chunk
+ *   (epv elements each, epv = 4 for 4-byte logits and 8 for 2-byte ones);
+ *   each lane sums its 32 values pairwise in (u, element) order, then the
+ *   64 lane sums are summed pairwise in lane order. seq_j: each lane adds
+ *   its B_j values one by one in (u, element) order starting from 0, then
+ *   the lane sums pairwise as in tree_j.
+ *     mcmax = max over j of mc_j and pmc_j
+ *     slot[2j] = RN(exp2m(RN(mc_j - mcmax)) * M_j),
+ *     slot[2j+1] = RN(exp2m(RN(pmc_j - mcmax)) * PM_j), slots >= 2 nch = 0
+ *     S = pairwise sum of the 256 slots
+ *     p(x) = S > 0 ? RN(exp2p(RN32(fma64(x, cd, -mcmax))) / S) : 0
+ *   (the exponent formed in binary64 and rounded once, so the scale carries
+ *   no binary32 rounding into it)
+ *   so p is a function of the processed logit alone: equal logits get equal
+ *   probabilities and a larger logit never gets a smaller one.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <string.h>
+
+#define CHUNK 2048
+#define LANES 64
+#define SLOTS 256
+#define MAX_CHUNKS 128
+
+static const float EXP2M_C[6] = {
+    1.0f, 0x1.62e428p-1f, 0x1.ebf918p-3f, 0x1.c6b6e4p-5f, 0x1.3d0c54p-7f, 0x1.5c08e4p-10f,
+};
+static const double EXP2P_C[6] = {
+    1.0, 0x1.62e42920369e4p-1, 0x1.ebf9bb8a817edp-3, 0x1.c6b752e01b730p-5, 0x1.3cea874a3c256p-7,
+    0x1.5bba1349df24ap-10,
+};
+
+float ls_o_exp2m(float t) {
+  const float tc = fmaxf(t, -200.0f);
+  const float kf = rintf(tc);
+  const float r = tc - kf;
+  float p = EXP2M_C[5];
+  p = fmaf(p, r, EXP2M_C[4]);
+  p = fmaf(p, r, EXP2M_C[3]);
+  p = fmaf(p, r, EXP2M_C[2]);
+  p = fmaf(p, r, EXP2M_C[1]);
+  p = fmaf(p, r, EXP2M_C[0]);
+  return ldexpf(p, (int)kf);
+}
+
+float ls_o_exp2p(float t) {
+  const float tc = fmaxf(t, -200.0f);
+  const float kf = rintf(tc);
+  const double r = (double)(tc - kf);
+  double p = EXP2P_C[5];
+  p = fma(p, r, EXP2P_C[4]);
+  p = fma(p, r, EXP2P_C[3]);
+  p = fma(p, r, EXP2P_C[2]);
+  p = fma(p, r, EXP2P_C[1]);
+  p = fma(p, r, EXP2P_C[0]);
+  return ldexpf((float)p, (int)kf);
+}
+
+void ls_o_exp2m_arr(const float* t, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = ls_o_exp2m(t[i]);
+}
+
+void ls_o_exp2p_arr(const float* t, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = ls_o_exp2p(t[i]);
+}
+
+/* fma over arrays (binary32, one rounding): out = a * b + c. */
+void ls_o_fmaf_arr(const float* a, const float* b, const float* c, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = fmaf(a[i], b[i], c[i]);
+}
+
+/* NaN-ignoring maximum (fmaxf semantics), -inf for none. */
+static float max_ign(float a, float b) { return fmaxf(a, b); }
+
+static float tree_sum(float* a, int n) {
+  for (int w = 1; w < n; w *= 2)
+    for (int i = 0; i < n; i += 2 * w) a[i] = a[i] + a[i + w];
+  return a[0];
+}
+
+typedef struct {
+  float m, mass, pm, pmass;
+} chunk_stat;
+
+/* Softmax of one processed row in the declared arithmetic.
+ *   x: V processed logits; pen: V flags (1 = penalised token, set B_j) or NULL;
+ *   chunks (optional, nch entries of 4 floats: m_j, M_j, pm_j, PM_j);
+ *   p_out (optional, V floats).
+ * Returns the number of chunks; *mcmax and *s receive the row constants. */
+static float p_val(float x, double cd, float mcmax, float s) {
+  if (!(s > 0.0f)) return 0.0f;
+  const float t = (float)fma((double)x, cd, -(double)mcmax);
+  return ls_o_exp2p(t) / s;
+}
+
+int ls_o_row_softmax(const float* x, const uint8_t* pen, int64_t v, double cd, int epv, float* chunks,
+                     float* mcmax_out, float* s_out, float* p_out) {
+  const float c = (float)cd;
+  const int nch = (int)((v + CHUNK - 1) / CHUNK);
+  if (nch > MAX_CHUNKS || (epv != 4 && epv != 8)) return -1;
+  static __thread chunk_stat st[MAX_CHUNKS];
+  const int nvc = CHUNK / (LANES * epv);  /* vectors per lane */
+  for (int j = 0; j < nch; ++j) {
+    const int64_t c0 = (int64_t)j * CHUNK;
+    float m = -INFINITY, pm = -INFINITY;
+    for (int i = 0; i < CHUNK; ++i) {
+      const int64_t g = c0 + i;
+      if (g >= v) break;
+      if (pen && pen[g]) pm = max_ign(pm, x[g]);
+      else m = max_ign(m, x[g]);
+    }
+    const float mc = m * c, pmc = pm * c;
+    float lane_a[LANES], lane_b[LANES];
+    for (int t = 0; t < LANES; ++t) {
+      float a[32];
+      float acc = 0.0f;
+      for (int u = 0; u < nvc; ++u) {
+        for (int e = 0; e < epv; ++e) {
+          const int64_t g = c0 + (int64_t)(u * LANES + t) * epv + e;
+          float ev = 0.0f;
+          if (g < v) {
+            if (pen && pen[g]) {
+              acc = acc + ls_o_exp2m(fmaf(x[g], c, -pmc));
+            } else {
+              ev = ls_o_exp2m(fmaf(x[g], c, -mc));
+            }
+          }
+          a[u * epv + e] = ev;
+        }
+      }
+      lane_a[t] = tree_sum(a, nvc * epv);
+      lane_b[t] = acc;
+    }
+    st[j].m = m;
+    st[j].pm = pm;
+    st[j].mass = tree_sum(lane_a, LANES);
+    st[j].pmass = tree_sum(lane_b, LANES);
+  }
+  float mcmax = -INFINITY;
+  for (int j = 0; j < nch; ++j) {
+    mcmax = fmaxf(mcmax, st[j].m * c);
+    mcmax = fmaxf(mcmax, st[j].pm * c);
+  }
+  float slot[SLOTS];
+  memset(slot, 0, sizeof(slot));
+  for (int j = 0; j < nch; ++j) {
+    const float mc = st[j].m * c, pmc = st[j].pm * c;
+    slot[2 * j] = ls_o_exp2m(mc - mcmax) * st[j].mass;
+    slot[2 * j + 1] = ls_o_exp2m(pmc - mcmax) * st[j].pmass;
+  }
+  const float s = tree_sum(slot, SLOTS);
+  if (chunks) {
+    for (int j = 0; j < nch; ++j) {
+      chunks[4 * j + 0] = st[j].m;
+      chunks[4 * j + 1] = st[j].mass;
+      chunks[4 * j + 2] = st[j].pm;
+      chunks[4 * j + 3] = st[j].pmass;
+    }
+  }
+  *mcmax_out = mcmax;
+  *s_out = s;
+  if (p_out) {
+    for (int64_t i = 0; i < v; ++i) p_out[i] = p_val(x[i], cd, mcmax, s);
+  }
+  return nch;
+}
+
+/* p of single logits with given row constants. */
+void ls_o_p_of(const float* x, int64_t n, double cd, float mcmax, float s, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = p_val(x[i], cd, mcmax, s);
+}
+
+/* Repetition penalty on a row, in place: for every flagged token,
+ * x < 0 ? RN(x * pen) : RN(x / pen) (the division is correctly rounded). */
+void ls_o_penalise(float* x, const uint8_t* flags, int64_t v, float pen) {
+  for (int64_t i = 0; i < v; ++i) {
+    if (flags[i]) x[i] = x[i] < 0.0f ? x[i] * pen : x[i] / pen;
+  }
+}
+
+/* ---- exhaustive checks, parallel over equal shares of binary32 values ---- */
+
+/* Order-preserving map between binary32 values and signed integers
+ * (-0 and +0 share the key 0). */
+static int64_t f2key(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  return (b & 0x80000000u) ? -(int64_t)(b & 0x7fffffffu) : (int64_t)b;
+}
+static float key2f(int64_t k) {
+  uint32_t b = k < 0 ? (uint32_t)(-k) | 0x80000000u : (uint32_t)k;
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+typedef struct {
+  int64_t k0, k1;        /* keys [k0, k1] */
+  int64_t n, reversals;  /* exp2p walk */
+  double max_rel;
+  float pmin, pmax;      /* exp2m polynomial range */
+} walk_job;
+
+static void* exp2p_walk(void* arg) {
+  walk_job* j = (walk_job*)arg;
+  float prev = ls_o_exp2p(key2f(j->k0));
+  for (int64_t k = j->k0 + 1; k <= j->k1; ++k) {
+    const float t = key2f(k);
+    const float e = ls_o_exp2p(t);
+    j->n++;
+    if (e < prev) j->reversals++;
+    if (t > -120.0f && t < 1.0f) {
+      const double ex = exp2((double)t);
+      const double er = fabs((double)e - ex) / ex;
+      if (er > j->max_rel) j->max_rel = er;
+    }
+    prev = e;
+  }
+  return 0;
+}
+
+static void* poly_walk(void* arg) {
+  walk_job* j = (walk_job*)arg;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t k = j->k0; k <= j->k1; ++k) {
+    const float r = key2f(k);
+    float p = EXP2M_C[5];
+    p = fmaf(p, r, EXP2M_C[4]);
+    p = fmaf(p, r, EXP2M_C[3]);
+    p = fmaf(p, r, EXP2M_C[2]);
+    p = fmaf(p, r, EXP2M_C[1]);
+    p = fmaf(p, r, EXP2M_C[0]);
+    if (p < mn) mn = p;
+    if (p > mx) mx = p;
+  }
+  j->pmin = mn;
+  j->pmax = mx;
+  return 0;
+}
+
+/* Runs `fn` over every binary32 value in [lo, hi], split into `threads`
+ * shares that overlap by one value (so exp2p_walk also compares across the
+ * seams). */
+static void walk(float lo, float hi, int threads, void* (*fn)(void*), walk_job* jobs) {
+  pthread_t th[64];
+  const int64_t a = f2key(lo), b = f2key(hi);
+  const int64_t span = b - a;
+  for (int i = 0; i < threads; ++i) {
+    memset(&jobs[i], 0, sizeof(walk_job));
+    jobs[i].k0 = a + span * i / threads;
+    jobs[i].k1 = a + span * (i + 1) / threads;
+    pthread_create(&th[i], 0, fn, &jobs[i]);
+  }
+  for (int i = 0; i < threads; ++i) pthread_join(th[i], 0);
+}
+
+/* Every binary32 t in [lo, hi]: returns the number of steps walked;
+ * *reversals counts consecutive t < t' with exp2p(t) > exp2p(t'); *max_rel
+ * is the largest relative error against 2^t on (-120, 1). */
+int64_t ls_o_exp2p_check(float lo, float hi, int threads, int64_t* reversals, double* max_rel) {
+  walk_job jobs[64];
+  if (threads < 1 || threads > 64) return -1;
+  walk(lo, hi, threads, exp2p_walk, jobs);
+  int64_t n = 0, rev = 0;
+  double mr = 0.0;
+  for (int i = 0; i < threads; ++i) {
+    n += jobs[i].n;
+    rev += jobs[i].reversals;
+    if (jobs[i].max_rel > mr) mr = jobs[i].max_rel;
+  }
+  *reversals = rev;
+  *max_rel = mr;
+  return n;
+}
+
+/* Extremes of exp2m's binary32 polynomial over every binary32 r in [lo, hi]
+ * (the candidate rule of the chunk pass needs P(r) >= 1 on [0, 1/2] and
+ * P(r) >= 1/2 on [-1/2, 0]). */
+void ls_o_exp2m_poly_range(float lo, float hi, int threads, float* pmin, float* pmax) {
+  walk_job jobs[64];
+  if (threads < 1 || threads > 64) threads = 1;
+  walk(lo, hi, threads, poly_walk, jobs);
+  float mn = INFINITY, mx = -INFINITY;
+  for (int i = 0; i < threads; ++i) {
+    if (jobs[i].pmin < mn) mn = jobs[i].pmin;
+    if (jobs[i].pmax > mx) mx = jobs[i].pmax;
+  }
+  *pmin = mn;
+  *pmax = mx;
+}

@@ -1,14 +1,18 @@
-"""Declared arithmetic of the sampling path (numpy restatement; test infrastructure).
+"""Declared arithmetic of the sampling path (restatement; test infrastructure).
 
 The reference's sampler results depend on float rounding inside torch softmax,
 torch CUDA cumsum and Triton tl.sum trees, none of which can be reproduced on
 another machine. The kernels and this oracle therefore share one declared
 arithmetic, made of operations that are exactly reproducible on both sides:
 
-* IEEE binary32 +, -, *, / with round-to-nearest-even, and fused multiply-add
-  with a single rounding (``fma32`` emulates it exactly here);
-* ``exp2q``: 2^t built only from those operations (rint reduction, a
-  degree-5 polynomial for 2^r on [-1/2, 1/2], exact scaling by 2^k);
+* IEEE binary32 and binary64 +, -, *, / with round-to-nearest-even, and fused
+  multiply-add with a single rounding (``fma32`` emulates the binary32 one
+  exactly in numpy; the binary64 one is only used inside the C core
+  oracle/native/ls_oracle.c, which numpy cannot state);
+* ``exp2m``: 2^t for chunk masses (rint reduction, a degree-5 binary32
+  polynomial for 2^r on [-1/2, 1/2], exact scaling by 2^k);
+* ``exp2p``: 2^t for probabilities (the same reduction, the polynomial in
+  binary64, one rounding to binary32): monotone over every binary32 t;
 * ``tree_sum_f32``: a binary32 sum in a fixed pairwise order;
 * masses as exact integers: a weight w in [0, 1] contributes
   ``fx46(w) = floor(w * 2^46)``; sums of these are exact, so every reduction
@@ -16,9 +20,10 @@ arithmetic, made of operations that are exactly reproducible on both sides:
 * ``u64_to_f32``: round-to-nearest-even conversion of an exact integer mass.
 
 Pinned by: tests/test_oracle_numerics.py (fma32 against exact rationals on
-random and constructed midpoint cases; exp2q within 4 ulp of 2^t over its
-domain with its special points; tree_sum_f32 against an explicit recursive
-pairwise sum; fx46 and u64_to_f32 against Fraction arithmetic).
+random and constructed midpoint cases; exp2m within 4 ulp and exp2p within
+2.5 ulp of 2^t, exp2p monotone by an exhaustive walk over every binary32
+argument; tree_sum_f32 against an explicit recursive pairwise sum; fx46 and
+u64_to_f32 against Fraction arithmetic).
 """
 
 from __future__ import annotations
@@ -31,18 +36,17 @@ F64 = np.float64
 FX_BITS = 46
 FX_ONE = 1 << FX_BITS
 
-# log2(e) rounded to binary32: the scale of the processed logits is
-# c = RN(LOG2E * RN(1/T)), so that 2^(c * x) = e^(x / T).
-LOG2E = F32(1.44269504)
-# exp2q: arguments are clamped at EXP2_FLOOR (NaN too), where 2^t is 0 in binary32.
+# log2(e): the temperature scale is cd = RN64(LOG2E_D / T) in binary64 and
+# c = RN32(cd) in binary32, so that 2^(c x) ~ e^(x / T).
+LOG2E_D = 1.4426950408889634
+LOG2E = F32(LOG2E_D)
+# exp2m / exp2p: arguments are clamped at EXP2_FLOOR (NaN too), where 2^t is 0 in binary32.
 EXP2_FLOOR = F32(-200.0)
-# 2^r on [-1/2, 1/2], relative-error fit, coefficients rounded to binary32;
-# the constant term is exactly 1, so exp2q(0) == 1.
+# exp2m's polynomial (2^r on [-1/2, 1/2], binary32 coefficients; the constant
+# term is exactly 1, so exp2m(0) == 1); restated in oracle/native/ls_oracle.c.
 EXP2_COEFFS = tuple(F32(float.fromhex(h)) for h in (
     "0x1.0p+0", "0x1.62e428p-1", "0x1.ebf918p-3", "0x1.c6b6e4p-5", "0x1.3d0c54p-7", "0x1.5c08e4p-10",
 ))
-# Upper bound of the polynomial over [-1/2, 1/2] (attained near r = 1/2).
-EXP2_POLY_MAX = 1.4142136
 
 
 def f32(x) -> np.ndarray:
@@ -75,27 +79,24 @@ def fma32(a, b, c) -> np.ndarray:
     return np.where(move, nb, r).astype(F32)
 
 
-def exp2q_k(t):
-    """Return (e, k): e = exp2q(t) = P(t - k) * 2^k with k = rint(max(t, -200)).
+def exp2m(t) -> np.ndarray:
+    """Chunk-mass exponential (binary32 polynomial); C core."""
+    from . import native
 
-    t is binary32 (normally t <= 0). NaN and t <= -200 give e = 0 (the scaling
-    underflows); k is returned as int32.
-    """
-    t = np.asarray(t, dtype=F32)
-    with np.errstate(invalid="ignore", over="ignore", under="ignore"):
-        tc = np.fmax(t, EXP2_FLOOR).astype(F32)
-        kf = np.rint(tc).astype(F32)
-        r = (tc - kf).astype(F32)  # exact
-        p = np.full_like(tc, EXP2_COEFFS[5])
-        for coef in EXP2_COEFFS[4::-1]:
-            p = fma32(p, r, coef)
-        k = kf.astype(np.int32)
-        e = np.ldexp(p, k).astype(F32)
-    return e, k
+    return native.exp2m(t)
 
 
-def exp2q(t) -> np.ndarray:
-    return exp2q_k(t)[0]
+def exp2p(t) -> np.ndarray:
+    """Probability exponential (binary64 polynomial, monotone); C core."""
+    from . import native
+
+    return native.exp2p(t)
+
+
+def scale_of(temperature: float) -> tuple[float, np.float32]:
+    """(cd, c): cd = RN64(LOG2E_D / T) with T the binary32 temperature, c = RN32(cd)."""
+    cd = LOG2E_D / float(F32(temperature))
+    return cd, F32(cd)
 
 
 def tree_sum_f32(a) -> np.ndarray:

@@ -1,18 +1,24 @@
-"""Sampling-path oracle on the declared arithmetic (numpy; test infrastructure).
+"""Sampling-path oracle on the declared arithmetic (numpy + C core; test infrastructure).
 
 Every function restates one reference function; the docstring cites it. Rows
 are processed independently. "p" is a softmax probability, "P" a filtered and
 renormalised probability; masses are exact 2^-46 fixed-point integers (see
-oracle.numerics). Parity status per function:
+oracle.numerics). The softmax itself (chunk masses, row normaliser, p of each
+logit) is computed by the C core oracle/native/ls_oracle.c. Parity status per
+function:
 
 - softmax_row, top_p_cutoff, filter_row, categorical_pick: pinned against
-  torch-CPU restatements (oracle.torch_ref) on seeded inputs, brute force on
-  tiny vocabularies and closed-form special cases (tests/test_oracle_sampling.py).
+  torch-CPU restatements (oracle.torch_ref) on seeded inputs at the full
+  BASELINE shapes, against the exact softmax in binary64, brute force on tiny
+  vocabularies, tie/monotonicity invariants and closed-form special cases
+  (tests/test_oracle_sampling.py).
 - accept: closed form (sampler.py:451-452).
 - speculative_verify (chain of k): pinned by exact enumeration of the
   losslessness invariant on tiny vocabularies and against the per-position
-  restatement of the reference policy.
-- apply_penalty: transformers' closed form; parity unpinned against SGLang's
+  restatement of the reference policy (oracle.torch_ref.speculative_verify)
+  at the full C3/C4 shapes.
+- apply_penalty: transformers' closed form x < 0 ? x * r : x / r, bit-equal
+  to oracle.torch_ref.apply_penalty; parity unpinned against SGLang's
   penalizer (sglang is not installed; the reference's own LoopSpec path
   rejects repetition_penalty != 1, server/loopspec_scheduler.py:141-148).
 - top_k cutoff: only the joint top-k/top-p rule of distributions.py:72-86 is
@@ -26,8 +32,9 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from . import native
 from .numerics import (
-    F32, F64, FX_BITS, LOG2E, exp2q, exp2q_k, fx46, floor_u_times, mass_to_f32, tree_sum_f32,
+    F32, F64, FX_BITS, LOG2E, exp2m, exp2p, fx46, floor_u_times, mass_to_f32, scale_of, tree_sum_f32,
 )
 
 
@@ -35,41 +42,40 @@ from .numerics import (
 # (a) logit processing
 # ---------------------------------------------------------------------------
 
-def inv_f32(x: float) -> np.float32:
-    """Binary32 reciprocal RN(1 / RN32(x))."""
-    return F32(F32(1.0) / F32(x))
+def history_mask(history, vocab: int) -> np.ndarray:
+    """Flags of the distinct in-vocabulary token ids of a history."""
+    m = np.zeros(vocab, dtype=bool)
+    if history is not None and len(history):
+        ids = np.asarray(history, dtype=np.int64)
+        ids = ids[(ids >= 0) & (ids < vocab)]
+        m[ids] = True
+    return m
 
 
 def apply_penalty(x: np.ndarray, history, penalty: float) -> np.ndarray:
-    """Repetition penalty over a token history (transformers closed form).
-
-    For every distinct token id in `history`: x < 0 -> x * penalty, else
-    x * RN(1/penalty) (a division by a scalar is a multiplication by its
-    binary32 reciprocal on the GPU torch path). Applied before temperature.
-    """
+    """Repetition penalty over a token history (transformers' closed form,
+    generation/logits_process.py:409-412): for every distinct token id of the
+    history, x < 0 -> RN(x * r), else RN(x / r) with r the binary32 penalty.
+    Applied before temperature."""
+    x = np.asarray(x, dtype=F32)
     if penalty == 1.0 or history is None or len(history) == 0:
-        return x
-    x = x.copy()
-    ids = np.unique(np.asarray(history, dtype=np.int64))
-    v = x[ids]
-    x[ids] = np.where(v < 0, (v * F32(penalty)).astype(F32), (v * inv_f32(penalty)).astype(F32))
-    return x
+        return x.copy()
+    return native.penalise(x, history_mask(history, len(x)), penalty)
 
 
 @dataclass
 class Processed:
-    """Processed logits of one row: x = penalised logits, c = the binary32
-    scale RN(LOG2E * RN(1/T)) applied inside the exponential, epv = elements
-    per 16-byte vector of the logits' storage type (4 for float32, 8 for
-    bfloat16 / float16), which fixes the summation order of the chunk masses."""
+    """Processed logits of one row: x = penalised logits, (cd, c) = the
+    temperature scale (binary64, binary32), epv = elements per 16-byte
+    vector of the logits' storage type (4 for float32, 8 for bfloat16 /
+    float16), which fixes the summation order of the chunk masses, and pen =
+    the flags of the penalised tokens (None without a penalty): they form a
+    sub-chunk of their own in every chunk."""
     x: np.ndarray
+    cd: float
     c: np.float32
     epv: int = 4
-
-
-def scale_of(temperature: float) -> np.float32:
-    """c = RN(LOG2E * RN(1/T)); T == 1 gives LOG2E."""
-    return F32(LOG2E * inv_f32(temperature))
+    pen: np.ndarray | None = None
 
 
 def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float = 1.0, history=None,
@@ -77,32 +83,65 @@ def process_logits(logits: np.ndarray, temperature: float = 1.0, penalty: float 
     """Penalised logits and the temperature scale (distributions.py:44-48).
 
     The reference divides float32 logits by the temperature and takes
-    softmax; here the temperature enters as the scale c of the base-2
-    exponent (2^(c x) = e^(x / T)), so T == 1 and T != 1 share one path.
+    softmax; here the temperature enters as the scale of the base-2 exponent
+    (2^(cd x) = e^(x / T)), so T == 1 and T != 1 share one path.
     """
-    x = np.asarray(logits, dtype=F32).copy()
-    x = apply_penalty(x, history, penalty)
-    return Processed(x, scale_of(temperature), epv)
+    x = np.asarray(logits, dtype=F32)
+    cd, c = scale_of(temperature)
+    if penalty != 1.0 and history is not None and len(history):
+        pen = history_mask(history, len(x))
+        return Processed(native.penalise(x, pen, penalty), cd, c, epv, pen)
+    return Processed(x.copy(), cd, c, epv, None)
 
 
 CHUNK = 2048  # elements per softmax chunk (a constant of the declared arithmetic)
 LANES = 64    # lanes per chunk in the mass summation order
-SCALE_SLOTS = 128  # chunks per row at most; the normaliser sums this many slots
+MAX_CHUNKS = 128  # chunks per row at most (vocabulary <= 262144)
 
 
 @dataclass
 class RowSoftmax:
-    x: np.ndarray      # penalised logits
-    c: np.float32      # exponent scale
-    m: np.float32      # row max of the scaled chunk maxima, max_j mc_j
-    e: np.ndarray      # exp2q(fma(x, c, -mc_j)), chunk-relative
-    m_chunks: np.ndarray   # per-chunk max of x
-    mc_chunks: np.ndarray  # RN(m_j * c)
-    f_chunks: np.ndarray   # exp2q(RN(mc_j - m))
-    mass_chunks: np.ndarray  # chunk masses M_j (binary32, fixed summation order)
-    s: np.float32      # normaliser S
-    g_chunks: np.ndarray   # RN(f_j / S)
-    p: np.ndarray      # probabilities RN(e_i * g_j)
+    x: np.ndarray          # processed logits
+    cd: float              # binary64 exponent scale
+    c: np.float32          # binary32 exponent scale
+    mcmax: np.float32      # row max of the scaled sub-chunk maxima
+    s: np.float32          # normaliser S
+    m_chunks: np.ndarray   # per-chunk max of the non-penalised x (m_j)
+    mass_chunks: np.ndarray  # M_j
+    pm_chunks: np.ndarray  # per-chunk max of the penalised x (pm_j)
+    pmass_chunks: np.ndarray  # PM_j
+    p: np.ndarray          # probabilities p(x_i)
+
+    @property
+    def mc_chunks(self) -> np.ndarray:
+        return (self.m_chunks * self.c).astype(F32)
+
+    @property
+    def pmc_chunks(self) -> np.ndarray:
+        return (self.pm_chunks * self.c).astype(F32)
+
+
+def softmax_row(x, c=None, epv: int = 4) -> RowSoftmax:
+    """softmax(x / T) in the declared arithmetic (distributions.py:44-48).
+
+    x is a Processed row (or raw logits with T = 1). The row is cut into
+    chunks of CHUNK elements; each chunk's non-penalised and penalised tokens
+    give a (max, mass) pair each, relative to their own max, so every chunk
+    can be reduced on its own before the row-wide values are known. The row
+    normaliser S combines them, and every probability is then a function of
+    its processed logit alone: p(x) = RN(exp2p(RN32(fma64(x, cd, -mcmax))) / S)
+    (oracle/native/ls_oracle.c states the arithmetic in full).
+    """
+    if isinstance(x, Processed):
+        pr = x
+    else:
+        cd, cf = scale_of(1.0) if c is None else (float(c), F32(c))
+        pr = Processed(np.asarray(x, dtype=F32), cd, cf, epv, None)
+    if -(-len(pr.x) // CHUNK) > MAX_CHUNKS:
+        raise ValueError("vocabulary larger than MAX_CHUNKS chunks")
+    p, mcmax, s, ch = native.row_softmax(pr.x, pr.cd, pr.epv, pr.pen)
+    return RowSoftmax(pr.x, pr.cd, pr.c, mcmax, s, ch[:, 0].copy(), ch[:, 1].copy(), ch[:, 2].copy(),
+                      ch[:, 3].copy(), p)
 
 
 def chunk_mass(e_chunk: np.ndarray, epv: int) -> np.float32:
@@ -118,57 +157,15 @@ def chunk_mass(e_chunk: np.ndarray, epv: int) -> np.float32:
     return F32(tree_sum_f32(tree_sum_f32(lanes)))
 
 
-def softmax_row(x, c=None, epv: int = 4) -> RowSoftmax:
-    """softmax(x / T) in the declared chunked arithmetic (distributions.py:44-48).
-
-    x is a Processed row (or raw logits with T = 1). The row is cut into chunks
-    of CHUNK elements. Chunk j: m_j = max x, mc_j = RN(m_j c),
-    e_i = exp2q(fma(x_i, c, -mc_j)), M_j = chunk_mass(e). Row: m = max mc_j,
-    f_j = exp2q(RN(mc_j - m)), S = pairwise sum over SCALE_SLOTS slots of
-    RN(f_j M_j) (zero past the last chunk), g_j = RN(f_j / S),
-    p_i = RN(e_i g_j). Every chunk can be processed on its own before the
-    row-wide values are known, which is what lets the kernels read the logits
-    once with many workgroups per row.
-    """
-    if isinstance(x, Processed):
-        x, c, epv = x.x, x.c, x.epv
-    c = LOG2E if c is None else F32(c)
-    x = np.asarray(x, dtype=F32)
-    v = len(x)
-    nch = -(-v // CHUNK)
-    if nch > SCALE_SLOTS:
-        raise ValueError("vocabulary larger than SCALE_SLOTS chunks")
-    xp = np.full(nch * CHUNK, -np.inf, dtype=F32)
-    xp[:v] = x
-    xc = xp.reshape(nch, CHUNK)
-    with np.errstate(invalid="ignore", over="ignore"):
-        m_chunks = np.max(xc, axis=1).astype(F32)
-        mc = (m_chunks * c).astype(F32)
-        t = _fma_rows(xc, c, (-mc).astype(F32))
-        e = exp2q(t)
-        mass = np.array([chunk_mass(e[j], epv) for j in range(nch)], dtype=F32)
-        m = F32(np.max(mc))
-        f = exp2q((mc - m).astype(F32))
-        fm = np.zeros(SCALE_SLOTS, dtype=F32)
-        fm[:nch] = (f * mass).astype(F32)
-        s = F32(tree_sum_f32(fm))
-        g = (f / s).astype(F32)
-        p = (e * g[:, None]).astype(F32).reshape(-1)[:v]
-    return RowSoftmax(x, c, m, e.reshape(-1)[:v], m_chunks, mc, f, mass, s, g, p)
-
-
-def _fma_rows(xc: np.ndarray, c: np.float32, nmc: np.ndarray) -> np.ndarray:
-    from .numerics import fma32
-    return fma32(xc, np.full_like(xc, c), np.broadcast_to(nmc[:, None], xc.shape))
+def p_of(soft: RowSoftmax, x) -> np.ndarray:
+    """p of arbitrary processed logits under the row's constants."""
+    return native.p_of(x, soft.cd, soft.mcmax, soft.s)
 
 
 def p_at(soft: RowSoftmax, idx: int) -> np.float32:
     """p of one element recomputed from its logit (what the kernels do for a
-    single token): RN(exp2q(fma(x, c, -mc_j)) * g_j)."""
-    from .numerics import fma32
-    j = idx // CHUNK
-    t = fma32(soft.x[idx], soft.c, -soft.mc_chunks[j])
-    return F32(exp2q(t) * soft.g_chunks[j])
+    single token)."""
+    return F32(p_of(soft, soft.x[idx : idx + 1])[0])
 
 
 def threshold_fx(top_p: float) -> int:
@@ -188,15 +185,13 @@ def top_p_cutoff(p: np.ndarray, top_p: float) -> tuple[np.float32, int]:
     p = np.asarray(p, dtype=F32)
     w = fx46(p)
     thr = threshold_fx(top_p)
-    vals, inv = np.unique(p, return_inverse=True)  # ascending unique values
-    mass = np.zeros(len(vals), dtype=object)
-    np.add.at(mass, inv, w.astype(object))
-    cum = 0
-    for j in range(len(vals) - 1, -1, -1):
-        cum += int(mass[j])
-        if cum >= thr:
-            return F32(vals[j]), cum
-    return F32(vals[0]), cum
+    order = np.argsort(-p, kind="stable")  # descending values
+    cum = np.cumsum(w[order], dtype=np.uint64)  # exact: the total is below 2^47
+    idx = int(np.searchsorted(cum, np.uint64(thr), side="left"))
+    if idx >= len(p):
+        return F32(p.min()), int(cum[-1])
+    c = F32(p[order[idx]])
+    return c, int(w[p >= c].sum(dtype=np.uint64))
 
 
 def top_k_value(p: np.ndarray, top_k: int) -> np.float32:
@@ -210,8 +205,11 @@ def retained_mass(p: np.ndarray, c: np.float32) -> int:
 
 
 def normalize_retained(p: np.ndarray, c: np.float32, mass_fx: int) -> np.ndarray:
-    """values >= c divided by the retained mass, else 0 (sampler.py:424)."""
+    """values >= c divided by the retained mass, else 0 (sampler.py:424); a
+    row whose retained mass is 0 (no finite logit) filters to all zeros."""
     p = np.asarray(p, dtype=F32)
+    if mass_fx == 0:
+        return np.zeros_like(p)
     mass = mass_to_f32(mass_fx)
     return np.where(p >= c, (p / mass).astype(F32), F32(0)).astype(F32)
 
@@ -344,7 +342,7 @@ def speculative_verify(target_logits, draft_logits, draft_tokens, uniforms, temp
         rows_d = [filter_row(process_logits(d[b, i], temperature, penalty, hist, epv), top_p, top_k)
                   for i in range(k)]
         for j, r in enumerate(rows_t + rows_d):
-            cut[b, j], mas[b, j], mx[b, j], nrm[b, j] = r.cutoff, r.mass_fx, r.soft.m, r.soft.s
+            cut[b, j], mas[b, j], mx[b, j], nrm[b, j] = r.cutoff, r.mass_fx, r.soft.mcmax, r.soft.s
         a = 0
         while a < k:
             x = int(xs[b, a])
@@ -450,4 +448,4 @@ def rejection_run(first, target, second, token: int, has_second: bool, u0: float
     return (int(token) if a else sampled, int(a), int(has_second and not a))
 
 
-__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "exp2q", "CHUNK"]
+__all__ = [n for n in dir() if not n.startswith("_")] + ["FX_BITS", "F64", "exp2m", "exp2p", "CHUNK"]

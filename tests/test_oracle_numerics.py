@@ -52,33 +52,64 @@ def test_fma32_midpoint_cases():
     assert naive != np.float32(1 + 2 ** -11 + 2 ** -23)
 
 
-def test_exp2_accuracy_and_special_points():
+def _exp2_ulp_error(f, t):
+    ref = np.exp2(t.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    return np.abs(f(t).astype(np.float64) - ref) / ulp
+
+
+@pytest.mark.parametrize("which,bound", [("exp2m", 4.0), ("exp2p", 2.5)])
+def test_exp2_accuracy_and_special_points(which, bound):
+    f = getattr(nm, which)
     rng = np.random.default_rng(1)
     t = np.concatenate([
         -rng.random(200000).astype(np.float32) * 126,
         -rng.random(50000).astype(np.float32) * 2,
-        np.float32([0.0, -0.0, -1e-30, -0.5, -1.5, -2.5, -0.49999997, -125.5, -126.0]),
+        np.float32([0.0, -0.0, -1e-30, -0.5, -1.5, -2.5, -0.49999997, -125.5, -126.0, 0.49999997]),
     ]).astype(np.float32)
-    e, k = nm.exp2q_k(t)
-    ref = np.exp2(t.astype(np.float64))
-    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
-    err = np.abs(e.astype(np.float64) - ref) / ulp
-    assert err.max() <= 4.0, err.max()
-    # k is the rounded argument (half to even) and e / 2^k is the polynomial's range
-    assert np.array_equal(k, np.rint(t).astype(np.int32))
-    scaled = np.ldexp(e.astype(np.float64), -k)
-    assert scaled.min() >= 2 ** -0.5 * (1 - 1e-6) and scaled.max() <= nm.EXP2_POLY_MAX
+    assert _exp2_ulp_error(f, t).max() <= bound
     # integers are exact powers of two; the floor, -inf and NaN give 0
     ints = -np.arange(0, 127, dtype=np.float32)
-    assert np.array_equal(nm.exp2q(ints), np.ldexp(np.float32(1), ints.astype(np.int32)).astype(np.float32))
-    assert (nm.exp2q(np.float32([-200.0, -1e30, -np.inf, np.nan])) == 0).all()
-    assert nm.exp2q(np.float32([-149.0]))[0] == np.float32(2.0 ** -149)  # denormals keep their exact value
-    # e^(x/T) = 2^(c x): the temperature scale agrees with the natural exponential
+    assert np.array_equal(f(ints), np.ldexp(np.float32(1), ints.astype(np.int32)).astype(np.float32))
+    assert (f(np.float32([-200.0, -1e30, -np.inf, np.nan])) == 0).all()
+    assert f(np.float32([-149.0]))[0] == np.float32(2.0 ** -149)  # denormals keep their exact value
+    # e^(x/T) = 2^(cd x): the temperature scale agrees with the natural exponential
     x = (rng.standard_normal(10000) * 3).astype(np.float32)
-    c = np.float32(nm.LOG2E * (np.float32(1) / np.float32(0.7)))
-    got = nm.exp2q(nm.fma32(x, c, np.float32(0)))
-    want = np.exp(x.astype(np.float64) / 0.7)
+    cd, c = nm.scale_of(0.7)
+    got = f(nm.fma32(x, c, np.float32(0)))
+    want = np.exp(x.astype(np.float64) / float(np.float32(0.7)))
     assert np.max(np.abs(got / want - 1)) < 3e-6
+    assert c == np.float32(cd) and cd == nm.LOG2E_D / float(np.float32(0.7))
+
+
+def test_exp2p_monotone_exhaustive():
+    """exp2p never decreases: every binary32 t from -201 to 1 (2.2e9 values)
+    -- what makes p a monotone function of the logit."""
+    from oracle import native
+
+    n, reversals, max_rel = native.exp2p_check(-201.0, 1.0)
+    assert n > 2_000_000_000
+    assert reversals == 0
+    assert max_rel < 2.5 * 2.0 ** -24
+
+
+def test_exp2m_not_monotone_but_candidate_safe():
+    """The binary32 polynomial of exp2m is not monotone (which is why p uses
+    exp2p), but it never drops below 1 on [0, 1/2] nor below 1/2 on [-1/2, 0]
+    (exhaustive over binary32 r): so t >= -L implies exp2m(t) >= 2^-L, the
+    property the chunk pass's candidate rule rests on."""
+    from oracle import native
+
+    lo_min, _ = native.exp2m_poly_range(-0.5, 0.0)
+    hi_min, hi_max = native.exp2m_poly_range(0.0, 0.5)
+    assert lo_min >= 0.5 and hi_min >= 1.0 and hi_max < 1.5
+    t = np.float32([-0.0, 0.5, 1.0]) - 7
+    assert (nm.exp2m(t) >= np.float32(2.0 ** -7)).all()
+    # one of the one-ulp reversals of the binary32 polynomial
+    a = np.float32(float.fromhex("-0x1.ffff96p-2"))
+    b = np.nextafter(a, np.float32(1))
+    assert nm.exp2m(np.float32([b]))[0] < nm.exp2m(np.float32([a]))[0]
+    assert nm.exp2p(np.float32([b]))[0] >= nm.exp2p(np.float32([a]))[0]
 
 
 def test_tree_sum_order():
@@ -126,18 +157,3 @@ def test_philox_known_answers():
     u = philox.uniforms((1000,), seed=5)
     assert u.dtype == np.float32 and (u >= 0).all() and (u < 1).all()
     assert np.array_equal(philox.uniforms((10,), seed=5, offset=3), u[3:13])
-
-
-def test_exp2_polynomial_bound_for_candidate_scale():
-    """The chunk kernel keeps every e >= 1.41422 * 2^-K as a candidate and
-    relies on e < 1.41422 * 2^k whenever exp2q scaled by 2^k: the polynomial
-    must stay below 1.41422 on [-1/2, 1/2]. Exhaustive over the binary32
-    arguments of [1/4, 1/2] (where the maximum lies), sampled below."""
-    top = np.arange(np.float32(0.25).view(np.uint32), np.float32(0.5).view(np.uint32) + 1,
-                    dtype=np.uint32).view(np.float32)
-    low = np.linspace(-0.5, 0.25, 200001, dtype=np.float64).astype(np.float32)
-    for r in (top, low):
-        p = np.full_like(r, nm.EXP2_COEFFS[5])
-        for coef in nm.EXP2_COEFFS[4::-1]:
-            p = nm.fma32(p, r, coef)
-        assert float(p.max()) < 1.41422

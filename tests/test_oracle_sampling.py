@@ -20,9 +20,8 @@ def test_softmax_matches_torch():
         ref64 = torch.softmax(x[r].double(), -1).numpy()
         ref32 = torch.softmax(x[r], -1).numpy()
         big = ref64 > 1e-30
-        # x - max is rounded to binary32 first (as torch's fp32 softmax does): for
-        # |x - max| ~ 24 that alone is ~1e-6 relative in exp(.)
-        assert np.max(np.abs(soft.p[big] - ref64[big]) / ref64[big]) < 3e-6
+        # only the binary32 rounding of the exponent and exp2p's 2.5 ulp remain
+        assert np.max(np.abs(soft.p[big] - ref64[big]) / ref64[big]) < 2e-6
         assert np.max(np.abs(soft.p[big] - ref32[big]) / ref32[big]) < 1e-5  # the contract tolerance
 
 
@@ -47,6 +46,32 @@ def test_chunk_mass_order():
     assert os_.chunk_mass(e, 8) == np.float32(1 + 2.0 ** -23)
 
 
+@pytest.mark.parametrize("epv", [4, 8])
+def test_native_chunk_masses_follow_the_declared_order(epv):
+    """The C core's M_j is chunk_mass(exp2m(fma32(x, c, -mc_j))) (numpy) for
+    every chunk, including a partial last one, and mcmax / S are the declared
+    combination of the chunk records."""
+    rng = np.random.default_rng(epv)
+    x = (rng.standard_normal(3 * os_.CHUNK + 1000) * 4).astype(np.float32)
+    pr = os_.process_logits(x, 0.7, epv=epv)
+    soft = os_.softmax_row(pr)
+    xp = np.full(4 * os_.CHUNK, -np.inf, np.float32)
+    xp[: len(x)] = pr.x
+    for j in range(4):
+        xc = xp[j * os_.CHUNK:(j + 1) * os_.CHUNK]
+        mc = np.float32(np.max(xc) * pr.c)
+        e = nm.exp2m(nm.fma32(xc, pr.c, -mc))
+        assert soft.mass_chunks[j] == os_.chunk_mass(e, epv), j
+        assert soft.m_chunks[j] == np.max(xc)
+    assert soft.mcmax == np.max(soft.mc_chunks)
+    slots = np.zeros(256, np.float32)
+    slots[0:8:2] = (nm.exp2m((soft.mc_chunks - soft.mcmax).astype(np.float32)) * soft.mass_chunks).astype(np.float32)
+    assert soft.s == nm.tree_sum_f32(slots)
+    # p of each logit from the row constants: exp2p of the binary64 exponent
+    t = np.float32((pr.x.astype(np.float64) * pr.cd) - np.float64(soft.mcmax))
+    assert np.array_equal(soft.p, (nm.exp2p(t) / soft.s).astype(np.float32))
+
+
 def test_chunked_softmax_closed_forms():
     c = os_.CHUNK
     # A zero row of 3 chunks + 5: every e = 1, M = (2048, 2048, 2048, 5),
@@ -55,51 +80,129 @@ def test_chunked_softmax_closed_forms():
     soft = os_.softmax_row(np.zeros(v, np.float32))
     assert np.array_equal(soft.mass_chunks, np.float32([c, c, c, 5])) and soft.s == np.float32(v)
     assert np.all(soft.p == np.float32(1) / np.float32(v))
-    # Zeros next to a maximum whose scaled value rounds to 1: t = -1 exactly,
-    # so their e is exactly 1/2.
-    x = np.zeros(c, np.float32)
-    x[0] = np.float32(1.0) / nm.LOG2E
-    soft = os_.softmax_row(x)
-    assert soft.mc_chunks[0] == 1 and soft.e[0] == 1 and np.all(soft.e[1:] == np.float32(0.5))
     # A chunk of -inf contributes nothing and the others are unaffected; the
     # maximum may sit in any chunk.
     x = (np.random.default_rng(2).standard_normal(3 * c) * 2).astype(np.float32)
     x[c:2 * c] = -np.inf
     x[2 * c + 7] = 30.0
     soft = os_.softmax_row(x)
-    assert soft.f_chunks[1] == 0 and soft.mass_chunks[1] == 0 and not soft.p[c:2 * c].any()
-    assert soft.f_chunks[2] == 1 and soft.p.argmax() == 2 * c + 7
+    assert soft.mass_chunks[1] == 0 and not soft.p[c:2 * c].any()
+    assert soft.p.argmax() == 2 * c + 7
     ref = torch.softmax(torch.from_numpy(x).double(), -1).numpy()
     big = ref > 1e-30
-    assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 3e-6
-    # The normaliser is sum_j f_j M_j to binary32 accuracy, and p sums to 1.
-    s64 = sum(float(soft.f_chunks[j]) * float(soft.mass_chunks[j]) for j in range(3))
-    assert abs(float(soft.s) / s64 - 1) < 1e-6
+    assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 2e-6
+    # p sums to 1; p of a single element recomputed from its logit is the row's value.
     assert abs(float(soft.p.astype(np.float64).sum()) - 1.0) < 1e-5
-    # p of a single element recomputed from its logit is the row's value.
     for i in (0, 5, c + 3, 2 * c + 7, 3 * c - 1):
         assert os_.p_at(soft, i) == soft.p[i]
+    # NaN logits get p = 0 and change nothing else; an all -inf row has S = 0 and p = 0
+    y = x.copy()
+    y[[3, c + 3]] = np.nan
+    sy = os_.softmax_row(y)
+    assert sy.p[3] == 0 and sy.p[c + 3] == 0
+    empty = os_.softmax_row(np.full(v, -np.inf, np.float32))
+    assert empty.s == 0 and not empty.p.any()
+    fr = os_.filter_row(np.full(v, -np.inf, np.float32), 0.7)
+    assert not fr.P.any()
 
 
-def test_softmax_layouts_and_temperature_agree_with_torch():
-    g = torch.Generator().manual_seed(4)
-    x = torch.randn(2, 128256, generator=g) * 4
-    for r in range(2):
-        for epv, temp in ((4, 1.0), (8, 0.7)):
-            soft = os_.softmax_row(os_.process_logits(x[r].numpy(), temp, epv=epv))
-            ref = torch.softmax(x[r].double() / temp, -1).numpy()
-            big = ref > 1e-30
-            assert np.max(np.abs(soft.p[big] - ref[big]) / ref[big]) < 1e-5
+def test_equal_logits_in_different_chunks_get_equal_p_and_are_kept_together():
+    """The tie defect of chunk-relative scaling: bit-identical logits in
+    different 2048-chunks must get bit-identical p, and the top-p cutoff keeps
+    all of them (distributions.py:66-69, ties kept)."""
+    rng = np.random.default_rng(11)
+    for dtype_epv, scale, temp, top_p in ((4, 3.0, 1.0, 0.7), (8, 4.0, 0.7, 0.9)):
+        x = (rng.standard_normal(128256) * scale).astype(np.float32)
+        if dtype_epv == 8:
+            x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+        soft0 = os_.softmax_row(os_.process_logits(x, temp, epv=dtype_epv))
+        r0 = os_.filter_row(os_.process_logits(x, temp, epv=dtype_epv), top_p)
+        # plant the cutoff value at positions in four other chunks
+        cut_idx = int(np.flatnonzero(r0.soft.p == r0.cutoff)[0])
+        tie_pos = [5 * 2048 + 17, 20 * 2048 + 1000, 41 * 2048 + 3, 62 * 2048 + 1279]
+        x[tie_pos] = x[cut_idx]
+        pr = os_.process_logits(x, temp, epv=dtype_epv)
+        r = os_.filter_row(pr, top_p)
+        vals = r.soft.p[[cut_idx] + tie_pos]
+        assert np.all(vals == vals[0])
+        assert np.all(r.P[[cut_idx] + tie_pos] > 0) or np.all(r.P[[cut_idx] + tie_pos] == 0)
+        # every logit equal to one in the support is in the support
+        kept = np.flatnonzero(r.P > 0)
+        assert np.all(r.P[np.isin(pr.x, pr.x[kept])] > 0)
+        del soft0
+
+
+def test_p_is_monotone_in_the_logit():
+    """A larger logit never gets a smaller p (sorting by logit sorts p), on
+    rows of both storage layouts, a temperature and near-ties in different chunks."""
+    rng = np.random.default_rng(12)
+    for epv, temp in ((4, 1.0), (8, 0.7), (4, 1.7)):
+        x = (rng.standard_normal(128256) * 4).astype(np.float32)
+        x[::997] = np.nextafter(x[::997], np.float32(np.inf))  # one-ulp neighbours
+        soft = os_.softmax_row(os_.process_logits(x, temp, epv=epv))
+        order = np.argsort(soft.x, kind="stable")
+        assert np.all(np.diff(soft.p[order]) >= 0)
 
 
 def test_temperature_and_penalty_closed_form():
     x = np.float32([-2.0, -0.5, 0.0, 0.5, 3.0])
     y = os_.process_logits(x, temperature=0.7, penalty=1.1, history=[0, 3, 3, 4])
-    inv_r = np.float32(1) / np.float32(1.1)
-    want = np.float32([np.float32(-2.0 * np.float32(1.1)), -0.5, 0.0, np.float32(0.5 * inv_r), np.float32(3.0 * inv_r)])
-    assert np.array_equal(y.x, want)
-    assert y.c == np.float32(nm.LOG2E * (np.float32(1) / np.float32(0.7)))
+    r = Fraction(float(np.float32(1.1)))
+    want = [exact_rne_f32(Fraction(-2.0) * r), -0.5, 0.0, exact_rne_f32(Fraction(0.5) / r),
+            exact_rne_f32(Fraction(3.0) / r)]
+    assert np.array_equal(y.x, np.float32(want))
+    assert np.array_equal(y.pen, [True, False, False, True, True])
+    cd, c = nm.scale_of(0.7)
+    assert y.cd == cd and y.c == c == np.float32(nm.LOG2E_D / float(np.float32(0.7)))
     assert np.array_equal(os_.process_logits(x, 1.0).x, x) and os_.process_logits(x, 1.0).c == nm.LOG2E
+
+
+def test_penalty_bit_equal_to_reference_formulation():
+    """x / r (not x * RN(1/r)) on every penalised logit: bit-equal to the
+    torch restatement of transformers' closed form on seeded rows."""
+    g = torch.Generator().manual_seed(9)
+    v = 32000
+    x = torch.randn(6, v, generator=g) * 4
+    hist = torch.randint(0, v, (3000,), generator=g)
+    for pen in (1.1, 1.3, 0.8):
+        pt = torch_ref.apply_penalty(x, hist, pen).numpy()
+        po = np.stack([os_.apply_penalty(x[r].numpy(), hist.numpy(), pen) for r in range(6)])
+        assert np.array_equal(pt, po), pen
+
+
+def test_penalised_subchunk_mass_order():
+    """PM_j: each lane adds its penalised e' (relative to the penalised max)
+    one by one in (vector, element) order, then the lanes pairwise."""
+    rng = np.random.default_rng(13)
+    for epv in (4, 8):
+        x = (rng.standard_normal(2048) * 3).astype(np.float32)
+        hist = rng.choice(2048, 300, replace=False)
+        pr = os_.process_logits(x, 0.9, penalty=1.2, history=hist, epv=epv)
+        soft = os_.softmax_row(pr)
+        pen = pr.pen
+        pm = np.max(pr.x[pen])
+        pmc = np.float32(pm * pr.c)
+        ep = nm.exp2m(nm.fma32(pr.x, pr.c, -pmc))
+        nvc = 2048 // (64 * epv)
+        lanes = np.zeros(64, np.float32)
+        for t in range(64):
+            acc = np.float32(0)
+            for u in range(nvc):
+                for e in range(epv):
+                    i = (u * 64 + t) * epv + e
+                    if pen[i]:
+                        acc = np.float32(acc + ep[i])
+            lanes[t] = acc
+        assert soft.pmass_chunks[0] == nm.tree_sum_f32(lanes), epv
+        assert soft.pm_chunks[0] == pm and soft.m_chunks[0] == np.max(pr.x[~pen])
+        # the penalised tokens' p is a function of their processed logit too
+        assert np.array_equal(soft.p, os_.p_of(soft, pr.x))
+
+
+def exact_rne_f32(x: Fraction) -> np.float32:
+    from tests.test_oracle_numerics import exact_rne_f32 as f
+
+    return f(x)
 
 
 def brute_cutoff(p, top_p):
@@ -326,8 +429,8 @@ def test_conditional_residual_matches_triton_restatement():
 
 
 def test_penalised_speculative_verify_matches_torch_reference():
-    """The repetition penalty in both restatements (x * RN(1/r) vs x / r differ
-    by at most an ulp) leaves accept lengths and tokens equal on seeded rows."""
+    """With the repetition penalty, accept lengths and tokens equal the
+    reference formulation's on seeded rows."""
     from loopspec_amd import philox
 
     g = torch.Generator().manual_seed(9)
@@ -338,7 +441,7 @@ def test_penalised_speculative_verify_matches_torch_reference():
     x = torch.randn(3, v, generator=g) * 4
     pt = torch_ref.apply_penalty(x, hists[1], 1.1)
     po = np.stack([os_.apply_penalty(x[r].numpy(), hists[1].numpy(), 1.1) for r in range(3)])
-    assert np.allclose(pt.numpy(), po, rtol=2e-7, atol=0)
+    assert np.array_equal(pt.numpy(), po)
     drafts = torch.zeros(b, k, dtype=torch.int64)
     du = torch.from_numpy(philox.uniforms((b, k), seed=5))
     for i in range(b):
@@ -350,3 +453,59 @@ def test_penalised_speculative_verify_matches_torch_reference():
                                  [h.numpy() for h in hists])
     assert np.array_equal(res.accept_len, a_ref.numpy())
     assert np.array_equal(res.tokens, t_ref.numpy())
+
+
+def _exact_support(row64: np.ndarray, top_p: float) -> np.ndarray:
+    """Top-p support of the exact (binary64) softmax of a processed row."""
+    e = np.exp(row64 - row64.max())
+    p = e / e.sum()
+    srt = np.sort(p)[::-1]
+    idx = min(int(np.searchsorted(np.cumsum(srt), top_p, side="left")), len(p) - 1)
+    return p >= srt[idx]
+
+
+FULL_SHAPE_CASES = [("C3", 0), ("C3", 1), ("C4", 5), ("C4", 2000), ("C4", 2001), ("C4", 2002), ("C4", 2003),
+                    ("C4", 2004)]
+
+
+@pytest.mark.parametrize("name,seed", FULL_SHAPE_CASES)
+def test_full_shape_parity_with_reference_formulation(name, seed):
+    """Declared arithmetic vs the reference's own torch formulation
+    (oracle.torch_ref) at the full BASELINE shapes: identical accept lengths
+    and tokens; every row keeps the same top-p set, except rows where the
+    reference's binary32 cumulative mass crosses top_p at another index than
+    the exact (binary64) softmax does -- a cumulative-mass boundary case, in
+    which the declared arithmetic must keep the exact set."""
+    from loopspec_amd import workloads as W
+
+    cfg = {"C3": W.C3, "C4": W.C4}[name]
+    inp = W.sampling_inputs(cfg, seed)
+    b_n, k = cfg.batch, cfg.k
+    epv = 8 if cfg.dtype == torch.bfloat16 else 4
+    tl, dl = inp["target"].float(), inp["draft"].float()
+    hist = None
+    if cfg.penalty != 1.0:
+        hist = [inp["history"][i, : int(inp["history_len"][i])] for i in range(b_n)]
+    drafts = torch.zeros(b_n, k, dtype=torch.int64)
+    boundary = 0
+    for i in range(b_n):
+        rows = torch.cat([tl[i], dl[i]])
+        if hist is not None:
+            rows = torch_ref.apply_penalty(rows, hist[i], cfg.penalty)
+        ref = torch_ref.filtered_probabilities(rows, cfg.temperature, 1 << 30, cfg.top_p)
+        h = None if hist is None else hist[i].numpy()
+        for r in range(2 * k + 1):
+            src = tl[i, r] if r <= k else dl[i, r - k - 1]
+            ours = os_.filter_row(os_.process_logits(src.numpy(), cfg.temperature, cfg.penalty, h, epv), cfg.top_p)
+            if not np.array_equal(ours.P > 0, ref[r].numpy() > 0):
+                exact = _exact_support(rows[r].double().numpy() / float(np.float32(cfg.temperature)), cfg.top_p)
+                assert np.array_equal(ours.P > 0, exact), (i, r)
+                boundary += 1
+        drafts[i] = torch_ref.categorical_pick(ref[k + 1:], inp["draft_uniforms"][i])
+    a_ref, t_ref = torch_ref.speculative_verify(tl, dl, drafts, inp["uniforms"], cfg.temperature, cfg.top_p,
+                                                cfg.penalty, hist)
+    res = os_.speculative_verify(tl.numpy(), dl.numpy(), drafts.numpy(), inp["uniforms"].numpy(), cfg.temperature,
+                                 cfg.top_p, cfg.penalty, None if hist is None else [x.numpy() for x in hist], epv=epv)
+    assert np.array_equal(res.accept_len, a_ref.numpy())
+    assert np.array_equal(res.tokens, t_ref.numpy())
+    assert boundary <= 2, boundary

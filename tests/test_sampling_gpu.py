@@ -107,68 +107,115 @@ def test_filter_logits_edge_rows(gpu, case):
         assert res["cutoff"][r].item() == want.cutoff
 
 
-def test_filter_logits_repair_and_slow_rows(gpu):
-    """Rows whose candidates' cutoff misses the worst-case bound: re-checked
-    chunk by chunk (repair), with the deficient chunks' candidates rebuilt
-    (rebuild), or selected exactly over the row (slow)."""
-    rows = candidates.repair_rows()
-    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["repair"][::-1].copy(), rows["rebuild"],
-                                   rows["rebuild"][::-1].copy()]))
-    announce("filter repair/slow rows")
-    res = verify.filter_logits(x.to(gpu), 1.0, 0.9, want_probs=True)
+@pytest.mark.parametrize("path", ["fast", "refill", "slow_list", "slow_dense"])
+def test_filter_and_sample_each_path(gpu, path):
+    """Rows built to take each finalisation path (tests/candidates.py)."""
+    row, top_p = candidates.path_rows()[path]
+    x = torch.from_numpy(np.stack([row, row[::-1].copy(), row]))
+    announce(f"filter/sample path {path}")
+    res = verify.filter_logits(x.to(gpu), 1.0, top_p, want_probs=True)
+    u = torch.from_numpy(philox.uniforms((3,), seed=21))
+    got = verify.sample_logits(x.to(gpu), u.to(gpu), 1.0, top_p)
     torch.cuda.synchronize()
-    for r in range(x.shape[0]):
-        want = oracle_filter(x[r].numpy(), 1.0, 0.9)
+    for r in range(3):
+        want = oracle_filter(x[r].numpy(), 1.0, top_p)
+        assert np.array_equal(res["probs"][r].cpu().numpy(), want.soft.p), r
         assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
         assert res["cutoff"][r].item() == want.cutoff, r
         assert res["mass"][r].item() == nm.mass_to_f32(want.mass_fx), r
+        assert got[r].item() == osmp.categorical_pick(want.P, u[r].item()), r
 
 
-def test_sample_and_spec_repair_and_slow_rows(gpu):
-    rows = candidates.repair_rows()
-    v = rows["repair"].shape[0]
-    x = torch.from_numpy(np.stack([rows["repair"], rows["slow"], rows["rebuild"]] * 4))
-    u = torch.from_numpy(philox.uniforms((x.shape[0],), seed=21))
-    announce("sample repair/slow rows")
-    got = verify.sample_logits(x.to(gpu), u.to(gpu), 1.0, 0.9)
-    torch.cuda.synchronize()
-    want = [osmp.categorical_pick(oracle_filter(x[r].numpy(), 1.0, 0.9).P, u[r].item()) for r in range(x.shape[0])]
-    assert got.cpu().tolist() == want
-    # spec verify, B=6, k=1: target rows (pos 0, bonus) and draft rows from the three kinds
-    cfg = workloads.SamplingConfig("repair", 6, 1, v, torch.float32, 1.0, 0.9)
+@pytest.mark.parametrize("path", ["refill", "slow_list", "slow_dense"])
+def test_spec_each_path(gpu, path):
+    """Spec verify with target and draft rows of one path: the accept test,
+    the residual over that path's support and the bonus draw."""
+    row, top_p = candidates.path_rows()[path]
+    v = row.shape[0]
+    fast, _ = candidates.path_rows()["fast"]
+    other = np.resize(fast, v)
+    cfg = workloads.SamplingConfig(path, 6, 1, v, torch.float32, 1.0, top_p)
     inp = workloads.sampling_inputs(cfg, 13)
-    kinds = ["repair", "slow", "rebuild"]
     for b in range(6):
-        inp["target"][b, 0] = torch.from_numpy(rows[kinds[b % 3]])
-        inp["target"][b, 1] = torch.from_numpy(rows[kinds[(b + 1) % 3]])
-        inp["draft"][b, 0] = torch.from_numpy(rows[kinds[(b // 2) % 3]])
+        inp["target"][b, 0] = torch.from_numpy(row if b % 2 == 0 else other)
+        inp["target"][b, 1] = torch.from_numpy(row if b % 3 == 0 else other)
+        inp["draft"][b, 0] = torch.from_numpy(row if b < 3 else row[::-1].copy())
     drafts = draft_tokens_from(inp, cfg)
-    announce("spec repair/slow rows")
+    if path == "slow_dense":
+        inp["uniforms"][:3, 0] = 0.9999999  # rejections: residuals over the dense support
+    announce(f"spec path {path}")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
     want = oracle_spec(cfg, inp, drafts)
     assert np.array_equal(acc, want.accept_len)
     assert np.array_equal(tok, want.tokens)
 
 
+def test_planted_cross_chunk_ties_at_the_cutoff(gpu):
+    """Bit-identical logits in different chunks at the top-p cutoff: equal p,
+    kept together (distributions.py:66-69), in filter and sample."""
+    rng = np.random.default_rng(31)
+    v = 128256
+    x = torch.from_numpy((rng.standard_normal((4, v)) * 4).astype(np.float32)).to(torch.bfloat16)
+    tie_pos = [5 * 2048 + 17, 20 * 2048 + 1000, 41 * 2048 + 3, 62 * 2048 + 1279]
+    for r in range(4):
+        first = oracle_filter(x[r].float().numpy(), 0.7, 0.9, epv=8)
+        ci = int(np.flatnonzero(first.soft.p == first.cutoff)[0])
+        x[r, tie_pos] = x[r, ci].clone()
+    announce("filter planted cross-chunk ties")
+    res = verify.filter_logits(x.to(gpu), 0.7, 0.9, want_probs=True)
+    u = torch.from_numpy(philox.uniforms((4,), seed=32))
+    got = verify.sample_logits(x.to(gpu), u.to(gpu), 0.7, 0.9)
+    torch.cuda.synchronize()
+    for r in range(4):
+        want = oracle_filter(x[r].float().numpy(), 0.7, 0.9, epv=8)
+        gp = res["probs"][r].cpu().numpy()
+        gf = res["filtered"][r].cpu().numpy()
+        assert np.array_equal(gf, want.P), r
+        assert np.all(gp[tie_pos] == gp[tie_pos[0]])
+        assert np.all(gf[tie_pos] > 0) or np.all(gf[tie_pos] == 0)
+        # the whole support is closed under equal logits
+        xf = x[r].float().numpy()
+        assert np.all(gf[np.isin(xf, xf[gf > 0])] > 0)
+        assert got[r].item() == osmp.categorical_pick(want.P, u[r].item())
+
+
+def clamp_row(vocab: int = 4096) -> np.ndarray:
+    """A row whose exact retained mass stays below fx46(1 - 2^-24): one
+    logit 0 and the rest at a value where exp2m (the chunk masses) rounds
+    high against exp2p (the probabilities), so the p sum a little under 1."""
+    x = np.full(vocab, np.float32(-0.014630884863436222), dtype=np.float32)
+    x[0] = 0.0
+    return x
+
+
 def test_top_p_just_below_one(gpu):
-    """top_p = 1 - 2^-24: on many rows the exact retained masses sum below it,
-    so no cutoff reaches top_p and the whole row is kept (cutoff = min p)."""
+    """top_p = 1 - 2^-24: on a row whose exact total mass is below it no
+    cutoff reaches top_p, and the reference clamps to the last sorted value,
+    keeping the whole row (cutoff = min p); Gaussian rows reach it."""
     top_p = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
     g = torch.Generator().manual_seed(77)
-    x = torch.randn(8, 49152, generator=g) * 3
+    x = torch.randn(6, 4096, generator=g) * 3
+    x[0] = torch.from_numpy(clamp_row())
+    x[3] = torch.from_numpy(clamp_row()[::-1].copy())
+    want0 = oracle_filter(x[0].numpy(), 1.0, top_p)
+    assert int(nm.fx46(want0.soft.p).sum(dtype=np.uint64)) < osmp.threshold_fx(top_p)
+    assert want0.cutoff == want0.soft.p.min()
     announce("filter top_p just below one")
     res = verify.filter_logits(x.to(gpu), 1.0, top_p, want_probs=True)
+    u = torch.from_numpy(philox.uniforms((6,), seed=78))
+    got = verify.sample_logits(x.to(gpu), u.to(gpu), 1.0, top_p)
     torch.cuda.synchronize()
-    kept_all = 0
-    for r in range(x.shape[0]):
+    for r in range(6):
         want = oracle_filter(x[r].numpy(), 1.0, top_p)
-        kept_all += int(want.cutoff == want.soft.p.min())
         assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
         assert res["cutoff"][r].item() == want.cutoff, r
         assert res["mass"][r].item() == nm.mass_to_f32(want.mass_fx), r
-    assert kept_all > 0  # the whole-row case was exercised
-    cfg = workloads.SamplingConfig("near1", 4, 2, 49152, torch.float32, 1.0, top_p)
+        assert got[r].item() == osmp.categorical_pick(want.P, u[r].item()), r
+    cfg = workloads.SamplingConfig("near1", 4, 2, 4096, torch.float32, 1.0, top_p)
     inp = workloads.sampling_inputs(cfg, 17)
+    inp["target"][1, 0] = torch.from_numpy(clamp_row())
+    inp["draft"][2, 1] = torch.from_numpy(clamp_row())
+    inp["target"][3, 2] = torch.from_numpy(clamp_row())
     drafts = draft_tokens_from(inp, cfg)
     announce("spec top_p just below one")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
@@ -234,12 +281,15 @@ def test_spec_verify_c3_full_shape(gpu, seed):
     assert np.array_equal(tok, want.tokens)
 
 
-def test_spec_verify_c4_like_with_penalty(gpu):
-    cfg = workloads.SamplingConfig("c4s", 4, 4, 128256, torch.bfloat16, 0.7, 0.9, penalty=1.1, target_std=4.0,
-                                   hist_min=256, hist_max=4096)
-    inp = workloads.sampling_inputs(cfg, 5)
+@pytest.mark.parametrize("seed", [5, 2003])
+def test_spec_verify_c4_full_shape(gpu, seed):
+    """Full C4: B=32, k=4, V=128256 bf16, T=0.7, top_p=0.9, repetition 1.1 over
+    Zipf histories (seeds 5 and 2003 emitted a different token than the
+    reference before every p became a function of its logit)."""
+    cfg = workloads.C4
+    inp = workloads.sampling_inputs(cfg, seed)
     drafts = draft_tokens_from(inp, cfg)
-    announce("spec C4-like")
+    announce(f"spec C4 full seed={seed}")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
     want = oracle_spec(cfg, inp, drafts)
     assert np.array_equal(acc, want.accept_len)
@@ -363,20 +413,21 @@ def test_spec_verify_empty_batch(gpu):
     assert acc.shape == (0,) and tok.shape == (0, 3)
 
 
-def test_spec_verify_more_workgroups_than_cus(gpu):
-    """B=100, k=3: 400 row workgroups, more than the CUs, so the build for two
-    workgroups per CU runs; rows taking the repair, rebuild and slow paths are
-    planted so its out-of-line slow path runs too."""
-    rows = candidates.repair_rows()
-    v = rows["repair"].shape[0]
-    cfg = workloads.SamplingConfig("many", 100, 3, v, torch.float32, 1.0, 0.9)
+def test_spec_verify_many_units_with_planted_paths(gpu):
+    """B=100, k=3 (400 units over the persistent workgroups), with rows taking
+    the refill and whole-row paths planted among fast ones."""
+    rows = candidates.path_rows()
+    refill, _ = rows["refill"]
+    v = refill.shape[0]
+    cfg = workloads.SamplingConfig("many", 100, 3, v, torch.float32, 1.0, 0.5)
     inp = workloads.sampling_inputs(cfg, 23)
-    kinds = ["repair", "slow", "rebuild"]
+    slow = np.resize(rows["slow_list"][0], v)
+    kinds = [refill, slow, refill[::-1].copy()]
     for b in range(0, 100, 7):
-        inp["target"][b, b % 4] = torch.from_numpy(rows[kinds[b % 3]])
-        inp["draft"][b, b % 3] = torch.from_numpy(rows[kinds[(b + 1) % 3]])
+        inp["target"][b, b % 4] = torch.from_numpy(kinds[b % 3])
+        inp["draft"][b, b % 3] = torch.from_numpy(kinds[(b + 1) % 3])
     drafts = draft_tokens_from(inp, cfg)
-    announce("spec verify 400 row workgroups")
+    announce("spec verify 400 units with planted paths")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
     want = oracle_spec(cfg, inp, drafts)
     assert np.array_equal(acc, want.accept_len)
