@@ -1,39 +1,39 @@
 // (a) logit processing and (c) lossless speculative sampling for gfx950.
 //
 // Launches per call: bitmap_kernel (with a repetition penalty: each batch
-// element's token history as a vocabulary bitmap), then fused_kernel, then,
-// for dense outputs only, dense_kernel.
+// element's token history as a vocabulary bitmap), stream_kernel, fin_kernel,
+// then, for dense outputs only, dense_kernel.
 //
-// fused_kernel is persistent. A 256-lane workgroup (four waves) takes four
-// consecutive (row, 2048-element chunk) items per step -- the first ticket
-// by its block index, the rest from eight interleaved ticket counters -- and
-// each wave streams one chunk:
-//   * its logits staged in LDS, decoded, penalised tokens set aside;
-//   * chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk mass M_j in
-//     the declared pairwise order; the penalised tokens' own max and mass
-//     (pm_j, PM_j) from a sparse pass over them (x / r or x * r);
-//   * candidates: every element with e >= 2^-L, L from a binary search on
-//     the chunk's vector maxima (at most `cap` vectors reach it), lowered
-//     until at most `cap` elements remain,
-//     written as (index, processed logit); a 32-byte record per chunk.
-// Then the wave stores drain and it arrives on its unit's counter. A unit is
-// a pair (target row i, draft row i) of a batch element (spec, i < k), the
-// bonus target row (spec, i = k) or one row (sample / dense). The workgroup
-// that brings a unit's last chunk finalises it at once, all four waves
-// together, while the other workgroups keep streaming:
-//   * row constants from the records: mcmax, S, and per chunk the largest p a
-//     non-candidate can have (exact, because p is monotone in the logit);
+// stream_kernel reads every logit once: one wave per (row, 2048-element
+// chunk) item, four independent waves per workgroup. A wave
+//   * stages its chunk in LDS, decodes it, sets penalised tokens aside;
+//   * computes the chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk
+//     mass M_j in the declared pairwise order; the penalised tokens' own max
+//     and mass (pm_j, PM_j) from a sparse pass over them (x / r or x * r);
+//   * keeps the candidates: every element with RN32(x c - mref) >= -L, mref =
+//     max(mc_j, pmc_j), L from a binary search on the chunk's vector maxima
+//     (at most `cap` vectors reach it), lowered until at most `cap` elements
+//     remain, written as (index, processed logit) into the chunk's slots;
+//     and a 32-byte record.
+// fin_kernel finalises one unit per workgroup. A unit is a pair (target row
+// i, draft row i) of a batch element (spec, i < k), the bonus target row
+// (spec, i = k) or one row (sample / dense):
+//   * the records and every candidate slot of both rows are loaded together;
+//     row constants mcmax, S and per chunk the largest p a non-candidate can
+//     have (exact, because p is monotone in the logit);
 //   * every candidate's p = RN(exp2p(RN32(fma64(x, cd, -mcmax))) / S) into
-//     LDS, the exact top-p cutoff by a three-round radix select on the
-//     binary32 bits of p with 2^-46 fixed-point masses (the value semantics
-//     of sort + cumsum + searchsorted, distributions.py:59-70);
+//     LDS, the exact top-p cutoffs of both rows by shared three-round radix
+//     selects on the binary32 bits of p with 2^-46 fixed-point masses (the
+//     value semantics of sort + cumsum + searchsorted, distributions.py:59-70);
 //   * valid when the cutoff exceeds every chunk's non-candidate bound; else
 //     the chunks whose bound reaches it are re-read and their {p >= cutoff}
 //     replaces their candidates (exact, since that cutoff is a lower bound of
 //     the row's); else the whole row is selected by passes over it;
-//   * spec: the accept bit of x_i, the residual draw on rejection, the bonus
-//     draw for i = k; the last of the k+1 units of a batch element writes its
-//     accepted length and tokens. sample: the draw. dense: the statistics.
+//   * spec: the accept bit of x_i, the residual draw on rejection (draft
+//     probabilities looked up through an LDS hash of the draft's entries),
+//     the bonus draw for i = k; the last of the k+1 units of a batch element
+//     writes its accepted length and tokens. sample: the draw. dense: the
+//     statistics.
 // The arithmetic is the declared arithmetic of ls_numerics.hpp, restated by
 // oracle/sampling.py and oracle/native/ls_oracle.c, so every output is
 // bit-identical to the oracle's.
@@ -45,7 +45,7 @@ namespace ls {
 namespace {
 
 constexpr int kChunk = 2048;               // softmax chunk (declared arithmetic)
-constexpr int kWG = 256;                   // fused workgroup
+constexpr int kWG = 256;                   // stream_kernel workgroup
 constexpr int kNW = kWG / kWave;           // waves per workgroup
 constexpr int kMaxChunks = 128;            // vocab <= 262144
 constexpr int kMaxVocab = kMaxChunks * kChunk;
@@ -53,14 +53,9 @@ constexpr int kRowCap = 2048;              // LDS entries per row in the finalis
 constexpr int kRadixBits = 10;
 constexpr int kBins = 1 << kRadixBits;     // radix digits per round
 constexpr int kMaxLevel = 31;              // candidate levels: e >= 2^-L, L in [0, 31]
-constexpr int kTickets = 8;                // ticket counters, one 64-byte line each
-constexpr int kLineU32 = 16;
-constexpr int kWgPerCu = 3;
 constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
 constexpr int64_t kMaxK = 64;
-// unit counters at a fixed place, sized for the largest call (spec: B (k+1))
-constexpr int64_t kMaxUnits = kMaxSpecBatch * (kMaxK + 1);
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
@@ -73,7 +68,7 @@ struct ChunkRec {
   float mass;       // M_j
   float pm;         // max of the penalised x (-inf if none)
   float pmass;      // PM_j
-  int32_t level;    // candidates: e >= 2^-level relative to max(mc_j, pmc_j); -1 with kChunkOverflow
+  int32_t level;    // candidates: RN32(x c - max(mc_j, pmc_j)) >= -level; -1 with kChunkOverflow
   uint32_t n;       // candidates written
   float xtok;       // processed logit of the row's draft token (kChunkHasTok)
   uint32_t flags;
@@ -95,7 +90,7 @@ struct Params {
   int64_t bstride1, pstride1;
   int mode, k, rpg;            // rpg: rows per group (spec 2k+1, else 1)
   int vocab, nch, cap;         // chunks per row, candidate slots per chunk
-  int items, tickets, groups, units;
+  int items, groups, units;
   float c;                     // RN32(cd)
   double cd;                   // RN64(log2(e) / T)
   float pen;                   // repetition penalty
@@ -122,8 +117,6 @@ struct Params {
   float* cutoff_out;
   float* mass_out;
   // workspace
-  uint32_t* ctl;       // ticket counters [kTickets lines], exit counter [1 line]
-  uint32_t* unit_cnt;  // [units]
   uint32_t* grp_cnt;   // [groups] (spec)
   ChunkRec* recs;      // [rows * nch]
   uint64_t* cands;     // [rows * nch * cap] of (index << 32 | bits(x))
@@ -231,56 +224,14 @@ __device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
 }
 
 // ---------------------------------------------------------------------------
-// Shared memory: the streaming phase and the finaliser share one region.
+// Shared memory of stream_kernel: each wave's chunk as loaded
 // ---------------------------------------------------------------------------
+template <int DT>
 struct StreamSh {
-  u32x4 stage[kNW][kChunk / 4];  // each wave's chunk as loaded (8 KB for 4-byte logits)
-};
-
-struct RowAux {
-  float mcmax, s, cut, mass_f;   // cutoff (0 unfiltered), binary32 retained mass
-  uint64_t mass_fx;
-  float bmax;                    // largest non-candidate bound
-  float xtok;
-  uint32_t n;                    // LDS entries
-  uint32_t flags;
-  uint32_t has_tok;
-  float top_p;
-};
-
-struct FinSh {
-  union {
-    ChunkRec recs[2][kMaxChunks];  // records of the unit's rows
-    uint64_t bins[kBins];          // radix bins
-    uint64_t csum[kMaxChunks];     // per-chunk weight sums of a draw
-  } u;
-  uint32_t cstart[2][kMaxChunks];  // each chunk's entries in the LDS list
-  uint32_t ccount[2][kMaxChunks];
-  float bound[2][kMaxChunks];      // per-chunk bound on the p of non-candidates
-  struct Entries {
-    uint32_t pbits[kRowCap];       // bits of p
-    uint32_t eidx[kRowCap];        // vocabulary index
-  } ent[2];                        // slot 1's 16 KB double as a draw's u64 weights
-  RowAux aux[2];
-  uint64_t red[2 * kNW];
-  uint64_t red2[2 * kNW];
-  uint32_t sel[4];
-  uint64_t sel64[4];
-  uint32_t list[kWG];              // a draw's entries of one chunk
-  uint32_t nlist;
-  uint32_t nadd;
-  int64_t token;
-};
-
-struct Sh {
-  union {
-    StreamSh st;
-    FinSh fin;
-  };
+  u32x4 stage[kNW][kChunk / Elem<DT>::kPerVec];  // the chunk's 16-byte vectors
   uint32_t pcount[kNW];
-  int32_t ready[2][kNW];
-  uint32_t ticket[3];
 };
+
 
 // ---------------------------------------------------------------------------
 // Items
@@ -325,11 +276,6 @@ __device__ __forceinline__ Item item_of(const Params& p, int it) {
     r.tok = -1;
   }
   return r;
-}
-
-__device__ __forceinline__ int unit_items(const Params& p, int unit) {
-  if (p.mode == kModeSpec) return (unit % (p.k + 1)) < p.k ? 2 * p.nch : p.nch;
-  return p.nch;
 }
 
 // Logits row of row id r (spec rows: targets 0..k, then drafts 0..k-1).
@@ -392,9 +338,8 @@ __global__ __launch_bounds__(kBmB) void bitmap_kernel(const Params p) {
 // Loads of one item (lanes past the chunk end re-read its last vector), plus,
 // with a penalty, the chunk's bitmap word t for lane t.
 template <int DT, int NVC>
-__device__ __forceinline__ void load_item(const Params& p, int it, u32x4 (&d)[NVC], uint32_t& pw) {
+__device__ __forceinline__ void load_item(const Params& p, const Item& I, u32x4 (&d)[NVC], uint32_t& pw) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  const Item I = item_of(p, it);
   const int c0 = I.chunk * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
@@ -419,25 +364,41 @@ __device__ __forceinline__ float staged(const u32x4* st, int li) {
   }
 }
 
-// One chunk item, processed by wave w. Returns the unit id if this wave's
-// arrival completed the unit, else -1 (wave-uniform).
+// exp2q(t) for a finite t: the clamp at -200 changes nothing there (both
+// forms give 0 below -200), so it is left out; a -inf or NaN operand gives
+// NaN, which the caller detects in the sum.
+__device__ __forceinline__ float exp2q_finite(float t) {
+  const float kf = __builtin_rintf(t);
+  const float r = t - kf;
+  float q = kExp2C5;
+  q = __builtin_fmaf(q, r, kExp2C4);
+  q = __builtin_fmaf(q, r, kExp2C3);
+  q = __builtin_fmaf(q, r, kExp2C2);
+  q = __builtin_fmaf(q, r, kExp2C1);
+  q = __builtin_fmaf(q, r, kExp2C0);
+  int k;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(k) : "v"(kf));  // saturating conversion
+  return __builtin_ldexpf(q, k);
+}
+
+// One chunk item, processed by wave w: its candidates and its record are
+// stored (read by fin_kernel, after this kernel). The item is wave-uniform.
 template <int DT, bool PEN>
-__device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int it, const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4],
-                           uint32_t pw) {
+__device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, int w, const Item& I,
+                                            const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4], uint32_t pw) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kWave * EPV);
   constexpr int NE = NVC * EPV;
   static_assert(NE == 32, "32 elements per lane");
   int t = threadIdx.x & (kWave - 1);
   asm volatile("" : "+v"(t));
-  const Item I = item_of(p, it);
   const int c0 = I.chunk * kChunk;
   const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
   const int nvc = nel / EPV;
-  const bool full = nvc == NVC * kWave;
+  const bool full = nel == kChunk;  // else the row's last chunk, past-the-end lanes at -inf
 
   // 1. stage the chunk as loaded
-  u32x4* st = sh.st.stage[w];
+  u32x4* st = sh.stage[w];
 #pragma unroll
   for (int u = 0; u < NVC; ++u) st[u * kWave + t] = d[u];
 
@@ -534,16 +495,32 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
   }
   const float pmc = pm * c;
 
-  // 6. e and the chunk mass (e replaces x)
+  // 6. the exponents t = fma(x, c, -mc) (replacing x), e = exp2m(t) and the
+  //    chunk mass
   const float nmc = -mc;
 #pragma unroll
-  for (int i = 0; i < NE; ++i) x[i] = exp2q(__builtin_fmaf(x[i], c, nmc));
+  for (int i = 0; i < NE; ++i) x[i] = __builtin_fmaf(x[i], c, nmc);
   float ea[NE];
+  float mass;
+  if constexpr (PEN) {
+    // penalised elements sit at -inf: the clamped form
 #pragma unroll
-  for (int i = 0; i < NE; ++i) ea[i] = x[i];
-  const float mass = wave_tree_sum(lane_tree_sum(ea));
+    for (int i = 0; i < NE; ++i) ea[i] = exp2q(x[i]);
+    mass = wave_tree_sum(lane_tree_sum(ea));
+  } else {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) ea[i] = exp2q_finite(x[i]);
+    mass = wave_tree_sum(lane_tree_sum(ea));
+    if (mass != mass) {
+      // an infinite logit, or past-the-end lanes: the clamped form
+#pragma unroll
+      for (int i = 0; i < NE; ++i) ea[i] = exp2q(x[i]);
+      mass = wave_tree_sum(lane_tree_sum(ea));
+    }
+  }
 
-  // 7. the level L: candidates are the e >= 2^-L relative to mref = max(mc, pmc)
+  // 7. the level L: candidates are the elements with RN32(x c - mref) >= -L,
+  //    mref = max(mc, pmc)
   const float mref = mc > pmc ? mc : pmc;
   const bool same = mref == mc && mc > -__builtin_inff();
   const int cap = p.cap;
@@ -551,10 +528,26 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
   uint32_t mask = 0;  // bit 31 - i <-> element i (A elements)
   uint32_t cnt = 0;
   if (mref > -__builtin_inff()) {
+    const float nref = -mref;
+    if constexpr (PEN) {
+      if (!same) {
+        // the penalised maximum lies above the rest (a penalty below 1, or
+        // no other finite logit): the exponents relative to mref
+#pragma unroll
+        for (int u = 0; u < NVC; ++u) {
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) {
+            const int li = (u * kWave + t) * EPV + e;
+            float v = staged<DT>(st, li);
+            if (((hb[u] >> e) & 1u) || u * kWave + t >= nvc) v = -__builtin_inff();
+            x[u * EPV + e] = __builtin_fmaf(v, c, nref);
+          }
+        }
+      }
+    }
     // a start from the vector maxima: the largest L in [0, kMaxLevel] at
     // which at most cap of the lane vectors hold a candidate (binary search;
     // the count only grows with L)
-    const float nref = -mref;
     float tv[NVC];
 #pragma unroll
     for (int u = 0; u < NVC; ++u) tv[u] = __builtin_fmaf(vm[u], c, nref);
@@ -567,33 +560,33 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
       for (int u = 0; u < NVC; ++u) nv += __builtin_popcountll(__ballot(tv[u] >= th));
       if (nv <= static_cast<uint32_t>(cap)) lo = mid; else hi = mid - 1;
     }
-    const int Ls = lo;
-    for (L = Ls; L >= 0; --L) {
+    for (L = lo; L >= 0; --L) {
+      const float th = -static_cast<float>(L);
       mask = 0;
-      if (same) {
-        const float th = __builtin_ldexpf(1.0f, -L);
 #pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          // mask = 2 mask + (e >= th): a compare into VCC and one add with carry
-          asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
-              : "+v"(mask) : "v"(x[i]), "v"(th) : "vcc");
-        }
-      } else {
-        // the penalised maximum lies above the rest (a penalty below 1, or
-        // no other finite logit): test the exponent against mref directly
-        const float th = -static_cast<float>(L);
+      for (int i = 0; i < NE; ++i) {
+        // mask = 2 mask + (t >= th): a compare into VCC and one add with carry
+        asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
+            : "+v"(mask) : "v"(x[i]), "v"(th) : "vcc");
+      }
+      cnt = static_cast<uint32_t>(__builtin_popcount(mask));
+      uint32_t own = cnt;
+      if constexpr (PEN) {
+        // the penalised candidates at this level count against the same slots
+        if (any_hit) {
 #pragma unroll
-        for (int u = 0; u < NVC; ++u) {
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) {
-            float v = vec_elem<DT>(d[u], e);
-            if (((hb[u] >> e) & 1u) || (!full && u * kWave + t >= nvc)) v = -__builtin_inff();
-            mask = 2u * mask + (__builtin_fmaf(v, c, nref) >= th ? 1u : 0u);
+          for (int u = 0; u < NVC; ++u) {
+            uint32_t bits = hb[u];
+            while (bits) {
+              const int e = __builtin_ctz(bits);
+              bits &= bits - 1u;
+              const float xp = penalise(staged<DT>(st, (u * kWave + t) * EPV + e), p.pen);
+              own += __builtin_fmaf(xp, c, nref) >= th ? 1u : 0u;
+            }
           }
         }
       }
-      cnt = static_cast<uint32_t>(__builtin_popcount(mask));
-      const uint32_t tot = wave_sum_u64(cnt);
+      const uint32_t tot = wave_sum_u64(own);
       if (tot <= static_cast<uint32_t>(cap)) {
         cnt = tot;
         break;
@@ -618,7 +611,7 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
       mask &= ~(0x80000000u >> i);
       const int li = ((i / EPV) * kWave + t) * EPV + (i % EPV);
       const float xv = staged<DT>(st, li);
-      store_sc64(out + pos, (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv));
+      out[pos] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv);
       ++pos;
     }
   }
@@ -647,7 +640,7 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
             const uint32_t q = __hip_atomic_fetch_add(&sh.pcount[w], 1u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_WORKGROUP);
             if (nA + q < static_cast<uint32_t>(cap))
-              store_sc64(out + nA + q, (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp));
+              out[nA + q] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp);
           }
         }
       }
@@ -671,32 +664,97 @@ __device__ __forceinline__ int stream_item(const Params& p, Sh& sh, int w, int i
     xtok = xv;
   }
 
-  // 11. the record, then drain every store and arrive on the unit
+  // 11. the record
   if (t == 0) {
     ChunkRec* rec = p.recs + static_cast<int64_t>(I.row) * p.nch + I.chunk;
-    uint64_t* r64 = reinterpret_cast<uint64_t*>(rec);
+    u32x4* r128 = reinterpret_cast<u32x4*>(rec);
     const uint32_t flags = (overflow ? kChunkOverflow : 0u) | (has_tok ? kChunkHasTok : 0u);
-    store_sc64(r64 + 0, pack_u32(__float_as_uint(m), __float_as_uint(mass)));
-    store_sc64(r64 + 1, pack_u32(__float_as_uint(pm), __float_as_uint(pmass)));
-    store_sc64(r64 + 2, pack_u32(static_cast<uint32_t>(overflow ? -1 : L), overflow ? 0u : nA));
-    store_sc64(r64 + 3, pack_u32(__float_as_uint(xtok), flags));
+    r128[0] = u32x4{__float_as_uint(m), __float_as_uint(mass), __float_as_uint(pm), __float_as_uint(pmass)};
+    r128[1] = u32x4{static_cast<uint32_t>(overflow ? -1 : L), overflow ? 0u : nA, __float_as_uint(xtok), flags};
   }
-  drain_stores();
-  int done = -1;
-  if (t == 0) {
-    const uint32_t old = atomic_arrive(p.unit_cnt + I.unit);
-    if (old + 1u == static_cast<uint32_t>(unit_items(p, I.unit))) done = I.unit;
-  }
-  return __shfl(done, 0);
 }
 
 // ===========================================================================
-// Finaliser
+// stream_kernel: one (row, chunk) item per wave, four independent waves per
+// workgroup
 // ===========================================================================
+template <int DT, bool PEN>
+__global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
+  constexpr int NVC = kChunk / (kWave * Elem<DT>::kPerVec);
+  __shared__ StreamSh<DT> sh;
+  // the wave's item, wave-uniform (its decomposition runs on the scalar unit)
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int it = static_cast<int>(blockIdx.x) * kNW + w;
+  if (it >= p.items) return;  // the waves of a workgroup share no barrier
+  const Item I = item_of(p, it);
+  u32x4 d[NVC];
+  uint32_t pw;
+  load_item<DT, NVC>(p, I, d, pw);
+  stream_item<DT, PEN>(p, sh, w, I, d, pw);
+}
+
+// ===========================================================================
+// Finaliser: fin_kernel, one workgroup per unit
+// ===========================================================================
+constexpr int kFW = 512;               // finaliser workgroup
+constexpr int kFNW = kFW / kWave;
+constexpr int kEPT = kRowCap / kFW;    // entries (and candidate slots) of one row per thread
+constexpr int kPosPT = kChunk / kFW;   // chunk positions per thread in a draw
+constexpr int kHash = 4096;            // draft-entry hash slots (at most half in use)
+constexpr int kSelBins = 2048;         // radix digits per select round (11 bits)
+constexpr int kSelPer = kSelBins / kFW;
+constexpr int kGather = kWave;         // a crossing bucket this small is finished by one wave
+
+struct RowAux {
+  float mcmax, s, cut, mass_f;   // cutoff (0 unfiltered), binary32 retained mass
+  uint64_t mass_fx;
+  float bmax;                    // largest non-candidate bound
+  float xtok;
+  uint32_t n;                    // LDS entries
+  uint32_t flags;
+  uint32_t has_tok;
+  float top_p;
+};
+
+struct FinSh {
+  union {
+    uint64_t bins[2][kSelBins];  // radix bins of the unit's two rows (zero between selects)
+    uint64_t pos[kChunk];        // a draw's weights by position in the chosen chunk
+    struct {
+      uint64_t cum[kRowCap];     // a draw's exclusive prefix masses by entry
+      uint64_t w[kRowCap];       // and its weights
+    } dr;
+    struct {
+      uint32_t sup[kRowCap];     // a residual draw's support entries, compacted
+      float dv[kRowCap];         // and max(P - Q, 0) at them, by entry
+    } res;
+  } u;
+  uint32_t gbits[2][kGather];    // a select's crossing bucket: bits of p and masses
+  uint64_t gw[2][kGather];
+  uint32_t gcount[2];
+  uint32_t hash[kHash];          // slot 1's entries by vocabulary index (entry + 1, 0 = empty)
+  struct Entries {
+    uint32_t pbits[kRowCap];     // bits of p
+    uint32_t eidx[kRowCap];      // vocabulary index
+  } ent[2];
+  uint64_t csum[kMaxChunks];     // per-chunk weight sums of a draw
+  uint32_t cstart[2][kMaxChunks];  // each chunk's entries in the LDS list
+  uint32_t ccount[2][kMaxChunks];
+  float bound[2][kMaxChunks];    // per-chunk bound on the p of non-candidates
+  RowAux aux[2];
+  uint64_t red[4][2 * kFNW];     // block scan slots (callers alternate buffers)
+  uint32_t sel[2];               // radix select: crossing digit per row
+  uint64_t sel64[2][2];          // (mass above the digit, the digit's mass)
+  uint32_t fbits[2];             // a finished select's cutoff bits and retained mass
+  uint64_t fmass[2];
+  uint32_t pick;                 // a draw's chunk (kNone at zero total)
+  uint64_t pick_rem;             // the target minus the mass before that chunk
+  uint32_t last;                 // spec: this unit completes its batch element
+  int64_t token;
+};
 
 // Block-wide inclusive scan of one u64 per thread; tot receives the total.
-// red must not be in use by another scan still being read (callers alternate
-// between two buffers).
+// red must not be in use by a scan whose reads may still be pending.
 __device__ __forceinline__ uint64_t block_incl_scan(uint64_t v, uint64_t* red, uint64_t* tot) {
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
   const uint64_t inc = wave_scan_add_u64(v);
@@ -704,7 +762,7 @@ __device__ __forceinline__ uint64_t block_incl_scan(uint64_t v, uint64_t* red, u
   __syncthreads();
   uint64_t base = 0, all = 0;
 #pragma unroll
-  for (int i = 0; i < kNW; ++i) {
+  for (int i = 0; i < kFNW; ++i) {
     const uint64_t x = red[i];
     base += i < wid ? x : 0;
     all += x;
@@ -719,27 +777,103 @@ __device__ __forceinline__ uint64_t block_sum(uint64_t v, uint64_t* red) {
   return tot;
 }
 
-// Row constants and per-chunk data of row slot s from the unit's records;
-// wave s runs it (lane l holds chunks 2l and 2l+1).
-__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, int row) {
+// Block-wide sums of two u64 per thread with one barrier (red: 2 kFNW slots).
+__device__ __forceinline__ void block_sum2(uint64_t a, uint64_t b, uint64_t* red, uint64_t* sa, uint64_t* sb) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  a = wave_sum_u64(a);
+  b = wave_sum_u64(b);
+  if (lane == 0) {
+    red[wid] = a;
+    red[kFNW + wid] = b;
+  }
+  __syncthreads();
+  uint64_t x = 0, y = 0;
+#pragma unroll
+  for (int i = 0; i < kFNW; ++i) {
+    x += red[i];
+    y += red[kFNW + i];
+  }
+  *sa = x;
+  *sb = y;
+}
+
+// ---------------------------------------------------------------------------
+// Draft-entry hash: open addressing over kHash slots, at most kRowCap keys.
+// ---------------------------------------------------------------------------
+static_assert(kHash == 4096 && kRowCap <= kHash / 2, "hash size");
+__device__ __forceinline__ uint32_t hash_slot(uint32_t x) { return (x * 2654435761u) >> 20; }
+
+__device__ __forceinline__ void hash_insert(FinSh& f, uint32_t x, uint32_t e) {
+  uint32_t h = hash_slot(x);
+  for (int probe = 0; probe < kHash; ++probe) {
+    if (atomicCAS(&f.hash[h], 0u, e + 1u) == 0u) return;
+    h = (h + 1u) & (kHash - 1);
+  }
+}
+
+// The entry of slot 1 holding vocabulary index x, or kNone.
+__device__ __forceinline__ uint32_t hash_find(const FinSh& f, uint32_t x) {
+  uint32_t h = hash_slot(x);
+  for (int probe = 0; probe < kHash; ++probe) {
+    const uint32_t v = f.hash[h];
+    if (v == 0u) return kNone;
+    if (f.ent[1].eidx[v - 1u] == x) return v - 1u;
+    h = (h + 1u) & (kHash - 1);
+  }
+  return kNone;
+}
+
+// Rebuilds the hash after slot 1's entries changed; entries a refill dropped
+// (p bits 0) stay out, so an index is found at its live entry.
+__device__ __forceinline__ void hash_rebuild(FinSh& f) {
+  for (int i = threadIdx.x; i < kHash; i += kFW) f.hash[i] = 0u;
+  __syncthreads();
+  const uint32_t n = f.aux[1].n;
+  for (uint32_t e = threadIdx.x; e < n; e += kFW) {
+    if (f.ent[1].pbits[e] != 0u) hash_insert(f, f.ent[1].eidx[e], e);
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Unit set-up: records, row constants, LDS entries
+// ---------------------------------------------------------------------------
+
+// Records of chunks 2l and 2l+1 of a row for lane l (zero past nch).
+struct RecPair {
+  u32x4 a0, a1, b0, b1;
+};
+
+__device__ __forceinline__ RecPair load_recs(const Params& p, int row) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const u32x4* base = reinterpret_cast<const u32x4*>(p.recs + static_cast<int64_t>(row) * p.nch);
+  const u32x4 z{0u, 0u, 0u, 0u};
+  RecPair r{z, z, z, z};
+  const int ja = 2 * lane, jb = ja + 1;
+  if (ja < p.nch) {
+    r.a0 = base[2 * ja];
+    r.a1 = base[2 * ja + 1];
+  }
+  if (jb < p.nch) {
+    r.b0 = base[2 * jb];
+    r.b1 = base[2 * jb + 1];
+  }
+  return r;
+}
+
+// Row constants and per-chunk data of row slot s from its records (wave s).
+__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, const RecPair& rp) {
   const int lane = threadIdx.x & (kWave - 1);
   const int nch = p.nch;
   const float c = p.c;
-  ChunkRec ra{}, rb{};
+  ChunkRec ra, rb;
+  {
+    u32x4 wa[2] = {rp.a0, rp.a1}, wb[2] = {rp.b0, rp.b1};
+    __builtin_memcpy(&ra, wa, 32);
+    __builtin_memcpy(&rb, wb, 32);
+  }
   const int ja = 2 * lane, jb = ja + 1;
   const bool ia = ja < nch, ib = jb < nch;
-  const uint64_t* base = reinterpret_cast<const uint64_t*>(p.recs + static_cast<int64_t>(row) * nch);
-  uint64_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0};
-  if (ia) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) wa[q] = load_sc64(base + 4 * ja + q);
-  }
-  if (ib) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) wb[q] = load_sc64(base + 4 * jb + q);
-  }
-  __builtin_memcpy(&ra, wa, 32);
-  __builtin_memcpy(&rb, wb, 32);
   const float ninf = -__builtin_inff();
   const float mca = ia ? ra.m * c : ninf, pmca = ia ? ra.pm * c : ninf;
   const float mcb = ib ? rb.m * c : ninf, pmcb = ib ? rb.pm * c : ninf;
@@ -774,6 +908,7 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, int 
   const uint32_t na = ia ? (ra.n < capu ? ra.n : capu) : 0u, nb = ib ? (rb.n < capu ? rb.n : capu) : 0u;
   const uint32_t own = na + nb;
   const uint32_t incl = wave_scan_add_u32(own);
+  const uint32_t ntot = lane_bcast_u32(incl, kWave - 1);
   if (ia) {
     f.bound[s][ja] = ba;
     f.cstart[s][ja] = incl - own;
@@ -795,102 +930,214 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, int 
     a.mcmax = mcmax;
     a.s = S;
     a.bmax = bmax;
-    a.n = lane_bcast_u32(incl, kWave - 1);
+    a.n = ntot;
     a.has_tok = tk != 0;
     a.xtok = xt;
     a.flags = S > 0.0f ? 0u : kRowEmpty;
     a.cut = 0.0f;
     a.mass_f = 1.0f;
     a.mass_fx = 0;
-  } else {
-    (void)lane_bcast_u32(incl, kWave - 1);
+    a.top_p = 1.0f;
   }
 }
 
-// Candidates of row slot s into the LDS entries (p bits, index).
-__device__ __forceinline__ void load_entries(const Params& p, FinSh& f, int s, int row, const RowK& K) {
+// Candidate slot i = t + q kFW of row slot s, loaded before the records were
+// known, into the LDS entries when the record's count covers it: entry
+// cstart + k holds (bits of x, index) until entry_p replaces x by p.
+__device__ __forceinline__ void place_slots(const Params& p, FinSh& f, int s, const uint64_t (&sl)[kEPT]) {
   const int t = threadIdx.x;
-  const uint32_t n = f.aux[s].n;
-  const int nch = p.nch;
-  const uint64_t* cb = p.cands + static_cast<int64_t>(row) * nch * p.cap;
-  for (uint32_t e = t; e < n; e += kWG) {
-    // the chunk holding entry e: the last j with cstart[j] <= e
-    int lo = 0, hi = nch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (f.cstart[s][mid] <= e) lo = mid; else hi = mid - 1;
+  const int nslot = p.nch * p.cap;
+  const int lc = __builtin_ctz(static_cast<unsigned>(p.cap));
+#pragma unroll
+  for (int q = 0; q < kEPT; ++q) {
+    const int i = t + q * kFW;
+    if (i < nslot) {
+      const int j = i >> lc;
+      const uint32_t k = static_cast<uint32_t>(i & (p.cap - 1));
+      if (k < f.ccount[s][j]) {
+        const uint32_t e = f.cstart[s][j] + k;
+        f.ent[s].pbits[e] = static_cast<uint32_t>(sl[q]);
+        f.ent[s].eidx[e] = static_cast<uint32_t>(sl[q] >> 32);
+      }
     }
-    const uint64_t v = load_sc64(cb + static_cast<int64_t>(lo) * p.cap + (e - f.cstart[s][lo]));
-    const float x = __uint_as_float(static_cast<uint32_t>(v));
-    const uint32_t idx = static_cast<uint32_t>(v >> 32);
+  }
+}
+
+// p of row slot s's placed entries, spread evenly over the workgroup; slot 1's
+// entries also go into the hash.
+__device__ __forceinline__ void entry_p(const Params& p, FinSh& f, int s, bool hash) {
+  const RowK K{f.aux[s].mcmax, f.aux[s].s, p.cd};
+  const uint32_t n = f.aux[s].n;
+  for (uint32_t e = threadIdx.x; e < n; e += kFW) {
+    const float x = __uint_as_float(f.ent[s].pbits[e]);
+    const uint32_t idx = f.ent[s].eidx[e];
     const bool ok = idx < static_cast<uint32_t>(p.vocab);  // always, for a well-formed workspace
     f.ent[s].pbits[e] = ok ? __float_as_uint(pval(K, x)) : 0u;
     f.ent[s].eidx[e] = ok ? idx : 0u;
+    if (hash && ok) hash_insert(f, idx, e);
   }
 }
 
-// Exact top-p cutoff over the LDS entries of slot s: c = max{v : sum over
-// entries with p >= v of fx46(p) >= thr}, by three radix rounds on the bits of
-// p (10 bits each; p <= 1, so bits >> 20 < 1024). Returns false when the
-// entries hold less than thr. Uses f.u.bins.
-__device__ __forceinline__ bool select_entries(FinSh& f, int s, uint64_t thr, float* cut, uint64_t* mass) {
-  const int t = threadIdx.x;
-  const uint32_t n = f.aux[s].n;
-  uint32_t prefix = 0;
-  uint64_t above = 0;
-  constexpr int kPer = kBins / kWG;  // bins per thread
-  for (int round = 0; round < 3; ++round) {
-    const int shift = 20 - round * kRadixBits;
+// ---------------------------------------------------------------------------
+// Top-p cutoffs
+// ---------------------------------------------------------------------------
+
+// Exact top-p cutoffs over the LDS entries of the rows in `mask` (bit s for
+// slot s), in shared rounds: c_s = max{v : sum over entries with p >= v of
+// fx46(p) >= thr_s}. Radix rounds on the bits of p (p <= 1, so bits < 2^30):
+// bits 29..19, 18..8 and 7..0; after each round the entries of the crossing
+// digit are gathered and, when at most kGather, finished by one wave (wave s
+// for row s). ok[s] is false when the entries hold less than thr_s. Entries of
+// zero mass never decide the cutoff and are skipped. f.u.bins must be zero on
+// entry, unless zeroed = false (then they are cleared here first).
+__device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const uint64_t (&thr)[2], float (&cut)[2],
+                                               uint64_t (&mass)[2], bool (&ok)[2], bool zeroed) {
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  bool live[2] = {(mask & 1u) != 0, (mask & 2u) != 0};
+  ok[0] = live[0];
+  ok[1] = live[1];
+  if (!zeroed) {
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) f.u.bins[kPer * t + q] = 0;
-    __syncthreads();
-    for (uint32_t e = t; e < n; e += kWG) {
-      const uint32_t b = f.ent[s].pbits[e];
-      if ((b >> (shift + kRadixBits)) == prefix) {
-        __hip_atomic_fetch_add(&f.u.bins[(b >> shift) & (kBins - 1)], fx46(__uint_as_float(b)), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-    }
-    __syncthreads();
-    // thread t holds the bins of digits 4(255 - t) .. +3: its inclusive scan is
-    // the mass at digits >= 4(255 - t)
-    const int g0 = kPer * (kWG - 1 - t);
-    uint64_t own = 0;
+    for (int s = 0; s < 2; ++s) {
+      if (live[s]) {
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) own += f.u.bins[g0 + q];
-    uint64_t tot;
-    const uint64_t incl = block_incl_scan(own, f.red + (round & 1) * kNW, &tot);
-    const uint64_t need = thr > above ? thr - above : 0;
-    if (t == 0) f.sel[0] = kNone;
-    __syncthreads();
-    if (incl >= need && incl - own < need) {
-      // the crossing digit inside this thread's group, from the top
-      uint64_t acc = incl - own;
-      int d = g0;
-      for (int q = kPer - 1; q >= 0; --q) {
-        acc += f.u.bins[g0 + q];
-        if (acc >= need) {
-          d = g0 + q;
-          acc -= f.u.bins[g0 + q];
-          break;
-        }
+        for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
       }
-      f.sel[0] = static_cast<uint32_t>(d);
-      f.sel64[0] = above + acc;  // mass strictly above digit d
-      f.sel64[1] = f.u.bins[d];
-    }
-    __syncthreads();
-    const uint32_t d = f.sel[0];
-    if (d == kNone) return false;
-    above = f.sel64[0];
-    prefix = (prefix << kRadixBits) | d;
-    if (round == 2) {
-      *cut = __uint_as_float(prefix);
-      *mass = above + f.sel64[1];
     }
     __syncthreads();
   }
-  return true;
+  const uint32_t n[2] = {f.aux[0].n, f.aux[1].n};
+  uint32_t prefix[2] = {0u, 0u};  // the resolved high bits: bits >> hshift
+  uint64_t above[2] = {0u, 0u};   // mass strictly above the resolved prefix
+  for (int round = 0; round < 3 && (live[0] || live[1]); ++round) {
+    const int shift = round == 0 ? 19 : (round == 1 ? 8 : 0);
+    const int width = round == 2 ? 8 : 11;
+    const int hshift = shift + width;
+    // 1. masses into the bins of this round's digit
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+      for (uint32_t e = t; e < n[s]; e += kFW) {
+        const uint32_t b = f.ent[s].pbits[e];
+        const uint64_t w = fx46(__uint_as_float(b));
+        if (w && (b >> hshift) == prefix[s])
+          __hip_atomic_fetch_add(&f.u.bins[s][(b >> shift) & ((1u << width) - 1u)], w, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    __syncthreads();
+    // 2. thread t holds digits kSelBins - 1 - (kSelPer t + q), descending;
+    //    the gather counts restart (their last reads precede the last barrier)
+    if (t < 2) f.gcount[t] = 0;
+    uint64_t v[2][kSelPer], sum[2] = {0u, 0u}, inc[2] = {0u, 0u};
+    uint64_t* red = f.red[round & 1];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+#pragma unroll
+      for (int q = 0; q < kSelPer; ++q) {
+        v[s][q] = f.u.bins[s][kSelBins - 1 - (kSelPer * t + q)];
+        sum[s] += v[s][q];
+      }
+      inc[s] = wave_scan_add_u64(sum[s]);
+      if (lane == kWave - 1) red[s * kFNW + wid] = inc[s];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+      uint64_t base = 0, tot = 0;
+#pragma unroll
+      for (int i = 0; i < kFNW; ++i) {
+        const uint64_t x = red[s * kFNW + i];
+        base += i < wid ? x : 0;
+        tot += x;
+      }
+      const uint64_t need = thr[s] - above[s];  // > 0: above < thr
+      if (tot < need) {
+        // the entries hold less than thr (uniform over the workgroup)
+        live[s] = false;
+        ok[s] = false;
+        continue;
+      }
+      uint64_t before = base + inc[s] - sum[s];
+      if (before < need && before + sum[s] >= need) {
+#pragma unroll
+        for (int q = 0; q < kSelPer; ++q) {
+          if (before < need && before + v[s][q] >= need) {
+            f.sel[s] = static_cast<uint32_t>(kSelBins - 1 - (kSelPer * t + q));
+            f.sel64[s][0] = above[s] + before;
+            f.sel64[s][1] = v[s][q];
+          }
+          before += v[s][q];
+        }
+      }
+    }
+    __syncthreads();
+    // 3. the crossing digit; its entries gathered; the bins cleared for the
+    //    next round (their reads are all before the last barrier)
+    uint64_t binmass[2] = {0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+      prefix[s] = (prefix[s] << width) | f.sel[s];
+      above[s] = f.sel64[s][0];
+      binmass[s] = f.sel64[s][1];
+      for (uint32_t e = t; e < n[s]; e += kFW) {
+        const uint32_t b = f.ent[s].pbits[e];
+        if ((b >> shift) == prefix[s] && fx46(__uint_as_float(b))) {
+          const uint32_t k = __hip_atomic_fetch_add(&f.gcount[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (k < kGather) {
+            f.gbits[s][k] = b;
+            f.gw[s][k] = fx46(__uint_as_float(b));
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
+    }
+    __syncthreads();
+    // 4. a small bucket is finished by one wave: lane l holds entry l, its
+    //    mass at and above it A_l; the cutoff is the largest p with A >= thr
+    bool fin[2] = {false, false};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+      const uint32_t cnt = f.gcount[s];
+      if (cnt <= static_cast<uint32_t>(kGather)) {
+        fin[s] = true;
+        if (wid == s) {
+          const bool in = static_cast<uint32_t>(lane) < cnt;
+          const uint32_t b = in ? f.gbits[s][lane] : 0u;
+          uint64_t A = above[s];
+          for (uint32_t j = 0; j < cnt; ++j) A += f.gbits[s][j] >= b ? f.gw[s][j] : 0;
+          const bool good = in && A >= thr[s];
+          const uint64_t best = wave_max_u64(good ? b : 0u);
+          const uint64_t at = wave_max_u64(good && b == static_cast<uint32_t>(best) ? A : 0u);
+          if (lane == 0) {
+            f.fbits[s] = static_cast<uint32_t>(best);
+            f.fmass[s] = at;
+          }
+        }
+      } else if (round == 2) {
+        // every entry of the bucket has the same bits
+        cut[s] = __uint_as_float(prefix[s]);
+        mass[s] = above[s] + binmass[s];
+        live[s] = false;
+      }
+    }
+    if (fin[0] || fin[1]) {
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (!fin[s]) continue;
+        cut[s] = __uint_as_float(f.fbits[s]);
+        mass[s] = f.fmass[s];
+        live[s] = false;
+      }
+    }
+  }
+  __syncthreads();
 }
 
 // Passes over a whole row for the slow path: fn(index, x) for every element,
@@ -900,7 +1147,7 @@ __device__ __forceinline__ void row_pass(const Params& p, const char* rowp, cons
                                          Fn fn) {
   constexpr int EPV = Elem<DT>::kPerVec;
   const u32x4* src = reinterpret_cast<const u32x4*>(rowp);
-  for (int64_t v = i0 / EPV + threadIdx.x; v < i1 / EPV; v += kWG) {
+  for (int64_t v = i0 / EPV + threadIdx.x; v < i1 / EPV; v += kFW) {
     const u32x4 d = src[v];
     uint32_t word = bm ? bm[(v * EPV) >> 5] : 0u;
 #pragma unroll
@@ -919,48 +1166,30 @@ __device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, c
   const int t = threadIdx.x;
   const char* rowp = row_ptr(p, row);
   const uint32_t* bm = row_bitmap(p, row);
+  uint64_t* bins = f.u.bins[0];
   uint32_t prefix = 0;
   uint64_t above = 0;
-  constexpr int kPer = kBins / kWG;
+  constexpr int kPer = kBins / kFW;
   for (int round = 0; round < 3; ++round) {
     const int shift = 20 - round * kRadixBits;
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) f.u.bins[kPer * t + q] = 0;
+    for (int q = 0; q < kPer; ++q) bins[kPer * t + q] = 0;
     __syncthreads();
     row_pass<DT>(p, rowp, bm, 0, p.vocab, [&](int64_t, float x) {
       const uint32_t b = __float_as_uint(pval(K, x));
       if ((b >> (shift + kRadixBits)) == prefix)
-        __hip_atomic_fetch_add(&f.u.bins[(b >> shift) & (kBins - 1)], fx46(__uint_as_float(b)), __ATOMIC_RELAXED,
+        __hip_atomic_fetch_add(&bins[(b >> shift) & (kBins - 1)], fx46(__uint_as_float(b)), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
     });
     __syncthreads();
-    const int g0 = kPer * (kWG - 1 - t);
+    const int g0 = kPer * (kFW - 1 - t);
     uint64_t own = 0;
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) own += f.u.bins[g0 + q];
+    for (int q = 0; q < kPer; ++q) own += bins[g0 + q];
     uint64_t tot;
-    const uint64_t incl = block_incl_scan(own, f.red + (round & 1) * kNW, &tot);
+    const uint64_t incl = block_incl_scan(own, f.red[round & 1], &tot);
     const uint64_t need = thr > above ? thr - above : 0;
-    if (t == 0) f.sel[0] = kNone;
-    __syncthreads();
-    if (incl >= need && incl - own < need) {
-      uint64_t acc = incl - own;
-      int d = g0;
-      for (int q = kPer - 1; q >= 0; --q) {
-        acc += f.u.bins[g0 + q];
-        if (acc >= need) {
-          d = g0 + q;
-          acc -= f.u.bins[g0 + q];
-          break;
-        }
-      }
-      f.sel[0] = static_cast<uint32_t>(d);
-      f.sel64[0] = above + acc;
-      f.sel64[1] = f.u.bins[d];
-    }
-    __syncthreads();
-    const uint32_t d = f.sel[0];
-    if (d == kNone) {
+    if (tot < need) {
       // the row holds less than thr: the reference clamps to the last sorted
       // value, the row minimum, and keeps everything
       if (round != 0) return false;  // cannot happen: later rounds include the crossing
@@ -970,20 +1199,37 @@ __device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, c
         mn = v < mn ? v : mn;
       });
       uint64_t key = static_cast<uint64_t>(__float_as_uint(mn));
-      key = ~block_max_u64<kWG>(~key, f.red2);  // min via max of complements
+      key = ~block_max_u64<kFW>(~key, f.red[2]);  // min via max of complements
       __syncthreads();
       *cut = __uint_as_float(static_cast<uint32_t>(key));
       *mass = tot;
       return true;
     }
-    above = f.sel64[0];
+    if (incl >= need && incl - own < need) {
+      uint64_t acc = incl - own;
+      int d = g0;
+      for (int q = kPer - 1; q >= 0; --q) {
+        const uint64_t bq = bins[g0 + q];
+        if (acc + bq >= need) {
+          d = g0 + q;
+          break;
+        }
+        acc += bq;
+      }
+      f.sel[0] = static_cast<uint32_t>(d);
+      f.sel64[0][0] = above + acc;
+      f.sel64[0][1] = bins[d];
+    }
+    __syncthreads();
+    const uint32_t d = f.sel[0];
+    above = f.sel64[0][0];
     prefix = (prefix << kRadixBits) | d;
     if (round == 2) {
       *cut = __uint_as_float(prefix);
-      *mass = above + f.sel64[1];
+      *mass = above + f.sel64[0][1];
     }
-    __syncthreads();
   }
+  __syncthreads();
   return true;
 }
 
@@ -992,36 +1238,38 @@ __device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, c
 template <int DT>
 __device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, int row, const RowK& K, int j, float cut) {
   constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int EPT = kChunk / kWG;  // elements per thread, contiguous
+  // elements per thread, contiguous, whole vectors (threads past the chunk idle)
+  constexpr int EPT = kChunk / kFW > EPV ? kChunk / kFW : EPV;
   const int t = threadIdx.x;
   const char* rowp = row_ptr(p, row);
   const uint32_t* bm = row_bitmap(p, row);
   const int64_t c0 = static_cast<int64_t>(j) * kChunk;
   const int64_t nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
+  const int64_t mine = t * EPT < kChunk ? nel : 0;  // this thread's elements lie below c0 + mine
   float pv[EPT];
   uint32_t keep = 0;
 #pragma unroll
   for (int q = 0; q < EPT / EPV; ++q) {
     const int64_t i0 = c0 + static_cast<int64_t>(t) * EPT + q * EPV;
     u32x4 d{0, 0, 0, 0};
-    if (i0 < c0 + nel) d = reinterpret_cast<const u32x4*>(rowp)[i0 / EPV];
-    const uint32_t word = (bm && i0 < c0 + nel) ? bm[i0 >> 5] : 0u;
+    if (i0 < c0 + mine) d = reinterpret_cast<const u32x4*>(rowp)[i0 / EPV];
+    const uint32_t word = (bm && i0 < c0 + mine) ? bm[i0 >> 5] : 0u;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       const int64_t i = i0 + e;
       float v = 0.0f;
-      if (i < c0 + nel) {
+      if (i < c0 + mine) {
         float x = vec_elem<DT>(d, e);
         if (bm && ((word >> (i & 31)) & 1u)) x = penalise(x, p.pen);
         v = pval(K, x);
       }
       pv[q * EPV + e] = v;
-      if (i < c0 + nel && v >= cut) keep |= 1u << (q * EPV + e);
+      if (i < c0 + mine && v >= cut) keep |= 1u << (q * EPV + e);
     }
   }
   const uint32_t own = static_cast<uint32_t>(__builtin_popcount(keep));
   uint64_t tot;
-  const uint64_t incl = block_incl_scan(own, f.red, &tot);
+  const uint64_t incl = block_incl_scan(own, f.red[0], &tot);
   const uint32_t base = f.aux[s].n;
   if (base + tot > static_cast<uint64_t>(kRowCap)) {
     __syncthreads();
@@ -1038,7 +1286,7 @@ __device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, i
   }
   // the chunk's old entries drop out of the select (p = 0 cannot reach the cutoff)
   const uint32_t os = f.cstart[s][j], oc = f.ccount[s][j];
-  for (uint32_t e = os + t; e < os + oc; e += kWG) f.ent[s].pbits[e] = 0u;
+  for (uint32_t e = os + t; e < os + oc; e += kFW) f.ent[s].pbits[e] = 0u;
   __syncthreads();
   if (t == 0) {
     f.cstart[s][j] = base;
@@ -1067,50 +1315,74 @@ __device__ __forceinline__ bool collect_support(const Params& p, FinSh& f, int s
   return true;
 }
 
-// Resolves the cutoff of row slot s: list mode (kRowList: the support is in
-// the LDS entries) or dense (the support is {p >= cut} of the whole row).
+// Resolves the cutoffs of the unit's nr rows: list mode (kRowList: the support
+// is in the LDS entries) or dense (the support is {p >= cut} of the whole
+// row). The rows' first selects share their rounds.
 template <int DT>
-__device__ __forceinline__ void resolve_row(const Params& p, FinSh& f, int s, int row, const RowK& K) {
-  RowAux& a = f.aux[s];
-  const float top_p = row_top_p(p, row);
-  const uint32_t empty = a.flags & kRowEmpty;
-  if (top_p >= 1.0f || empty) {
-    // unfiltered: P = p over the whole row (an empty row has p = 0 everywhere)
-    if (threadIdx.x == 0) {
-      a.flags = empty;
-      a.cut = 0.0f;
-      a.mass_f = 1.0f;
-      a.top_p = top_p;
+__device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, const int (&rows)[2], const RowK (&K)[2]) {
+  uint32_t mask = 0;
+  uint64_t thr[2] = {0u, 0u};
+  float top_p[2] = {1.0f, 1.0f};
+  for (int s = 0; s < nr; ++s) {
+    top_p[s] = row_top_p(p, rows[s]);
+    if (top_p[s] < 1.0f && !(f.aux[s].flags & kRowEmpty)) {
+      mask |= 1u << s;
+      // a threshold of 0 (top_p < 2^-46) selects the largest p, as 1 does
+      // whenever that p has a nonzero mass
+      const uint64_t tf = fx46(top_p[s]);
+      thr[s] = tf > 0 ? tf : 1;
     }
-    __syncthreads();
-    return;
   }
-  const uint64_t thr = fx46(top_p);
-  float cut = 0.0f;
-  uint64_t mass = 0;
-  bool ok = select_entries(f, s, thr, &cut, &mass);
-  uint32_t flags = kRowFiltered | kRowList;
-  if (ok && !(cut > a.bmax)) {
-    // re-read the chunks whose non-candidates may reach the cutoff
-    flags |= kRowRefilled;
-    for (int j = 0; j < p.nch && ok; ++j) {
-      if (f.bound[s][j] >= cut) ok = refill_chunk<DT>(p, f, s, row, K, j, cut);
+  float cut[2] = {0.0f, 0.0f};
+  uint64_t mass[2] = {0u, 0u};
+  bool ok[2] = {false, false};
+  if (mask) select_entries(f, mask, thr, cut, mass, ok, true);
+  uint32_t flags[2] = {f.aux[0].flags & kRowEmpty, f.aux[1].flags & kRowEmpty};
+  bool changed1 = false;
+  for (int s = 0; s < nr; ++s) {
+    if (!((mask >> s) & 1u)) continue;  // unfiltered: P = p over the whole row
+    flags[s] = kRowFiltered | kRowList;
+    if (ok[s] && !(cut[s] > f.aux[s].bmax)) {
+      // re-read the chunks whose non-candidates may reach the cutoff
+      flags[s] |= kRowRefilled;
+      for (int j = 0; j < p.nch && ok[s]; ++j) {
+        if (f.bound[s][j] >= cut[s]) ok[s] = refill_chunk<DT>(p, f, s, rows[s], K[s], j, cut[s]);
+      }
+      if (ok[s]) {
+        float c1[2];
+        uint64_t m1[2];
+        bool o1[2];
+        select_entries(f, 1u << s, thr, c1, m1, o1, false);
+        ok[s] = o1[s];
+        cut[s] = c1[s];
+        mass[s] = m1[s];
+      }
+      if (s == 1) changed1 = true;
     }
-    if (ok) ok = select_entries(f, s, thr, &cut, &mass);
-  }
-  if (!ok) {
-    flags = kRowFiltered | kRowSlow;
-    select_row<DT>(p, f, row, K, thr, &cut, &mass);
-    if (collect_support<DT>(p, f, s, row, K, cut)) flags |= kRowList;
+    if (!ok[s]) {
+      flags[s] = kRowFiltered | kRowSlow;
+      select_row<DT>(p, f, rows[s], K[s], thr[s], &cut[s], &mass[s]);
+      if (collect_support<DT>(p, f, s, rows[s], K[s], cut[s])) flags[s] |= kRowList;
+      if (s == 1) changed1 = true;
+    }
   }
   if (threadIdx.x == 0) {
-    a.flags = flags;
-    a.cut = cut;
-    a.mass_fx = mass;
-    a.mass_f = mass_to_f32(mass);
-    a.top_p = top_p;
+    for (int s = 0; s < nr; ++s) {
+      RowAux& a = f.aux[s];
+      a.flags = flags[s];
+      a.top_p = top_p[s];
+      if (flags[s] & kRowFiltered) {
+        a.cut = cut[s];
+        a.mass_fx = mass[s];
+        a.mass_f = mass_to_f32(mass[s]);
+      } else {
+        a.cut = 0.0f;
+        a.mass_f = 1.0f;
+      }
+    }
   }
   __syncthreads();
+  if (nr == 2 && changed1 && (f.aux[1].flags & kRowList)) hash_rebuild(f);
 }
 
 // Filtered probability of a row at p (P = p when unfiltered).
@@ -1126,14 +1398,14 @@ __device__ __forceinline__ float filtered_of(const RowAux& a, float pv) {
 // index 0 at zero total (categorical_pick).
 // ---------------------------------------------------------------------------
 
-// Chunk j* holding the target, from f.u.csum: lane l of wave 0 holds chunks
-// 2l and 2l+1. Writes f.sel64[0] = target - mass before j*, f.sel[0] = j*
+// Chunk j* holding the target, from f.csum: lane l of wave 0 holds chunks
+// 2l and 2l+1. Writes f.pick_rem = target - mass before j*, f.pick = j*
 // (kNone at zero total). Ends with a barrier.
 __device__ __forceinline__ void pick_chunk(const Params& p, FinSh& f, float u) {
   const int t = threadIdx.x;
   if (t < kWave) {
     const int ja = 2 * t, jb = ja + 1;
-    const uint64_t a = ja < p.nch ? f.u.csum[ja] : 0, b = jb < p.nch ? f.u.csum[jb] : 0;
+    const uint64_t a = ja < p.nch ? f.csum[ja] : 0, b = jb < p.nch ? f.csum[jb] : 0;
     const uint64_t incl = wave_scan_add_u64(a + b);
     const uint64_t total = lane_bcast_u64(incl, kWave - 1);
     const uint64_t target = floor_u_times(u, total);
@@ -1142,35 +1414,35 @@ __device__ __forceinline__ void pick_chunk(const Params& p, FinSh& f, float u) {
     const bool in_a = ja < p.nch && ex <= target && ex + a > target;
     const bool in_b = jb < p.nch && ex + a <= target && ex + a + b > target;
     if (total == 0) {
-      if (t == 0) f.sel[0] = kNone;
+      if (t == 0) f.pick = kNone;
     } else if (in_a) {
-      f.sel[0] = static_cast<uint32_t>(ja);
-      f.sel64[0] = target - ex;
+      f.pick = static_cast<uint32_t>(ja);
+      f.pick_rem = target - ex;
     } else if (in_b) {
-      f.sel[0] = static_cast<uint32_t>(jb);
-      f.sel64[0] = target - ex - a;
+      f.pick = static_cast<uint32_t>(jb);
+      f.pick_rem = target - ex - a;
     }
   }
   __syncthreads();
 }
 
-// Within a chunk of 2048 positions: thread t owns positions 8t..8t+7 with
-// weights w[0..7]; the first position whose inclusive mass exceeds `rem`
-// (the target minus the mass before the chunk) goes to f.token as c0 + pos.
-__device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64_t (&w)[8], uint64_t rem) {
+// Within a chunk of 2048 positions: thread t owns positions kPosPT t .. +
+// kPosPT - 1 with weights w; the first position whose inclusive mass exceeds
+// `rem` (the target minus the mass before the chunk) goes to f.token as c0 + pos.
+__device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64_t (&w)[kPosPT], uint64_t rem) {
   const int t = threadIdx.x;
   uint64_t own = 0;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) own += w[q];
+  for (int q = 0; q < kPosPT; ++q) own += w[q];
   uint64_t tot;
-  const uint64_t incl = block_incl_scan(own, f.red, &tot);
+  const uint64_t incl = block_incl_scan(own, f.red[3], &tot);
   const uint64_t ex = incl - own;
   if (ex <= rem && incl > rem) {
     uint64_t acc = ex;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kPosPT; ++q) {
       if (acc + w[q] > rem) {
-        f.token = c0 + 8 * t + q;
+        f.token = c0 + kPosPT * t + q;
         break;
       }
       acc += w[q];
@@ -1179,36 +1451,105 @@ __device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64
   __syncthreads();
 }
 
-// List-mode draw over slot 0's entries with weights wts[e] (u64, held in the
-// slot-1 region); the entries of chunk j are f.cstart/ccount[0][j].
-__device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t* wts, float u) {
-  const int t = threadIdx.x;
+// List-mode draw over slot 0's entries, thread t weighing entries kEPT t + q
+// by wl[q]. With each chunk's entries contiguous and the chunks in order
+// (`ordered`: no chunk was refilled), a scan over the list finds the chunk,
+// and a chunk of at most kWave entries is finished by one wave, which orders
+// its entries by index; otherwise per-chunk sums find the chunk and its
+// entries are scattered to their positions (indices are distinct among
+// entries of nonzero weight).
+__device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t (&wl)[kEPT], float u,
+                                             bool ordered) {
+  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
   const uint32_t n = f.aux[0].n;
-  for (int j = t; j < p.nch; j += kWG) f.u.csum[j] = 0;
+  uint32_t js;
+  uint64_t rem;
+  if (ordered) {
+    uint64_t own = 0;
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) own += wl[q];
+    uint64_t total;
+    const uint64_t incl = block_incl_scan(own, f.red[3], &total);
+    if (total == 0) return 0;
+    const uint64_t target = floor_u_times(u, total);
+    uint64_t run = incl - own;
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      const uint32_t e = kEPT * t + q;
+      if (e < n) {
+        f.u.dr.cum[e] = run;
+        f.u.dr.w[e] = wl[q];
+        if (run <= target && target < run + wl[q]) f.pick = f.ent[0].eidx[e] >> 11;
+      }
+      run += wl[q];
+    }
+    __syncthreads();
+    js = f.pick;
+    const uint32_t s0 = f.cstart[0][js], sc = f.ccount[0][js];
+    rem = target - f.u.dr.cum[s0];
+    if (sc <= static_cast<uint32_t>(kWave)) {
+      if (wid == 0) {
+        // lane l: entry s0 + l, its weight, and the mass of the chunk's
+        // entries of lower index (broadcast reads, eight per step)
+        const bool in = static_cast<uint32_t>(lane) < sc;
+        const uint32_t e = s0 + lane;
+        const uint32_t idx = in ? f.ent[0].eidx[e] : 0xffffffffu;
+        const uint64_t cw = in ? f.u.dr.w[e] : 0u;
+        uint64_t below = 0;
+        for (uint32_t j0 = 0; j0 < sc; j0 += 8) {
+          uint32_t ij[8];
+          uint64_t wj[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint32_t j = j0 + q < sc ? j0 + q : sc - 1;
+            ij[q] = f.ent[0].eidx[s0 + j];
+            wj[q] = j0 + q < sc ? f.u.dr.w[s0 + j] : 0u;
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) below += ij[q] < idx ? wj[q] : 0u;
+        }
+        const bool hit = in && cw > 0 && below <= rem && rem < below + cw;
+        const uint64_t hm = __ballot(hit);
+        if (hm && lane == __builtin_ctzll(hm)) f.token = static_cast<int64_t>(idx);
+      }
+      __syncthreads();
+      return f.token;
+    }
+    __syncthreads();  // every read of f.u.cum precedes the position scatter
+  } else {
+    for (int j = t; j < p.nch; j += kFW) f.csum[j] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      const uint32_t e = kEPT * t + q;
+      if (e < n && wl[q])
+        __hip_atomic_fetch_add(&f.csum[f.ent[0].eidx[e] >> 11], wl[q], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    pick_chunk(p, f, u);
+    js = f.pick;
+    if (js == kNone) return 0;
+    rem = f.pick_rem;
+  }
+  // chunk js by positions
+#pragma unroll
+  for (int q = 0; q < kPosPT; ++q) f.u.pos[kPosPT * t + q] = 0;
   if (t == 0) f.token = 0;
   __syncthreads();
-  for (uint32_t e = t; e < n; e += kWG) {
-    const uint64_t w = wts[e];
-    if (w) __hip_atomic_fetch_add(&f.u.csum[f.ent[0].eidx[e] >> 11], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  __syncthreads();
-  pick_chunk(p, f, u);
-  const uint32_t js = f.sel[0];
-  if (js == kNone) return 0;
-  const uint64_t rem = f.sel64[0];
-  const uint32_t s0 = f.cstart[0][js], sc = f.ccount[0][js];
-  const int64_t c0 = static_cast<int64_t>(js) * kChunk;
-  // thread t gathers the weights of the chunk's positions 8t..8t+7
-  uint64_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (uint32_t e = s0; e < s0 + sc; ++e) {
-    const int pos = static_cast<int>(f.ent[0].eidx[e] - c0);
-    const uint64_t we = wts[e];
-    if ((pos >> 3) == t) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) w[q] += (pos & 7) == q ? we : 0;
+  for (int q = 0; q < kEPT; ++q) {
+    const uint32_t e = kEPT * t + q;
+    if (e < n && wl[q]) {
+      const uint32_t ix = f.ent[0].eidx[e];
+      if ((ix >> 11) == js) f.u.pos[ix & (kChunk - 1)] = wl[q];
     }
   }
-  pick_in_chunk(f, c0, w, rem);
+  __syncthreads();
+  uint64_t w[kPosPT];
+#pragma unroll
+  for (int q = 0; q < kPosPT; ++q) w[q] = f.u.pos[kPosPT * t + q];
+  pick_in_chunk(f, static_cast<int64_t>(js) * kChunk, w, rem);
   return f.token;
 }
 
@@ -1216,25 +1557,25 @@ __device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const ui
 template <int DT, typename WFn>
 __device__ __forceinline__ int64_t draw_dense(const Params& p, FinSh& f, const char* rowp, const uint32_t* bm, float u, WFn wfn) {
   const int t = threadIdx.x;
-  for (int j = t; j < p.nch; j += kWG) f.u.csum[j] = 0;
+  for (int j = t; j < p.nch; j += kFW) f.csum[j] = 0;
   if (t == 0) f.token = 0;
   __syncthreads();
   row_pass<DT>(p, rowp, bm, 0, p.vocab, [&](int64_t i, float x) {
     const uint64_t w = wfn(i, x);
-    if (w) __hip_atomic_fetch_add(&f.u.csum[i >> 11], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (w) __hip_atomic_fetch_add(&f.csum[i >> 11], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   });
   __syncthreads();
   pick_chunk(p, f, u);
-  const uint32_t js = f.sel[0];
+  const uint32_t js = f.pick;
   if (js == kNone) return 0;
   const int64_t c0 = static_cast<int64_t>(js) * kChunk;
-  uint64_t w[8];
+  uint64_t w[kPosPT];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int64_t i = c0 + 8 * t + q;
+  for (int q = 0; q < kPosPT; ++q) {
+    const int64_t i = c0 + kPosPT * t + q;
     w[q] = i < p.vocab ? wfn(i, load_x<DT>(p, rowp, bm, i)) : 0;
   }
-  pick_in_chunk(f, c0, w, f.sel64[0]);
+  pick_in_chunk(f, c0, w, f.pick_rem);
   return f.token;
 }
 
@@ -1244,12 +1585,9 @@ __device__ __forceinline__ float q_at(const Params& p, const FinSh& f, const Row
   const RowAux& a = f.aux[1];
   if (a.flags & kRowEmpty) return 0.0f;
   if (a.flags & kRowList) {
-    const int j = static_cast<int>(x >> 11);
-    const uint32_t s0 = f.cstart[1][j], sc = f.ccount[1][j];
-    for (uint32_t e = s0; e < s0 + sc; ++e) {
-      if (f.ent[1].eidx[e] == x) return filtered_of(a, __uint_as_float(f.ent[1].pbits[e]));
-    }
-    return 0.0f;  // every draft element with q >= its cutoff is an entry
+    // every draft element with q >= its cutoff is an entry
+    const uint32_t e = hash_find(f, x);
+    return e == kNone ? 0.0f : filtered_of(a, __uint_as_float(f.ent[1].pbits[e]));
   }
   return filtered_of(a, pval(K1, load_x<DT>(p, row_ptr(p, row1), row_bitmap(p, row1), x)));
 }
@@ -1259,19 +1597,14 @@ template <int DT>
 __device__ __forceinline__ int64_t draw_target(const Params& p, FinSh& f, int row0, const RowK& K0, float u) {
   const RowAux& a = f.aux[0];
   if (a.flags & kRowList) {
-    uint64_t* wts = reinterpret_cast<uint64_t*>(&f.ent[1]);
-    uint64_t wl[kRowCap / kWG];
+    uint64_t wl[kEPT];
     const uint32_t n = a.n;
 #pragma unroll
-    for (int q = 0; q < kRowCap / kWG; ++q) {
-      const uint32_t e = threadIdx.x + q * kWG;
+    for (int q = 0; q < kEPT; ++q) {
+      const uint32_t e = kEPT * threadIdx.x + q;
       wl[q] = e < n ? fx46(filtered_of(a, __uint_as_float(f.ent[0].pbits[e]))) : 0;
     }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kRowCap / kWG; ++q) wts[threadIdx.x + q * kWG] = wl[q];
-    __syncthreads();
-    return draw_list(p, f, wts, u);
+    return draw_list(p, f, wl, u, !(a.flags & kRowRefilled));
   }
   return draw_dense<DT>(p, f, row_ptr(p, row0), row_bitmap(p, row0), u,
                         [&](int64_t, float x) { return fx46(filtered_of(a, pval(K0, x))); });
@@ -1285,45 +1618,47 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
   const int t = threadIdx.x;
   const RowAux& a = f.aux[0];
   if (a.flags & kRowList) {
-    constexpr int kPer = kRowCap / kWG;
     const uint32_t n = a.n;
-    float dl[kPer], pl[kPer];
-    uint64_t dsum = 0, psum = 0;
+    // P at this thread's entries; the support entries (P > 0) compacted
+    float pl[kEPT];
+    uint32_t own = 0;
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const uint32_t e = t + q * kWG;
-      float P = 0.0f, d = 0.0f;
-      if (e < n) {
-        P = filtered_of(a, __uint_as_float(f.ent[0].pbits[e]));
-        if (P > 0.0f) {
-          const float Q = q_at<DT>(p, f, K1, row1, f.ent[0].eidx[e]);
-          d = P - Q;
-          d = d > 0.0f ? d : 0.0f;
-        }
-      }
-      dl[q] = d;
-      pl[q] = P;
+    for (int q = 0; q < kEPT; ++q) {
+      const uint32_t e = kEPT * t + q;
+      pl[q] = e < n ? filtered_of(a, __uint_as_float(f.ent[0].pbits[e])) : 0.0f;
+      own += pl[q] > 0.0f ? 1u : 0u;
+    }
+    uint64_t nsup;
+    const uint64_t incl = block_incl_scan(own, f.red[0], &nsup);
+    uint32_t k = static_cast<uint32_t>(incl) - own;
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      if (pl[q] > 0.0f) f.u.res.sup[k++] = kEPT * t + q;
+    }
+    __syncthreads();
+    // d = max(P - Q, 0) at the support entries, Q through the draft's hash
+    uint64_t dsum = 0, psum = 0;
+    for (uint32_t j = t; j < static_cast<uint32_t>(nsup); j += kFW) {
+      const uint32_t e = f.u.res.sup[j];
+      const float P = filtered_of(a, __uint_as_float(f.ent[0].pbits[e]));
+      const float Q = q_at<DT>(p, f, K1, row1, f.ent[0].eidx[e]);
+      float d = P - Q;
+      d = d > 0.0f ? d : 0.0f;
+      f.u.res.dv[e] = d;
       dsum += fx46(d);
       psum += fx46(P);
     }
-    const uint64_t dtot = block_sum(dsum, f.red);
-    const uint64_t ptot = block_sum(psum, f.red2);
-    float den;
-    bool use_d = dtot > 0;
-    if (use_d) {
-      den = mass_to_f32(dtot);
-    } else {
-      den = ptot > 0 ? mass_to_f32(ptot) : 1.0f;
+    uint64_t dtot, ptot;
+    block_sum2(dsum, psum, f.red[1], &dtot, &ptot);
+    const bool use_d = dtot > 0;
+    const float den = use_d ? mass_to_f32(dtot) : (ptot > 0 ? mass_to_f32(ptot) : 1.0f);
+    uint64_t wl[kEPT];
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      const float d = pl[q] > 0.0f ? f.u.res.dv[kEPT * t + q] : 0.0f;
+      wl[q] = fx46((use_d ? d : pl[q]) / den);
     }
-    uint64_t wl[kPer];
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) wl[q] = fx46((use_d ? dl[q] : pl[q]) / den);
-    __syncthreads();  // slot 1's entries are no longer read
-    uint64_t* wts = reinterpret_cast<uint64_t*>(&f.ent[1]);
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) wts[t + q * kWG] = wl[q];
-    __syncthreads();
-    return draw_list(p, f, wts, u);
+    return draw_list(p, f, wl, u, !(a.flags & kRowRefilled));
   }
   // dense target support: passes over both rows
   const char* r0 = row_ptr(p, row0);
@@ -1343,8 +1678,8 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
     dsum += fx46(dval(i, x0));
     psum += fx46(filtered_of(a, pval(K0, x0)));
   });
-  const uint64_t dtot = block_sum(dsum, f.red);
-  const uint64_t ptot = block_sum(psum, f.red2);
+  const uint64_t dtot = block_sum(dsum, f.red[0]);
+  const uint64_t ptot = block_sum(psum, f.red[1]);
   const bool use_d = dtot > 0;
   const float den = use_d ? mass_to_f32(dtot) : (ptot > 0 ? mass_to_f32(ptot) : 1.0f);
   __syncthreads();
@@ -1355,12 +1690,13 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
 }
 
 // ---------------------------------------------------------------------------
-// Unit finalisation
+// fin_kernel: unit blockIdx.x, after stream_kernel wrote every record
 // ---------------------------------------------------------------------------
 template <int DT>
-__device__ __forceinline__ void finalize_unit(const Params& p, Sh& sh, int unit) {
-  FinSh& f = sh.fin;
+__global__ __launch_bounds__(kFW) void fin_kernel(const Params p) {
+  __shared__ FinSh f;
   const int t = threadIdx.x, w = t / kWave;
+  const int unit = blockIdx.x;
   int g, i, nr;
   int rows[2];
   if (p.mode == kModeSpec) {
@@ -1376,41 +1712,81 @@ __device__ __forceinline__ void finalize_unit(const Params& p, Sh& sh, int unit)
     rows[0] = unit;
     rows[1] = unit;
   }
-  if (t == 0) atomic_store_u32(p.unit_cnt + unit, 0u);
-  if (w < nr) row_setup(p, f, w, rows[w]);
+  // the unit's uniforms and draft token, wanted only at the end: loaded now
+  float u_acc = 0.0f, u_draw = 0.0f;
+  int64_t xdraft = 0;
+  if (p.mode == kModeSpec) {
+    const float* ug = p.uniforms + static_cast<int64_t>(g) * (2 * p.k + 1);
+    if (i < p.k) {
+      u_acc = ug[i];
+      u_draw = ug[p.k + i];
+      xdraft = p.draft_tokens[static_cast<int64_t>(g) * p.k + i];
+    } else {
+      u_draw = ug[2 * p.k];
+    }
+  } else if (p.mode == kModeSample) {
+    u_draw = p.row_uniforms[rows[0]];
+  }
+  // every load of the set-up issued before any result is used: the records
+  // (wave s < nr, row s) first, then every candidate slot of both rows
+  RecPair rp;
+  if (w < nr) rp = load_recs(p, rows[w]);
+  const int nslot = p.nch * p.cap;
+  uint64_t sl[2][kEPT];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const uint64_t* cb = p.cands + static_cast<int64_t>(rows[s]) * nslot;
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      const int e = t + q * kFW;
+      sl[s][q] = (s < nr && e < nslot) ? cb[e] : 0u;
+    }
+  }
+  // cleared while the loads are in flight: the draft hash and the radix bins
+  if (nr == 2) {
+    for (int h = t; h < kHash; h += kFW) f.hash[h] = 0u;
+  }
+#pragma unroll
+  for (int q = 0; q < kSelPer; ++q) {
+    f.u.bins[0][kSelPer * t + q] = 0;
+    f.u.bins[1][kSelPer * t + q] = 0;
+  }
+  if (w < nr) row_setup(p, f, w, rp);
+  __syncthreads();
+  place_slots(p, f, 0, sl[0]);
+  if (nr == 2) place_slots(p, f, 1, sl[1]);
+  __syncthreads();
+  entry_p(p, f, 0, false);
+  if (nr == 2) entry_p(p, f, 1, true);
   __syncthreads();
   RowK K[2];
   for (int s = 0; s < 2; ++s) K[s] = RowK{f.aux[s < nr ? s : 0].mcmax, f.aux[s < nr ? s : 0].s, p.cd};
-  for (int s = 0; s < nr; ++s) load_entries(p, f, s, rows[s], K[s]);
-  __syncthreads();
-  for (int s = 0; s < nr; ++s) resolve_row<DT>(p, f, s, rows[s], K[s]);
+  resolve_rows<DT>(p, f, nr, rows, K);
 
   if (p.mode == kModeSpec) {
     const int k = p.k;
-    const float* ug = p.uniforms + static_cast<int64_t>(g) * (2 * k + 1);
     int64_t token;
     bool acc = false;
     if (i == k) {
-      token = draw_target<DT>(p, f, rows[0], K[0], ug[2 * k]);
+      token = draw_target<DT>(p, f, rows[0], K[0], u_draw);
     } else {
       const RowAux& a0 = f.aux[0];
       const RowAux& a1 = f.aux[1];
       const float P = a0.has_tok ? filtered_of(a0, pval(K[0], a0.xtok)) : 0.0f;
       const float Q = a1.has_tok ? filtered_of(a1, pval(K[1], a1.xtok)) : 0.0f;
-      acc = accept_draw(ug[i], P, Q);
-      const int64_t x = p.draft_tokens[static_cast<int64_t>(g) * k + i];
-      token = acc ? x : draw_residual<DT>(p, f, rows[0], rows[1], K[0], K[1], ug[k + i]);
+      acc = accept_draw(u_acc, P, Q);
+      token = acc ? xdraft : draw_residual<DT>(p, f, rows[0], rows[1], K[0], K[1], u_draw);
     }
-    // publish, then the last of the group's k+1 units writes the outputs
+    // publish, then the last of the batch element's k+1 units writes the outputs
     if (t == 0) {
       store_sc64(p.words + static_cast<int64_t>(g) * (k + 1) + i,
                  static_cast<uint64_t>(token) | (acc ? (1ull << 63) : 0ull));
       drain_stores();
       const uint32_t old = atomic_arrive(p.grp_cnt + g);
-      sh.fin.sel[1] = old == static_cast<uint32_t>(k) ? 1u : 0u;
+      f.last = old == static_cast<uint32_t>(k) ? 1u : 0u;
     }
     __syncthreads();
-    if (sh.fin.sel[1] && t < kWave) {
+    if (f.last && t < kWave) {
       // accepted length: the first rejected position (k if none), 64 positions per pass
       const uint64_t* wg = p.words + static_cast<int64_t>(g) * (k + 1);
       int a = k;
@@ -1433,7 +1809,7 @@ __device__ __forceinline__ void finalize_unit(const Params& p, Sh& sh, int unit)
       }
     }
   } else if (p.mode == kModeSample) {
-    const int64_t token = draw_target<DT>(p, f, rows[0], K[0], p.row_uniforms[rows[0]]);
+    const int64_t token = draw_target<DT>(p, f, rows[0], K[0], u_draw);
     if (t == 0) p.row_tokens[rows[0]] = token;
   } else {
     if (t == 0) {
@@ -1452,71 +1828,7 @@ __device__ __forceinline__ void finalize_unit(const Params& p, Sh& sh, int unit)
       if (p.mass_out) p.mass_out[rows[0]] = filt ? a.mass_f : 1.0f;
     }
   }
-  __syncthreads();
 }
-
-// ---------------------------------------------------------------------------
-// The persistent kernel
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t next_ticket(const Params& p) {
-  const uint32_t x = blockIdx.x & (kTickets - 1);
-  const uint32_t n = atomic_arrive(p.ctl + x * kLineU32);
-  return gridDim.x + x + kTickets * n;
-}
-
-template <int DT, bool PEN>
-__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(kWgPerCu)))
-void fused_kernel(const Params p) {
-  constexpr int EPV = Elem<DT>::kPerVec;
-  constexpr int NVC = kChunk / (kWave * EPV);
-  __shared__ Sh sh;
-  const int t = threadIdx.x, w = t / kWave, lane = t & (kWave - 1);
-  uint32_t q = blockIdx.x;
-  u32x4 cur[NVC], nxt[NVC];
-  uint32_t cpw = 0, npw = 0;
-  if (4 * q + w < static_cast<uint32_t>(p.items)) load_item<DT, NVC>(p, 4 * q + w, cur, cpw);
-  if (t == 0) sh.ticket[2] = next_ticket(p);
-  __syncthreads();
-  uint32_t qn = sh.ticket[2];
-  for (int step = 0;; ++step) {
-    const bool has_next = qn < static_cast<uint32_t>(p.tickets);
-    if (has_next && 4 * qn + w < static_cast<uint32_t>(p.items)) load_item<DT, NVC>(p, 4 * qn + w, nxt, npw);
-    uint32_t tk = 0;
-    if (t == 0 && has_next) tk = next_ticket(p);
-    int done = -1;
-    if (4 * q + w < static_cast<uint32_t>(p.items)) done = stream_item<DT, PEN>(p, sh, w, 4 * q + w, cur, cpw);
-    if (lane == 0) sh.ready[step & 1][w] = done;
-    if (t == 0) sh.ticket[step & 1] = tk;
-    __syncthreads();
-    const uint32_t qnn = sh.ticket[step & 1];
-    int rdy[kNW];
-#pragma unroll
-    for (int r = 0; r < kNW; ++r) rdy[r] = sh.ready[step & 1][r];
-#pragma unroll
-    for (int r = 0; r < kNW; ++r) {
-      if (rdy[r] >= 0) finalize_unit<DT>(p, sh, rdy[r]);
-    }
-    if (!has_next) break;
-    q = qn;
-    qn = qnn;
-#pragma unroll
-    for (int u = 0; u < NVC; ++u) {
-      u32x4 v = nxt[u];
-      asm volatile("" : "+v"(v));
-      cur[u] = v;
-    }
-    cpw = npw;
-  }
-  // the last workgroup out resets the ticket counters for the next call
-  if (t == 0) {
-    const uint32_t old = atomic_arrive(p.ctl + kTickets * kLineU32);
-    if (old + 1u == gridDim.x) {
-      for (int x = 0; x < kTickets; ++x) atomic_store_u32(p.ctl + x * kLineU32, 0u);
-      atomic_store_u32(p.ctl + kTickets * kLineU32, 0u);
-    }
-  }
-}
-
 // ===========================================================================
 // dense_kernel: p and the filtered distribution for one (row, chunk) item
 // ===========================================================================
@@ -1567,25 +1879,20 @@ __global__ __launch_bounds__(kCB) void dense_kernel(const Params p) {
 // Host side
 // ===========================================================================
 struct Layout {
-  uint64_t ctl, unit_cnt, grp_cnt, recs, cands, stats, words, bitmap, total;
+  uint64_t grp_cnt, recs, cands, stats, words, bitmap, total;
 };
 
 int nch_for(int64_t vocab) { return static_cast<int>((vocab + kChunk - 1) / kChunk); }
 int cap_for(int nch) { return nch <= 32 ? 64 : (nch <= 64 ? 32 : 16); }
 
-// Workspace: [ticket + exit counters] [unit counters] [group counters] --
-// every counter at a fixed place sized for the largest call, so that calls of
-// any shape on one workspace find them zero (each call leaves them zero) --
-// then, shaped by the call, [chunk records] [candidates] [row statistics]
-// [published words] [penalty bitmaps].
+// Workspace: [group counters] -- at a fixed place sized for the largest call,
+// so that calls of any shape on one workspace find them zero (each call leaves
+// them zero) -- then, shaped by the call, [chunk records] [candidate slots]
+// [row statistics] [published words] [penalty bitmaps].
 Layout ws_layout(int64_t rows, int64_t words, int64_t groups, int nch) {
   auto al = [](uint64_t x) { return (x + 255u) & ~255ull; };
   Layout l{};
   uint64_t off = 0;
-  l.ctl = off;
-  off = al(off + (kTickets + 1) * kLineU32 * 4u);
-  l.unit_cnt = off;
-  off = al(off + static_cast<uint64_t>(kMaxUnits) * 4u);
   l.grp_cnt = off;
   off = al(off + static_cast<uint64_t>(kMaxSpecBatch) * 4u);
   l.recs = off;
@@ -1604,8 +1911,6 @@ Layout ws_layout(int64_t rows, int64_t words, int64_t groups, int nch) {
 
 void bind_workspace(Params& p, void* ws, const Layout& l) {
   char* b = static_cast<char*>(ws);
-  p.ctl = reinterpret_cast<uint32_t*>(b + l.ctl);
-  p.unit_cnt = reinterpret_cast<uint32_t*>(b + l.unit_cnt);
   p.grp_cnt = reinterpret_cast<uint32_t*>(b + l.grp_cnt);
   p.recs = reinterpret_cast<ChunkRec*>(b + l.recs);
   p.cands = reinterpret_cast<uint64_t*>(b + l.cands);
@@ -1617,13 +1922,13 @@ void bind_workspace(Params& p, void* ws, const Layout& l) {
 template <int DT>
 void launch_dt(const Params& p, hipStream_t st) {
   if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(p.groups)), dim3(kBmB), 0, st, p);
-  const int cap_wgs = device_cu_count() * kWgPerCu;
-  const dim3 grid(p.tickets < cap_wgs ? p.tickets : cap_wgs);
+  const dim3 sgrid(static_cast<unsigned>((p.items + kNW - 1) / kNW));
   if (p.use_pen) {
-    hipLaunchKernelGGL((fused_kernel<DT, true>), grid, dim3(kWG), 0, st, p);
+    hipLaunchKernelGGL((stream_kernel<DT, true>), sgrid, dim3(kWG), 0, st, p);
   } else {
-    hipLaunchKernelGGL((fused_kernel<DT, false>), grid, dim3(kWG), 0, st, p);
+    hipLaunchKernelGGL((stream_kernel<DT, false>), sgrid, dim3(kWG), 0, st, p);
   }
+  hipLaunchKernelGGL((fin_kernel<DT>), dim3(static_cast<unsigned>(p.units)), dim3(kFW), 0, st, p);
   if (p.mode == kModeDense && (p.probs_out || p.filt_out)) {
     hipLaunchKernelGGL((dense_kernel<DT>), dim3(static_cast<unsigned>(p.items)), dim3(kCB), 0, st, p);
   }
@@ -1658,7 +1963,6 @@ int setup_common(Params& p, int dtype, int64_t rows, int64_t vocab, float temper
   p.cap = cap_for(p.nch);
   p.bm_words = p.nch * (kChunk / 32);
   p.items = static_cast<int>(rows * p.nch);
-  p.tickets = (p.items + kNW - 1) / kNW;
   p.cd = kLog2eD / static_cast<double>(temperature);
   p.c = static_cast<float>(p.cd);
   p.use_pen = penalty != 1.0f;

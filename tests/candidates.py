@@ -1,7 +1,7 @@
 """Which finalisation path the sampling kernels take for a row (test helper).
 
 The library's streaming pass keeps, per 2048-element chunk, the elements
-whose chunk-relative e = exp2m(fma(x, c, -mc_j)) reaches 2^-L ("candidates"),
+whose chunk-relative exponent RN32(x c - mc_j) reaches -L ("candidates"),
 L chosen from the chunk's data: the largest level in [0, 31] at which at most
 cap of the lanes' 16-byte vectors hold a candidate (by their vector maxima),
 then lowered while more than cap elements qualify (none kept when even L = 0
@@ -53,7 +53,7 @@ def _chunk_candidates(xs: np.ndarray, c: np.float32, mc: np.float32, cap: int, e
     valid_vec = np.arange(nvc * LANES) * epv < n
     vm = np.where(valid_vec, vec.max(axis=1), -np.inf).astype(np.float32)
     tv = nm.fma32(vm, c, -mc)
-    e = nm.exp2m(nm.fma32(xs, c, -mc))
+    tx = nm.fma32(xs, c, -mc)
 
     def nv(level):
         return int((tv >= np.float32(-level)).sum())
@@ -66,7 +66,7 @@ def _chunk_candidates(xs: np.ndarray, c: np.float32, mc: np.float32, cap: int, e
         else:
             hi = mid - 1
     for level in range(lo, -1, -1):
-        mask = e >= np.float32(2.0 ** -level)
+        mask = tx >= np.float32(-level)
         if mask.sum() <= cap:
             return level, mask
     return -1, np.zeros(n, dtype=bool)
