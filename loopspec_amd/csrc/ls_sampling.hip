@@ -59,7 +59,8 @@ constexpr int64_t kMaxK = 64;
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
-enum ChunkFlag : uint32_t { kChunkOverflow = 1u, kChunkHasTok = 2u };
+// kChunkPenCands: penalised candidates follow the others, in no particular order
+enum ChunkFlag : uint32_t { kChunkOverflow = 1u, kChunkHasTok = 2u, kChunkPenCands = 4u };
 enum RowFlag : uint32_t { kRowFiltered = 1u, kRowList = 2u, kRowEmpty = 4u, kRowSlow = 8u, kRowRefilled = 16u };
 
 // Per-chunk result of the streaming pass.
@@ -562,13 +563,18 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
     }
     for (L = lo; L >= 0; --L) {
       const float th = -static_cast<float>(L);
-      mask = 0;
+      // four interleaved chains of eight: m_q = 2 m_q + (t >= th), a compare
+      // into VCC and one add with carry each
+      uint32_t mq[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int i = 0; i < NE; ++i) {
-        // mask = 2 mask + (t >= th): a compare into VCC and one add with carry
-        asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
-            : "+v"(mask) : "v"(x[i]), "v"(th) : "vcc");
+      for (int i = 0; i < NE / 4; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          asm("v_cmp_ge_f32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
+              : "+v"(mq[q]) : "v"(x[(NE / 4) * q + i]), "v"(th) : "vcc");
+        }
       }
+      mask = (mq[0] << 24) | (mq[1] << 16) | (mq[2] << 8) | mq[3];
       cnt = static_cast<uint32_t>(__builtin_popcount(mask));
       uint32_t own = cnt;
       if constexpr (PEN) {
@@ -586,7 +592,7 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
           }
         }
       }
-      const uint32_t tot = wave_sum_u64(own);
+      const uint32_t tot = lane_bcast_u32(wave_scan_add_u32(own), kWave - 1);
       if (tot <= static_cast<uint32_t>(cap)) {
         cnt = tot;
         break;
@@ -598,26 +604,45 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
     }
   }
 
-  // 8. A candidates, lane-major order: (chunk index << 32 | bits(x))
+  // 8. A candidates in index order, (chunk index << 32 | bits(x)): element e
+  //    of vector u of lane t is chunk element (64 u + t) EPV + e, so vector u
+  //    of every lane precedes vector u + 1. Each lane's per-vector counts,
+  //    8 bits apiece (a vector's total over the lanes is at most cap <= 64),
+  //    go through one wave scan.
   uint64_t* out = p.cands + (static_cast<int64_t>(I.row) * p.nch + I.chunk) * p.cap;
   uint32_t nA = 0;
   if (L >= 0) {
-    const uint32_t own = static_cast<uint32_t>(__builtin_popcount(mask));
-    const uint32_t incl = wave_scan_add_u32(own);
-    nA = lane_bcast_u32(incl, kWave - 1);
-    uint32_t pos = incl - own;
-    while (mask) {
-      const int i = __builtin_clz(mask);
-      mask &= ~(0x80000000u >> i);
-      const int li = ((i / EPV) * kWave + t) * EPV + (i % EPV);
-      const float xv = staged<DT>(st, li);
-      out[pos] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv);
-      ++pos;
+    uint64_t packed = 0;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      const uint32_t vb = (mask >> (32 - (u + 1) * EPV)) & ((1u << EPV) - 1u);
+      packed |= static_cast<uint64_t>(__builtin_popcount(vb)) << (8 * u);
     }
+    const uint64_t incl = wave_scan_add_u64(packed);
+    const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
+    const uint64_t excl = incl - packed;
+    uint32_t base = 0;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      // bits of vector u, element 0 in the top bit
+      uint32_t vb = (mask >> (32 - (u + 1) * EPV)) & ((1u << EPV) - 1u);
+      uint32_t pos = base + static_cast<uint32_t>((excl >> (8 * u)) & 0xffu);
+      while (vb) {
+        const int e = __builtin_clz(vb) - (32 - EPV);
+        vb &= ~(1u << (EPV - 1 - e));
+        const int li = (u * kWave + t) * EPV + e;
+        const float xv = staged<DT>(st, li);
+        out[pos] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv);
+        ++pos;
+      }
+      base += static_cast<uint32_t>((tot >> (8 * u)) & 0xffu);
+    }
+    nA = base;
   }
 
   // 9. penalised sub-chunk: its mass (lane-sequential in (u, element) order,
   //    then the lanes pairwise) and its candidates (appended, any order)
+  const uint32_t nA_plain = nA;
   float pmass = 0.0f;
   bool overflow = L < 0 && mref > -__builtin_inff();
   if constexpr (PEN) {
@@ -668,7 +693,8 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   if (t == 0) {
     ChunkRec* rec = p.recs + static_cast<int64_t>(I.row) * p.nch + I.chunk;
     u32x4* r128 = reinterpret_cast<u32x4*>(rec);
-    const uint32_t flags = (overflow ? kChunkOverflow : 0u) | (has_tok ? kChunkHasTok : 0u);
+    const uint32_t flags = (overflow ? kChunkOverflow : 0u) | (has_tok ? kChunkHasTok : 0u) |
+                           (nA > nA_plain ? kChunkPenCands : 0u);
     r128[0] = u32x4{__float_as_uint(m), __float_as_uint(mass), __float_as_uint(pm), __float_as_uint(pmass)};
     r128[1] = u32x4{static_cast<uint32_t>(overflow ? -1 : L), overflow ? 0u : nA, __float_as_uint(xtok), flags};
   }
@@ -722,7 +748,6 @@ struct FinSh {
     uint64_t pos[kChunk];        // a draw's weights by position in the chosen chunk
     struct {
       uint64_t cum[kRowCap];     // a draw's exclusive prefix masses by entry
-      uint64_t w[kRowCap];       // and its weights
     } dr;
     struct {
       uint32_t sup[kRowCap];     // a residual draw's support entries, compacted
@@ -741,6 +766,7 @@ struct FinSh {
   uint32_t cstart[2][kMaxChunks];  // each chunk's entries in the LDS list
   uint32_t ccount[2][kMaxChunks];
   float bound[2][kMaxChunks];    // per-chunk bound on the p of non-candidates
+  uint8_t plain[2][kMaxChunks];  // the chunk's entries are in index order
   RowAux aux[2];
   uint64_t red[4][2 * kFNW];     // block scan slots (callers alternate buffers)
   uint32_t sel[2];               // radix select: crossing digit per row
@@ -913,11 +939,13 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, cons
     f.bound[s][ja] = ba;
     f.cstart[s][ja] = incl - own;
     f.ccount[s][ja] = na;
+    f.plain[s][ja] = (ra.flags & kChunkPenCands) ? 0 : 1;
   }
   if (ib) {
     f.bound[s][jb] = bb;
     f.cstart[s][jb] = incl - own + na;
     f.ccount[s][jb] = nb;
+    f.plain[s][jb] = (rb.flags & kChunkPenCands) ? 0 : 1;
   }
   const float bmax = wave_max_f32(ba > bb ? ba : bb);
   const bool ta = ia && (ra.flags & kChunkHasTok), tb2 = ib && (rb.flags & kChunkHasTok);
@@ -1110,7 +1138,18 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
           const bool in = static_cast<uint32_t>(lane) < cnt;
           const uint32_t b = in ? f.gbits[s][lane] : 0u;
           uint64_t A = above[s];
-          for (uint32_t j = 0; j < cnt; ++j) A += f.gbits[s][j] >= b ? f.gw[s][j] : 0;
+          for (uint32_t j0 = 0; j0 < cnt; j0 += 8) {
+            uint32_t bj[8];
+            uint64_t wj[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const bool v = j0 + q < cnt;
+              bj[q] = f.gbits[s][v ? j0 + q : 0];
+              wj[q] = v ? f.gw[s][j0 + q] : 0u;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) A += bj[q] >= b ? wj[q] : 0u;
+          }
           const bool good = in && A >= thr[s];
           const uint64_t best = wave_max_u64(good ? b : 0u);
           const uint64_t at = wave_max_u64(good && b == static_cast<uint32_t>(best) ? A : 0u);
@@ -1291,6 +1330,7 @@ __device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, i
   if (t == 0) {
     f.cstart[s][j] = base;
     f.ccount[s][j] = static_cast<uint32_t>(tot);
+    f.plain[s][j] = 1;
     f.aux[s].n = base + static_cast<uint32_t>(tot);
     f.bound[s][j] = 0.0f;
   }
@@ -1323,7 +1363,9 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
   uint32_t mask = 0;
   uint64_t thr[2] = {0u, 0u};
   float top_p[2] = {1.0f, 1.0f};
-  for (int s = 0; s < nr; ++s) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s >= nr) break;
     top_p[s] = row_top_p(p, rows[s]);
     if (top_p[s] < 1.0f && !(f.aux[s].flags & kRowEmpty)) {
       mask |= 1u << s;
@@ -1339,7 +1381,8 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
   if (mask) select_entries(f, mask, thr, cut, mass, ok, true);
   uint32_t flags[2] = {f.aux[0].flags & kRowEmpty, f.aux[1].flags & kRowEmpty};
   bool changed1 = false;
-  for (int s = 0; s < nr; ++s) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
     if (!((mask >> s) & 1u)) continue;  // unfiltered: P = p over the whole row
     flags[s] = kRowFiltered | kRowList;
     if (ok[s] && !(cut[s] > f.aux[s].bmax)) {
@@ -1367,7 +1410,9 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
     }
   }
   if (threadIdx.x == 0) {
-    for (int s = 0; s < nr; ++s) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s >= nr) break;
       RowAux& a = f.aux[s];
       a.flags = flags[s];
       a.top_p = top_p[s];
@@ -1453,11 +1498,11 @@ __device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64
 
 // List-mode draw over slot 0's entries, thread t weighing entries kEPT t + q
 // by wl[q]. With each chunk's entries contiguous and the chunks in order
-// (`ordered`: no chunk was refilled), a scan over the list finds the chunk,
-// and a chunk of at most kWave entries is finished by one wave, which orders
-// its entries by index; otherwise per-chunk sums find the chunk and its
-// entries are scattered to their positions (indices are distinct among
-// entries of nonzero weight).
+// (`ordered`: no chunk was refilled), a scan over the list finds the entry
+// holding the target, which is the draw when its chunk's entries are in index
+// order; otherwise (per-chunk sums find the chunk when not `ordered`) the
+// chunk's entries are scattered to their positions (indices are distinct
+// among entries of nonzero weight) and scanned there.
 __device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t (&wl)[kEPT], float u,
                                              bool ordered) {
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
@@ -1478,44 +1523,18 @@ __device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const ui
       const uint32_t e = kEPT * t + q;
       if (e < n) {
         f.u.dr.cum[e] = run;
-        f.u.dr.w[e] = wl[q];
-        if (run <= target && target < run + wl[q]) f.pick = f.ent[0].eidx[e] >> 11;
+        if (run <= target && target < run + wl[q]) f.pick = e;
       }
       run += wl[q];
     }
     __syncthreads();
-    js = f.pick;
-    const uint32_t s0 = f.cstart[0][js], sc = f.ccount[0][js];
-    rem = target - f.u.dr.cum[s0];
-    if (sc <= static_cast<uint32_t>(kWave)) {
-      if (wid == 0) {
-        // lane l: entry s0 + l, its weight, and the mass of the chunk's
-        // entries of lower index (broadcast reads, eight per step)
-        const bool in = static_cast<uint32_t>(lane) < sc;
-        const uint32_t e = s0 + lane;
-        const uint32_t idx = in ? f.ent[0].eidx[e] : 0xffffffffu;
-        const uint64_t cw = in ? f.u.dr.w[e] : 0u;
-        uint64_t below = 0;
-        for (uint32_t j0 = 0; j0 < sc; j0 += 8) {
-          uint32_t ij[8];
-          uint64_t wj[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const uint32_t j = j0 + q < sc ? j0 + q : sc - 1;
-            ij[q] = f.ent[0].eidx[s0 + j];
-            wj[q] = j0 + q < sc ? f.u.dr.w[s0 + j] : 0u;
-          }
-#pragma unroll
-          for (int q = 0; q < 8; ++q) below += ij[q] < idx ? wj[q] : 0u;
-        }
-        const bool hit = in && cw > 0 && below <= rem && rem < below + cw;
-        const uint64_t hm = __ballot(hit);
-        if (hm && lane == __builtin_ctzll(hm)) f.token = static_cast<int64_t>(idx);
-      }
-      __syncthreads();
-      return f.token;
-    }
-    __syncthreads();  // every read of f.u.cum precedes the position scatter
+    // the entry holding the target; in a chunk whose entries are in index
+    // order it is the draw
+    const uint32_t idx = f.ent[0].eidx[f.pick];
+    js = idx >> 11;
+    if (f.plain[0][js]) return static_cast<int64_t>(idx);
+    rem = target - f.u.dr.cum[f.cstart[0][js]];
+    __syncthreads();  // every read of f.u.dr precedes the position scatter
   } else {
     for (int j = t; j < p.nch; j += kFW) f.csum[j] = 0;
     __syncthreads();
@@ -1693,7 +1712,8 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
 // fin_kernel: unit blockIdx.x, after stream_kernel wrote every record
 // ---------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(kFW) void fin_kernel(const Params p) {
+__global__ __launch_bounds__(kFW) __attribute__((amdgpu_flat_work_group_size(kFW, kFW)))
+void fin_kernel(const Params p) {
   __shared__ FinSh f;
   const int t = threadIdx.x, w = t / kWave;
   const int unit = blockIdx.x;
