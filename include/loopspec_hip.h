@@ -161,6 +161,24 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride,
                    uint64_t workspace_bytes, ls_stream_t stream);
 uint64_t ls_spec_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 
+/* ls_spec_verify without a workspace argument and without allocating: the
+ * scratch is a 16 MiB static device array of the library (one per GPU, held
+ * until the process ends), for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Calls needing more than 16 MiB
+ * (ls_spec_verify_workspace) fail with LS_ERR_VALUE before any launch. Every
+ * call on a GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (concurrent streams) race. Same arguments, results and errors as
+ * ls_spec_verify otherwise. */
+int ls_spec_verify_noalloc(const void* target_logits, int64_t target_batch_stride,
+                           int64_t target_pos_stride, const void* draft_logits,
+                           int64_t draft_batch_stride, int64_t draft_pos_stride,
+                           const int64_t* draft_tokens, const float* uniforms, int dtype,
+                           int64_t batch, int64_t k, int64_t vocab, float temperature,
+                           float top_p, int64_t top_k, float penalty, const int32_t* history,
+                           int64_t history_stride, const int32_t* history_len,
+                           int32_t* accept_len, int64_t* tokens, ls_stream_t stream);
+
 /* Filter each logits row and draw one token per row with uniforms[row]
  * (float32 [rows]) into out_tokens (int64 [rows]); history rows as above,
  * one per logits row; rows <= 65536. Workspace: ls_sample_logits_workspace

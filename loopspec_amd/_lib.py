@@ -53,6 +53,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _P, _I64, _P, _P, _P, _P, _U64, _P],
     ),
     "ls_spec_verify_workspace": (_U64, [_I64, _I64, _I64]),
+    "ls_spec_verify_noalloc": (
+        _I32,
+        [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I32, _I64, _I64, _I64, _F32, _F32, _I64, _F32,
+         _P, _I64, _P, _P, _P, _P],
+    ),
     "ls_sample_logits": (
         _I32, [_P, _I64, _I32, _I64, _I64, _F32, _F32, _I64, _F32, _P, _I64, _P, _P, _P, _P, _U64, _P],
     ),

@@ -37,6 +37,8 @@
 // The arithmetic is the declared arithmetic of ls_numerics.hpp, restated by
 // oracle/sampling.py and oracle/native/ls_oracle.c, so every output is
 // bit-identical to the oracle's.
+#include <mutex>
+
 #include "ls_common.hpp"
 #include "ls_numerics.hpp"
 #include "ls_runtime.hpp"
@@ -1994,8 +1996,54 @@ int setup_common(Params& p, int dtype, int64_t rows, int64_t vocab, float temper
   return LS_OK;
 }
 
+// Zeroes n 32-bit words (a kernel, not a memset, so that it may be captured
+// into a graph and replayed).
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
 }  // namespace
 }  // namespace ls
+
+// ---------------------------------------------------------------------------
+// Static scratch of ls_spec_verify_noalloc: the workspace of one call, kept in
+// this GPU's copy of a file-scope array for the life of the process. Host code
+// uses the address hipGetSymbolAddress returns for the current device, never
+// the array's name.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20;  // 16 MiB per GPU
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // per device, null until set up
+
+// The current device's scratch address. The first call on a device looks it
+// up and zeroes the group counters there (on `st`); every call leaves them
+// zero again.
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  LS_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices) return ls::fail(LS_ERR_RUNTIME, "spec_verify_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return ls::hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return ls::fail(LS_ERR_RUNTIME, "spec_verify_noalloc: no scratch address");
+    const int64_t words = ls::kMaxSpecBatch;  // the group counters at the workspace's start
+    hipLaunchKernelGGL(ls::zero_words_kernel, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, st,
+                       static_cast<uint32_t*>(p), words);
+    const int rc = ls::check_launch("spec_verify_noalloc scratch set-up");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LS_OK;
+}
+}  // namespace
 
 using namespace ls;
 
@@ -2045,6 +2093,26 @@ int ls_spec_verify(const void* target_logits, int64_t target_batch_stride, int64
   if (!workspace || ws_bytes < l.total) return fail(LS_ERR_VALUE, "spec_verify: workspace too small");
   bind_workspace(p, workspace, l);
   return launch(p, dtype, static_cast<hipStream_t>(stream));
+}
+
+int ls_spec_verify_noalloc(const void* target_logits, int64_t target_batch_stride, int64_t target_pos_stride,
+                           const void* draft_logits, int64_t draft_batch_stride, int64_t draft_pos_stride,
+                           const int64_t* draft_tokens, const float* uniforms, int dtype, int64_t batch, int64_t k,
+                           int64_t vocab, float temperature, float top_p, int64_t top_k, float penalty,
+                           const int32_t* history, int64_t history_stride, const int32_t* history_len,
+                           int32_t* accept_len, int64_t* tokens, ls_stream_t stream) {
+  const uint64_t need = (batch > 0 && k >= 1 && vocab > 0) ? ls_spec_verify_workspace(batch, k, vocab) : 0;
+  if (need > kNoAllocScratchBytes)
+    return fail(LS_ERR_VALUE, "spec_verify_noalloc: the call needs " + std::to_string(need) +
+                                  " bytes of scratch, above the 16 MiB static scratch; use ls_spec_verify with a workspace");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(st, &ws);
+  if (rc) return rc;
+  return ls_spec_verify(target_logits, target_batch_stride, target_pos_stride, draft_logits, draft_batch_stride,
+                        draft_pos_stride, draft_tokens, uniforms, dtype, batch, k, vocab, temperature, top_p, top_k,
+                        penalty, history, history_stride, history_len, accept_len, tokens, ws, kNoAllocScratchBytes,
+                        stream);
 }
 
 uint64_t ls_sample_logits_workspace(int64_t rows, int64_t vocab) {
