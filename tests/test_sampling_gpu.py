@@ -12,6 +12,7 @@ import torch
 
 from oracle import numerics as nm
 from oracle import sampling as osmp
+from oracle import torch_ref
 from loopspec_amd import philox, verify, workloads
 from tests import candidates
 from tests.conftest import announce
@@ -294,6 +295,61 @@ def test_spec_verify_c4_full_shape(gpu, seed):
     want = oracle_spec(cfg, inp, drafts)
     assert np.array_equal(acc, want.accept_len)
     assert np.array_equal(tok, want.tokens)
+
+
+def _exact_support(row64: np.ndarray, top_p: float) -> np.ndarray:
+    """Top-p support of the exact (binary64) softmax of a processed row."""
+    e = np.exp(row64 - row64.max())
+    p = e / e.sum()
+    srt = np.sort(p)[::-1]
+    idx = min(int(np.searchsorted(np.cumsum(srt), top_p, side="left")), len(p) - 1)
+    return p >= srt[idx]
+
+
+@pytest.mark.parametrize("name,seed", [("C3", 0), ("C3", 1), ("C4", 5), ("C4", 2003)])
+def test_full_shape_matches_torch_reference(gpu, name, seed):
+    """The library at the full BASELINE shapes against the reference's own torch
+    formulation (oracle.torch_ref, drafts drawn from its q): ls_spec_verify's
+    accept lengths and tokens are identical, and ls_filter_logits keeps the same
+    top-p set on every row, except rows where the reference's binary32
+    cumulative mass crosses top_p at another index than the exact (binary64)
+    softmax does; there the library must keep the exact set (at most two such
+    rows per case). With a penalty the rows are penalised by the reference's
+    closed form on the host before ls_filter_logits (it takes no history)."""
+    cfg = {"C3": workloads.C3, "C4": workloads.C4}[name]
+    inp = workloads.sampling_inputs(cfg, seed)
+    b_n, k, v = cfg.batch, cfg.k, cfg.vocab
+    tl, dl = inp["target"].float(), inp["draft"].float()
+    hist = None
+    if cfg.penalty != 1.0:
+        hist = [inp["history"][i, : int(inp["history_len"][i])] for i in range(b_n)]
+    rows_all, ref_all = [], []
+    drafts = torch.zeros(b_n, k, dtype=torch.int64)
+    for i in range(b_n):
+        rows = torch.cat([tl[i], dl[i]])
+        if hist is not None:
+            rows = torch_ref.apply_penalty(rows, hist[i], cfg.penalty)
+        ref = torch_ref.filtered_probabilities(rows, cfg.temperature, 1 << 30, cfg.top_p)
+        drafts[i] = torch_ref.categorical_pick(ref[k + 1:], inp["draft_uniforms"][i])
+        rows_all.append(rows)
+        ref_all.append(ref)
+    proc = torch.cat(rows_all).contiguous()
+    announce(f"filter_logits {name} full seed={seed} rows={proc.shape[0]}")
+    got = verify.filter_logits(proc.to(gpu), cfg.temperature, cfg.top_p)["filtered"].cpu()
+    ref_p = torch.cat(ref_all)
+    boundary = 0
+    for r in range(proc.shape[0]):
+        if not torch.equal(got[r] > 0, ref_p[r] > 0):
+            exact = _exact_support(proc[r].double().numpy() / float(np.float32(cfg.temperature)), cfg.top_p)
+            assert np.array_equal(got[r].numpy() > 0, exact), r
+            boundary += 1
+    assert boundary <= 2, boundary
+    announce(f"spec {name} full seed={seed} vs torch reference")
+    acc, tok = run_spec(cfg, inp, drafts, gpu)
+    a_ref, t_ref = torch_ref.speculative_verify(tl, dl, drafts, inp["uniforms"], cfg.temperature, cfg.top_p,
+                                                cfg.penalty, hist)
+    assert np.array_equal(acc, a_ref.numpy())
+    assert np.array_equal(tok, t_ref.numpy())
 
 
 @pytest.mark.parametrize("variant", ["unfiltered", "flat", "forced_reject", "k1", "k3_fp16"])
