@@ -26,6 +26,7 @@ import subprocess
 import sys
 import time
 
+import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth, GB/s
@@ -301,6 +302,40 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
     }
 
 
+def _check_commit_step(step, state, acc, dst, status, page_size: int, k: int) -> None:
+    """One more eager step, its tables checked against the commit's definition:
+    row b's accepted tokens land at positions ctx..ctx+a-1 of its page table,
+    pages it did not own are the next ring entries in batch order, owned
+    entries are unchanged, ctx grows by a and the ring cursor by the pages
+    taken."""
+    before = {n: state[n].cpu().numpy().copy() for n in ("page_table", "ctx_len", "page_state", "free_pages")}
+    step(0)
+    torch.cuda.synchronize()
+    if status.item() != 0:
+        raise RuntimeError("C5 check step: commit reported a failed row")
+    a = acc[0].cpu().numpy().astype(np.int64)
+    pt, ctx = state["page_table"].cpu().numpy(), state["ctx_len"].cpu().numpy()
+    cur, ring = int(state["page_state"][0].item()), before["free_pages"]
+    d = dst.cpu().numpy()
+    nxt = int(before["page_state"][0])
+    for b in range(len(a)):
+        c0 = int(before["ctx_len"][b])
+        owned, after = -(-c0 // page_size), -(-(c0 + int(a[b])) // page_size)
+        ok = ctx[b] == c0 + a[b] and np.array_equal(pt[b, :owned], before["page_table"][b, :owned])
+        for i in range(owned, after):
+            ok = ok and pt[b, i] == ring[nxt % len(ring)]
+            nxt += 1
+        for j in range(k):
+            pos = c0 + j
+            want = int(pt[b, pos // page_size]) * page_size + pos % page_size if j < a[b] else -1
+            ok = ok and d[b, j] == want
+        if not ok:
+            raise RuntimeError(f"C5 check step: row {b}'s commit tables differ from their definition")
+    if cur != nxt:
+        raise RuntimeError("C5 check step: the ring cursor moved by another count than the pages taken")
+    _log("C5 check step: destination slots, page table, ctx_len and ring cursor verified")
+
+
 def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
     """C5: C3 sampling verify at B=128, then the paged commit of each row's
     accepted draft tokens' KV (24 layers x 4 loops x {K, V}, 16 heads x 128,
@@ -332,12 +367,13 @@ def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
         verify.speculative_verify(s["target"], s["draft"], s["draft_tokens"], s["uniforms"], cfg.temperature,
                                   cfg.top_p, accept_len=acc[i], tokens=tok[i], workspace=ws)
         graph_ops.commit_kv(state["kv"], acc[i], state["branch_slots"], state["page_table"], state["ctx_len"],
-                            state["free_pages"], state["page_cursor"], kvc.page_size, dst_slots=dst,
+                            state["free_pages"], state["page_state"], kvc.page_size, dst_slots=dst,
                             status=status)
 
     ms_per_step, timed, wsteps = _time_graph(step, nsets, steps, warmup)
     if status.item() != 0:
         raise RuntimeError("C5 commit reported an out-of-range page (page table too narrow)")
+    _check_commit_step(step, state, acc, dst, status, kvc.page_size, cfg.k)
     accepted = acc.sum().item() / nsets
     logit_bytes = workloads.sampling_algorithmic_bytes(cfg)
     kv_bytes = workloads.kv_commit_algorithmic_bytes(kvc, cfg.batch, cfg.k, int(round(accepted)))

@@ -354,19 +354,26 @@ int ls_copy_state_rows(const void* source, void* destination, const int64_t* row
  * to [0, k]) branch tokens (branch_slots int64 [B, k]) at positions ctx_len[b]..
  * of its page table (int32 [B, max_pages]); a position in a page the row does
  * not own yet (page index >= ceil(ctx_len/page_size)) takes the next page of the
- * free-page ring free_pages[(*page_cursor + i) % ring_size] in batch order. Writes
- * dst_slots int64 [B, k] (-1 for non-accepted tokens), updates page_table,
- * ctx_len and *page_cursor, then copies every plane's token row from the branch
- * slot to the destination slot. Out-of-range pages/slots are skipped and set
- * *status |= 1 (status may be NULL). planes == 0 runs only the slot plan.
- * The reference's own commit is an ownership transfer of page-size-1 slots
- * (sglang_recurrent/loopspec/branching/manager.py:410-482); this is the paged
- * counterpart with the same ring-allocation rule (graph_ops.py:117-134). */
+ * free-page ring free_pages[page_state[0] % ring_size], page_state[0]+1, ... in
+ * batch order. page_state int64 [2] = {next, end}: ring entries next .. end-1
+ * hold free pages (the caller advances end as it returns pages to the ring).
+ * Writes dst_slots int64 [B, k] (-1 for tokens not committed), updates
+ * page_table, ctx_len and page_state[0], then copies every plane's token row
+ * from the branch slot to the destination slot. A row whose tokens would reach
+ * past its page table, or land on a page id outside [0, num_pages), commits
+ * nothing and keeps its page table and ctx_len (*status |= 1). If the rows
+ * together want more pages than next .. end-1 holds, no page is allocated:
+ * every row that wanted one commits nothing (*status |= 2); rows that fit in
+ * their own pages still commit. status may be NULL. planes == 0 runs only the
+ * slot plan. The reference's own commit is an ownership transfer of
+ * page-size-1 slots (sglang_recurrent/loopspec/branching/manager.py:410-482);
+ * this is the paged counterpart with the same ring-allocation rule
+ * (graph_ops.py:117-134). */
 int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t token_bytes,
                  int64_t num_pages, int64_t page_size, const int32_t* accept_len,
                  const int64_t* branch_slots, int64_t batch, int64_t k, int32_t* page_table,
                  int64_t max_pages, int64_t* ctx_len, const int64_t* free_pages,
-                 int64_t ring_size, int64_t* page_cursor, int64_t* dst_slots, int32_t* status,
+                 int64_t ring_size, int64_t* page_state, int64_t* dst_slots, int32_t* status,
                  ls_stream_t stream);
 
 #ifdef __cplusplus

@@ -119,62 +119,108 @@ __global__ __launch_bounds__(kCopyBlock) void copy_rows_kernel(const char* __res
 }
 
 // Page allocation and destination slots for the commit (one workgroup).
+// page_state = {next, end}: ring entries next .. end - 1 (mod ring) hold free
+// pages. Row b wants the pages its accepted tokens reach beyond the ones it
+// owns; a row whose tokens would reach past its page table (max_pages) is
+// bad (status bit 1). When the good rows together want more pages than the
+// ring holds, nothing is allocated, every row that wanted a page is bad and
+// status bit 2 is set. Otherwise the wanted pages are taken in batch order; a
+// row meeting a page id outside the pool (in the ring or its table) is bad
+// (status bit 1), its ring entries consumed. A bad row keeps its page table
+// and ctx_len and gets no destination slots (-1).
+__device__ __forceinline__ void kv_row_need(const int32_t* accept_len, const int64_t* ctx_len, int64_t b, int k,
+                                            int page_size, int64_t max_pages, int64_t* a, int64_t* ctx,
+                                            int64_t* owned, int64_t* need, bool* fits) {
+  int64_t av = accept_len[b];
+  av = av < 0 ? 0 : (av > k ? k : av);
+  const int64_t c = ctx_len[b];
+  const int64_t own = (c + page_size - 1) / page_size;
+  const int64_t after = (c + av + page_size - 1) / page_size;
+  *a = av;
+  *ctx = c;
+  *owned = own;
+  *need = after > own ? after - own : 0;
+  *fits = after <= max_pages;
+}
+
 __global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
     const int32_t* __restrict__ accept_len, int64_t batch, int k, int page_size, int64_t max_pages,
     int64_t num_pages, int32_t* __restrict__ page_table, int64_t* __restrict__ ctx_len,
-    const int64_t* __restrict__ free_pages, int64_t ring, int64_t* page_cursor, int64_t* __restrict__ dst_slots,
+    const int64_t* __restrict__ free_pages, int64_t ring, int64_t* page_state, int64_t* __restrict__ dst_slots,
     int32_t* status) {
   __shared__ uint32_t red[kScanBlock / kWave];
-  const int64_t base = *page_cursor;
+  const int64_t next = page_state[0], end = page_state[1];
+  // pass 1: pages wanted by the rows that fit their page table
+  int64_t wanted = 0;
+  for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
+    const int64_t b = b0 + threadIdx.x;
+    int64_t a = 0, ctx = 0, owned = 0, need = 0;
+    bool fits = true;
+    if (b < batch) kv_row_need(accept_len, ctx_len, b, k, page_size, max_pages, &a, &ctx, &owned, &need, &fits);
+    uint32_t total;
+    block_excl_scan_u32(static_cast<uint32_t>(fits ? need : 0), red, &total);
+    wanted += total;
+  }
+  const bool enough = next + wanted <= end;
+  // pass 2: allocate (all or nothing), destination slots, context lengths
   int64_t carry = 0;
   for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
     const int64_t b = b0 + threadIdx.x;
     int64_t a = 0, ctx = 0, owned = 0, need = 0;
-    if (b < batch) {
-      a = accept_len[b];
-      a = a < 0 ? 0 : (a > k ? k : a);
-      ctx = ctx_len[b];
-      owned = (ctx + page_size - 1) / page_size;
-      const int64_t pages_after = (ctx + a + page_size - 1) / page_size;
-      need = pages_after > owned ? pages_after - owned : 0;
-    }
+    bool fits = true;
+    if (b < batch) kv_row_need(accept_len, ctx_len, b, k, page_size, max_pages, &a, &ctx, &owned, &need, &fits);
+    const int64_t take = (fits && enough) ? need : 0;
     uint32_t total;
-    const uint32_t excl = block_excl_scan_u32(static_cast<uint32_t>(need), red, &total);
+    const uint32_t excl = block_excl_scan_u32(static_cast<uint32_t>(take), red, &total);
     if (b < batch) {
-      bool bad = false;
       int32_t* pt = page_table + b * max_pages;
-      for (int64_t i = 0; i < need; ++i) {
-        const int64_t pidx = owned + i;
-        int64_t ro = (base + carry + excl + i) % ring;
+      int32_t bits = 0;
+      bool bad = false;
+      if (!fits) {
+        bad = true;
+        bits |= 1;
+      } else if (need > 0 && !enough) {
+        bad = true;
+        bits |= 2;
+      }
+      auto ring_page = [&](int64_t i) -> int64_t {
+        int64_t ro = (next + carry + excl + i) % ring;
         ro += ro < 0 ? ring : 0;
-        const int64_t page = free_pages[ro];
-        if (pidx < max_pages) {
-          pt[pidx] = static_cast<int32_t>(page);
-        } else {
-          bad = true;
+        return free_pages[ro];
+      };
+      if (!bad) {
+        // every page the accepted tokens land on must lie in the pool
+        for (int64_t i = 0; i < take; ++i) {
+          const int64_t page = ring_page(i);
+          if (page < 0 || page >= num_pages) bad = true;
         }
+        for (int j = 0; j < a; ++j) {
+          const int64_t pidx = (ctx + j) / page_size;
+          if (pidx < owned) {
+            const int64_t page = pt[pidx];
+            if (page < 0 || page >= num_pages) bad = true;
+          }
+        }
+        if (bad) bits |= 1;
+      }
+      if (!bad) {
+        for (int64_t i = 0; i < take; ++i) pt[owned + i] = static_cast<int32_t>(ring_page(i));
       }
       for (int j = 0; j < k; ++j) {
         int64_t slot = -1;
-        if (j < a) {
+        if (!bad && j < a) {
           const int64_t pos = ctx + j;
-          const int64_t pidx = pos / page_size;
-          const int64_t page = pidx < max_pages ? pt[pidx] : -1;
-          if (page >= 0 && page < num_pages) {
-            slot = page * page_size + pos % page_size;
-          } else {
-            bad = true;
-          }
+          slot = static_cast<int64_t>(pt[pos / page_size]) * page_size + pos % page_size;
         }
         dst_slots[b * k + j] = slot;
       }
-      ctx_len[b] = ctx + a;
-      if (bad && status) atomicOr(status, 1);
+      if (!bad) ctx_len[b] = ctx + a;
+      if (bits && status) atomicOr(status, bits);
     }
     carry += total;
   }
   __syncthreads();
-  if (threadIdx.x == 0) *page_cursor = base + carry;
+  if (threadIdx.x == 0) page_state[0] = next + carry;
 }
 
 // One workgroup per (token, group of planes): copy the token's row of every
@@ -464,13 +510,13 @@ int ls_copy_state_rows(const void* source, void* destination, const int64_t* row
 int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t token_bytes, int64_t num_pages,
                  int64_t page_size, const int32_t* accept_len, const int64_t* branch_slots, int64_t batch, int64_t k,
                  int32_t* page_table, int64_t max_pages, int64_t* ctx_len, const int64_t* free_pages,
-                 int64_t ring_size, int64_t* page_cursor, int64_t* dst_slots, int32_t* status, ls_stream_t stream) {
+                 int64_t ring_size, int64_t* page_state, int64_t* dst_slots, int32_t* status, ls_stream_t stream) {
   if (batch < 0 || k < 1 || k > 64 || page_size <= 0 || page_size > (1 << 20) || max_pages <= 0 || num_pages <= 0 ||
       ring_size <= 0 ||
       planes < 0 || token_bytes <= 0)
     return fail(LS_ERR_VALUE, "kv_commit: invalid shape");
   if (batch == 0) return LS_OK;
-  if (!accept_len || !branch_slots || !page_table || !ctx_len || !free_pages || !page_cursor || !dst_slots)
+  if (!accept_len || !branch_slots || !page_table || !ctx_len || !free_pages || !page_state || !dst_slots)
     return fail(LS_ERR_VALUE, "kv_commit: NULL pointer");
   if (planes > 0 && (!kv || token_bytes % 16 != 0 || plane_stride_bytes % 16 != 0 || !aligned16(kv)))
     return fail(LS_ERR_VALUE, "kv_commit: KV rows must be 16-byte aligned multiples of 16 bytes");
@@ -479,7 +525,7 @@ int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t t
   const auto st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(kv_plan_kernel, dim3(1), dim3(kScanBlock), 0, st, accept_len, batch, static_cast<int>(k),
                      static_cast<int>(page_size), max_pages, num_pages, page_table, ctx_len, free_pages, ring_size,
-                     page_cursor, dst_slots, status);
+                     page_state, dst_slots, status);
   int rc = check_launch("kv_commit plan launch");
   if (rc || planes == 0) return rc;
   const int ppw = 8;

@@ -118,32 +118,35 @@ def update_request_mapping(mapping: Any, request_rows: Any, source_rows: Any, co
 
 def commit_kv(kv: torch.Tensor | None, accept_len: torch.Tensor, branch_slots: torch.Tensor,
               page_table: torch.Tensor, ctx_len: torch.Tensor, free_pages: torch.Tensor,
-              page_cursor: torch.Tensor, page_size: int, *, dst_slots: torch.Tensor | None = None,
+              page_state: torch.Tensor, page_size: int, *, dst_slots: torch.Tensor | None = None,
               status: torch.Tensor | None = None) -> torch.Tensor:
     """Commit each row's accepted branch tokens into its main KV timeline.
 
     kv: [planes, num_pages * page_size, *token_shape] (planes = layers x loops x
     {K, V}) or None to only plan. accept_len int32 [B]; branch_slots int64
     [B, k]; page_table int32 [B, max_pages]; ctx_len int64 [B]; free_pages
-    int64 ring; page_cursor int64 scalar. Positions ctx_len.. take the row's
-    pages, new pages come from the ring in batch order (the allocation rule of
-    graph_ops.py:117-134); page_table, ctx_len and page_cursor are updated in
+    int64 ring; page_state int64 [2] = (next, end): ring entries next .. end-1
+    hold free pages. Positions ctx_len.. take the row's pages, new pages come
+    from the ring in batch order (the allocation rule of graph_ops.py:117-134);
+    page_table, ctx_len and page_state[0] are updated in
     place and every plane's token row is copied branch slot -> destination slot.
     Returns dst_slots int64 [B, k] (-1 for tokens that were not accepted).
     The reference's own commit is an ownership transfer of page-size-1 slots
     (sglang_recurrent/loopspec/branching/manager.py:410-482).
     """
     for t, n in ((accept_len, "accept_len"), (branch_slots, "branch_slots"), (page_table, "page_table"),
-                 (ctx_len, "ctx_len"), (free_pages, "free_pages"), (page_cursor, "page_cursor")):
+                 (ctx_len, "ctx_len"), (free_pages, "free_pages"), (page_state, "page_state")):
         _lib.require_cuda(t, "commit_kv " + n)
         if not t.is_contiguous():
             raise ValueError(f"commit_kv: {n} must be contiguous")
     if accept_len.dtype != torch.int32 or page_table.dtype != torch.int32:
         raise ValueError("commit_kv: accept_len and page_table must be int32")
     for t, n in ((branch_slots, "branch_slots"), (ctx_len, "ctx_len"), (free_pages, "free_pages"),
-                 (page_cursor, "page_cursor")):
+                 (page_state, "page_state")):
         if t.dtype != torch.int64:
             raise ValueError(f"commit_kv: {n} must be int64")
+    if page_state.numel() != 2:
+        raise ValueError("commit_kv: page_state must hold (next, end)")
     batch, k = branch_slots.shape
     if dst_slots is None:
         dst_slots = torch.empty((batch, k), dtype=torch.int64, device=branch_slots.device)
@@ -162,7 +165,7 @@ def commit_kv(kv: torch.Tensor | None, accept_len: torch.Tensor, branch_slots: t
     _lib.call(
         "ls_kv_commit", kv_ptr, planes, plane_bytes, token_bytes, num_pages, page_size, accept_len.data_ptr(),
         branch_slots.data_ptr(), batch, k, page_table.data_ptr(), page_table.shape[1], ctx_len.data_ptr(),
-        free_pages.data_ptr(), free_pages.shape[0], page_cursor.data_ptr(), dst_slots.data_ptr(),
+        free_pages.data_ptr(), free_pages.shape[0], page_state.data_ptr(), dst_slots.data_ptr(),
         _lib.ptr(status), _lib.stream(branch_slots.device),
     )
     return dst_slots

@@ -210,7 +210,7 @@ def kv_commit_state(kv: KVCommitConfig, batch: int, k: int, steps: int, seed: in
         "page_table": torch.from_numpy(pt).to(device),
         "ctx_len": torch.from_numpy(ctx).to(device),
         "free_pages": torch.from_numpy(ring).to(device),
-        "page_cursor": torch.zeros((), dtype=torch.int64, device=device),
+        "page_state": torch.tensor([0, 1 << 62], dtype=torch.int64, device=device),
         "branch_slots": torch.from_numpy(branch).to(device),
         "kv": torch.empty((kv.planes, num_pages * ps, kv.heads, kv.head_dim), dtype=kv.dtype, device=device),
         "num_pages": num_pages,

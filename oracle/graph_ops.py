@@ -63,37 +63,68 @@ def copy_state_rows(source: np.ndarray, destination: np.ndarray, row_indices, ga
     return destination
 
 
-def kv_commit_plan(accept_len, branch_slots, page_table, ctx_len, free_pages, page_cursor: int, page_size: int):
+def kv_commit_plan(accept_len, branch_slots, page_table, ctx_len, free_pages, page_state, page_size: int,
+                   num_pages: int | None = None):
     """Paged commit of accepted draft tokens from the branch into the main timeline.
 
-    Row b appends its first accept_len[b] branch tokens at positions
-    ctx_len[b], ctx_len[b]+1, ... of its page table. A position in a page that
-    the row does not own yet (page index >= ceil(ctx_len / page_size)) takes the
-    next page of the free-page ring, in batch order and then page order, exactly
-    like allocate_decode_slots assigns ring entries (graph_ops.py:117-134). The
-    destination slot of position p is page_table[b, p // page_size] * page_size
-    + p % page_size. Returns (dst_slots [B, k] int64 with -1 for non-accepted
-    tokens, page_table', ctx_len', page_cursor') and leaves the inputs unchanged.
+    Row b appends its first accept_len[b] (clamped to [0, k]) branch tokens at
+    positions ctx_len[b], ctx_len[b]+1, ... of its page table. A position in a
+    page the row does not own yet (page index >= ceil(ctx_len / page_size))
+    takes the next page of the free-page ring, in batch order and then page
+    order, exactly like allocate_decode_slots assigns ring entries
+    (graph_ops.py:117-134). page_state = (next, end): ring entries next ..
+    end - 1 (mod len(free_pages)) hold free pages. The destination slot of
+    position p is page_table[b, p // page_size] * page_size + p % page_size.
+
+    Failures commit nothing for the row concerned (page table and ctx_len kept,
+    destination slots -1): tokens reaching past the page table's width, or a
+    page id outside [0, num_pages) (status bit 1, its ring entries consumed);
+    when the rows together want more pages than the ring holds, no page is
+    allocated and every row that wanted one fails (status bit 2).
+    Returns (dst_slots [B, k] int64, page_table', ctx_len', (next', end),
+    status) and leaves the inputs unchanged.
     """
     pt = np.array(page_table, copy=True)
     cl = np.array(ctx_len, dtype=np.int64, copy=True)
-    B, k = np.asarray(branch_slots).shape
+    bs = np.asarray(branch_slots)
+    B, k = bs.shape
+    max_pages = pt.shape[1]
+    npages = (1 << 62) if num_pages is None else int(num_pages)
     dst = np.full((B, k), -1, dtype=np.int64)
     cap = len(free_pages)
-    cur = int(page_cursor)
+    nxt, end = int(page_state[0]), int(page_state[1])
+    rows = []
     for b in range(B):
-        a = int(accept_len[b])
-        owned = -(-int(cl[b]) // page_size)
+        a = min(max(int(accept_len[b]), 0), k)
+        ctx = int(cl[b])
+        owned = -(-ctx // page_size)
+        after = -(-(ctx + a) // page_size)
+        rows.append((a, ctx, owned, max(after - owned, 0), after <= max_pages))
+    wanted = sum(need for (_, _, _, need, fits) in rows if fits)
+    enough = nxt + wanted <= end
+    status = 0
+    cur = nxt
+    for b, (a, ctx, owned, need, fits) in enumerate(rows):
+        if not fits:
+            status |= 1
+            continue
+        if need > 0 and not enough:
+            status |= 2
+            continue
+        take = need if enough else 0
+        pages = [int(free_pages[(cur + i) % cap]) for i in range(take)]
+        cur += take
+        touched = pages + [int(pt[b, (ctx + j) // page_size]) for j in range(a) if (ctx + j) // page_size < owned]
+        if any(pg < 0 or pg >= npages for pg in touched):
+            status |= 1
+            continue
+        for i, pg in enumerate(pages):
+            pt[b, owned + i] = np.int32(pg)
         for j in range(a):
-            pos = int(cl[b]) + j
-            pidx = pos // page_size
-            if pidx >= owned:
-                pt[b, pidx] = np.int32(free_pages[cur % cap])
-                cur += 1
-                owned += 1
-            dst[b, j] = int(pt[b, pidx]) * page_size + pos % page_size
-        cl[b] += a
-    return dst, pt, cl, cur
+            pos = ctx + j
+            dst[b, j] = int(pt[b, pos // page_size]) * page_size + pos % page_size
+        cl[b] = ctx + a
+    return dst, pt, cl, (cur, end), status
 
 
 def kv_commit_copy(kv: np.ndarray, branch_slots, dst_slots):

@@ -140,32 +140,71 @@ def test_kv_commit(gpu, page_size):
     announce(f"kv_commit page_size={page_size}")
     t = {n: torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for n, a in
          (("acc", acc), ("branch", branch), ("pt", pt), ("ctx", ctx), ("ring", ring))}
-    t_cur = torch.tensor(cursor, dtype=torch.int64, device=gpu)
+    t_cur = torch.tensor([cursor, cursor + len(ring)], dtype=torch.int64, device=gpu)
     t_kv = kv.to(gpu)
     status = torch.zeros(1, dtype=torch.int32, device=gpu)
     dst = go.commit_kv(t_kv, t["acc"], t["branch"], t["pt"], t["ctx"], t["ring"], t_cur, page_size, status=status)
-    wdst, wpt, wcl, wcur = og.kv_commit_plan(acc, branch, pt, ctx, ring, cursor, page_size)
+    wdst, wpt, wcl, wstate, wstatus = og.kv_commit_plan(acc, branch, pt, ctx, ring, (cursor, cursor + len(ring)),
+                                                        page_size, num_pages)
     assert np.array_equal(dst.cpu().numpy(), wdst)
     assert np.array_equal(t["pt"].cpu().numpy(), wpt)
     assert np.array_equal(t["ctx"].cpu().numpy(), wcl)
-    assert t_cur.item() == wcur
-    assert status.item() == 0
+    assert tuple(t_cur.cpu().tolist()) == wstate
+    assert status.item() == wstatus == 0
     want_kv = og.kv_commit_copy(kv.view(torch.int16).numpy().copy(), branch, wdst)
     assert np.array_equal(t_kv.cpu().view(torch.int16).numpy(), want_kv)
 
 
 def test_kv_commit_reports_overflow(gpu):
-    """A row whose pages would exceed its page-table width is skipped and flagged."""
-    pt = torch.tensor([[0, 1]], dtype=torch.int32, device=gpu)
-    ctx = torch.tensor([4], dtype=torch.int64, device=gpu)  # page_size 2: both entries owned
-    acc = torch.tensor([2], dtype=torch.int32, device=gpu)
-    branch = torch.tensor([[8, 9]], dtype=torch.int64, device=gpu)
-    ring = torch.tensor([3], dtype=torch.int64, device=gpu)
-    cur = torch.zeros((), dtype=torch.int64, device=gpu)
+    """A row whose pages would exceed its page-table width commits nothing,
+    keeps its context length and is flagged; the other row commits."""
+    pt = torch.tensor([[0, 1], [2, -1]], dtype=torch.int32, device=gpu)
+    ctx = torch.tensor([4, 1], dtype=torch.int64, device=gpu)  # page_size 2: row 0 owns both entries
+    acc = torch.tensor([2, 2], dtype=torch.int32, device=gpu)
+    branch = torch.tensor([[8, 9], [10, 11]], dtype=torch.int64, device=gpu)
+    ring = torch.tensor([3, 4], dtype=torch.int64, device=gpu)
+    state = torch.tensor([0, 2], dtype=torch.int64, device=gpu)
     status = torch.zeros(1, dtype=torch.int32, device=gpu)
-    dst = go.commit_kv(None, acc, branch, pt, ctx, ring, cur, 2, status=status)
+    announce("kv_commit overflow")
+    dst = go.commit_kv(None, acc, branch, pt, ctx, ring, state, 2, status=status)
     assert status.item() == 1
-    assert dst.cpu().tolist() == [[-1, -1]]
+    assert dst.cpu().tolist() == [[-1, -1], [5, 6]]
+    assert ctx.cpu().tolist() == [4, 3]
+    assert pt.cpu().tolist() == [[0, 1], [2, 3]]
+    assert state.cpu().tolist() == [1, 2]
+
+
+@pytest.mark.parametrize("avail", [0, 2, 3, 6])
+def test_kv_commit_ring_exhaustion(gpu, avail):
+    """When the rows want more pages than the ring holds, nothing is allocated:
+    rows that wanted pages commit nothing and keep their context length (status
+    bit 2); rows that fit in their own pages commit. Matches the oracle."""
+    rng = np.random.default_rng(avail)
+    B, k, ps, max_pages, num_pages = 6, 4, 4, 16, 200
+    ctx = np.array([3, 4, 8, 1, 2, 7], dtype=np.int64)
+    acc = np.array([1, 4, 4, 3, 0, 4], dtype=np.int32)  # rows 1, 2, 5 want pages (row 0: 3 + 1 fits)
+    pt = np.full((B, max_pages), -1, dtype=np.int32)
+    for b in range(B):
+        owned = -(-int(ctx[b]) // ps)
+        pt[b, :owned] = 10 * b + np.arange(owned)
+    ring = (100 + rng.permutation(50)).astype(np.int64)
+    branch = (150 * ps + np.arange(B * k, dtype=np.int64)).reshape(B, k)
+    state = (7, 7 + avail)
+    want = og.kv_commit_plan(acc, branch, pt, ctx, ring, state, ps, num_pages)
+    t = {n: torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for n, a in
+         (("acc", acc), ("branch", branch), ("pt", pt), ("ctx", ctx), ("ring", ring))}
+    t_state = torch.tensor(state, dtype=torch.int64, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    announce(f"kv_commit exhaustion avail={avail}")
+    dst = go.commit_kv(None, t["acc"], t["branch"], t["pt"], t["ctx"], t["ring"], t_state, ps, status=status)
+    assert np.array_equal(dst.cpu().numpy(), want[0])
+    assert np.array_equal(t["pt"].cpu().numpy(), want[1])
+    assert np.array_equal(t["ctx"].cpu().numpy(), want[2])
+    assert tuple(t_state.cpu().tolist()) == want[3]
+    assert status.item() == want[4]
+    if avail < 3:  # rows 1, 2 and 5 want one page each
+        assert want[4] == 2 and want[3] == state
+        assert want[2][1] == ctx[1] and want[2][0] == ctx[0] + 1
 
 
 def _pool_ops(seed, cap, pre, steps, batch):

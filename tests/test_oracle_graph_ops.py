@@ -96,7 +96,9 @@ def test_kv_commit_plan_invariants(page_size):
         ring = perm[used:].astype(np.int64)
         cursor = int(rng.integers(0, 3 * len(ring)))
         branch = (np.arange(B * k, dtype=np.int64).reshape(B, k) + 10_000)
-        dst, pt2, cl2, cur2 = og.kv_commit_plan(acc, branch, pt, ctx, ring, cursor, page_size)
+        dst, pt2, cl2, (cur2, end2), status = og.kv_commit_plan(acc, branch, pt, ctx, ring,
+                                                                (cursor, cursor + len(ring)), page_size, num_pages)
+        assert status == 0 and end2 == cursor + len(ring)
         assert (cl2 == ctx + acc).all()
         new_pages = []
         for b in range(B):
@@ -116,6 +118,31 @@ def test_kv_commit_plan_invariants(page_size):
         # No slot is shared between rows (pages are disjoint by construction).
         slots = [s for b in range(B) for s in _walk(pt2[b], int(cl2[b]), page_size)]
         assert len(slots) == len(set(slots))
+
+
+def test_kv_commit_plan_failures_commit_nothing_for_the_row():
+    """Hand-computed cases (page_size 2): a row reaching past its page table, a
+    ring too short for the rows together, a page id outside the pool."""
+    branch = np.array([[50, 51], [52, 53]], dtype=np.int64)
+    # row 0 owns pages 0, 1 (ctx 4) and would need a third entry; row 1 needs one page
+    pt = np.array([[0, 1], [2, -1]], dtype=np.int32)
+    dst, pt2, cl2, state, status = og.kv_commit_plan([2, 2], branch, pt, [4, 1], [7, 8], (0, 2), 2, 20)
+    assert status == 1 and state == (1, 2)
+    assert dst.tolist() == [[-1, -1], [5, 14]]
+    assert pt2.tolist() == [[0, 1], [2, 7]] and cl2.tolist() == [4, 3]
+    # the ring holds one free page, the rows want two: nothing is allocated
+    pt = np.array([[0, -1], [2, -1]], dtype=np.int32)
+    dst, pt2, cl2, state, status = og.kv_commit_plan([2, 2], branch, pt, [2, 2], [7, 8], (5, 6), 2, 20)
+    assert status == 2 and state == (5, 6)
+    assert dst.tolist() == [[-1, -1], [-1, -1]]
+    assert pt2.tolist() == pt.tolist() and cl2.tolist() == [2, 2]
+    # a row fitting its own page still commits when the ring is short
+    dst, pt2, cl2, state, status = og.kv_commit_plan([1, 2], branch, pt, [1, 2], [7, 8], (5, 5), 2, 20)
+    assert status == 2 and dst.tolist() == [[1, -1], [-1, -1]] and cl2.tolist() == [2, 2]
+    # a ring page outside the pool: the row commits nothing, its ring entry is spent
+    dst, pt2, cl2, state, status = og.kv_commit_plan([2, 2], branch, pt, [2, 2], [99, 8], (0, 2), 2, 20)
+    assert status == 1 and state == (2, 2)
+    assert dst.tolist() == [[-1, -1], [16, 17]] and pt2.tolist() == [[0, -1], [2, 8]] and cl2.tolist() == [2, 4]
 
 
 def test_kv_commit_copy_moves_accepted_rows_only():
