@@ -1,24 +1,22 @@
-"""Logical pipeline of LoopSpec: lanes, results, schedule, and the commit loop.
+"""Interface types of LoopSpec's logical pipeline that the decision policies
+take and return (sglang_recurrent/loopspec/pipeline.py:13-207): lanes, lane
+results, the executor protocol and the schedule's endpoint geometry.
 
-Host-side data types the decision policies consume, restated from
-sglang_recurrent/loopspec/pipeline.py (no tensors are handled here). The loop
-``continue_pipelined`` is the reference's acceptance/prune rule
-(pipeline.py:254-423): it commits one token per cycle from the lane reaching
-final depth, keeps the child whose token and originating readout match the
-accepted proposal, and discards every branch that does not descend from it.
-Chained over k sequential draft positions this is exactly the accept-prefix
-rule the fused verify kernels implement.
+The pipeline's commit loop itself (pipeline.py:254-423) is host control flow
+and is not part of this package: its accept-prefix rule over k sequential
+draft positions is what the batched verify entry points compute on the GPU.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Any, Mapping, Protocol, Sequence
+from typing import Any, Protocol, Sequence
 
 
 @dataclass
 class PipelineLane:
-    """One input token moving through repeated core iterations (pipeline.py:13-43)."""
+    """A token in flight: its stage, position, branch ancestry and the q1 / q2
+    proposals (token and distribution) recorded on its way (pipeline.py:13-43)."""
 
     stage: int
     index: int
@@ -35,7 +33,7 @@ class PipelineLane:
 
 @dataclass(frozen=True)
 class PipelineResult:
-    """One lane's result and optional proposal (pipeline.py:46-59)."""
+    """What one forward returns for a lane (pipeline.py:46-59)."""
 
     state: int
     prediction: int
@@ -46,7 +44,7 @@ class PipelineResult:
 
 
 class PipelineExecutor(Protocol):
-    """Model execution boundary used by continue_pipelined (pipeline.py:62-86)."""
+    """The model-side boundary a pipeline drives (pipeline.py:62-86)."""
 
     schedule: "PipelineSchedule"
 
@@ -59,40 +57,45 @@ class PipelineExecutor(Protocol):
 
 @dataclass(frozen=True)
 class PipelineSchedule:
-    """S total iterations, K per cycle, optional q2 after K*X (pipeline.py:132-207)."""
+    """S recurrent iterations per token (`stages`), K per cycle (`step_size`),
+    and an optional second readout after K X iterations (`second_step`);
+    pipeline.py:124-207 defines the same quantities."""
 
     stages: int
     step_size: int
     second_step: int | None = None
 
     def __post_init__(self) -> None:
-        if not isinstance(self.stages, int) or self.stages <= 0:
-            raise ValueError(f"stages S must be a positive integer, got {self.stages}")
-        k = self.step_size
-        if not isinstance(k, int) or not 1 <= k < self.stages or self.stages % k:
-            raise ValueError(f"step_size K must be a positive divisor of S with K < S; got K={k}, S={self.stages}")
-        x = self.second_step
-        if x is not None and (not isinstance(x, int) or not 1 < x < self.depth):
-            raise ValueError(f"second_step X must satisfy 1 < X < S/K so K*X < S; got X={x}, S/K={self.depth}")
+        s, k, x = self.stages, self.step_size, self.second_step
+        if type(s) is not int or s < 1:
+            raise ValueError(f"PipelineSchedule: stages must be an int >= 1 (got {s!r})")
+        if type(k) is not int or not (0 < k < s) or s % k != 0:
+            raise ValueError(f"PipelineSchedule: step_size must divide stages and be below it (got {k!r} for {s})")
+        if x is not None and (type(x) is not int or not (1 < x < s // k)):
+            raise ValueError(f"PipelineSchedule: second_step must lie strictly between 1 and "
+                             f"stages / step_size = {s // k} (got {x!r})")
 
     @property
     def depth(self) -> int:
+        """Cycles a lane needs to reach its final readout."""
         return self.stages // self.step_size
 
     @property
     def proposal_stage(self) -> int:
+        """Last iteration (0-based) before the q1 readout."""
         return self.step_size - 1
 
     @property
     def second_stage(self) -> int | None:
-        return None if self.second_step is None else self.step_size * self.second_step - 1
+        """Last iteration before the q2 readout, if there is one."""
+        return None if self.second_step is None else self.second_step * self.step_size - 1
 
     @property
     def endpoint_kinds(self) -> dict[int, str]:
-        kinds = {self.proposal_stage: "q1"}
-        if self.second_stage is not None:
+        """Readout iteration -> 'q1' / 'q2' / 'final'."""
+        kinds = {self.proposal_stage: "q1", self.stages - 1: "final"}
+        if self.second_step is not None:
             kinds[self.second_stage] = "q2"
-        kinds[self.stages - 1] = "final"
         return kinds
 
     @property
@@ -101,110 +104,16 @@ class PipelineSchedule:
 
     @property
     def row_birth_sizes(self) -> list[int]:
-        """New stage-zero lanes per time step: 1 each, or b_t = b_(t-1) + b_(t-X) with q2."""
-        if self.second_step is None:
-            return [1] * self.depth
-        births = [1] * self.second_step
-        for t in range(self.second_step, self.depth):
-            births.append(births[t - 1] + births[t - self.second_step])
+        """Lanes born at stage zero at each time step 0 .. depth-1 in the full
+        tree: one per step, and with a second readout after X cycles, from step
+        X on, the previous step's births plus those X steps back."""
+        x = self.second_step
+        births: list[int] = []
+        for t in range(self.depth):
+            births.append(1 if x is None or t < x else births[t - 1] + births[t - x])
         return births
 
     @property
     def max_rows(self) -> int:
+        """Bound on the lanes alive at once."""
         return sum(self.row_birth_sizes)
-
-
-def _descends_from(branch: int | None, ancestor: int, parents: Mapping[int, int | None]) -> bool:
-    while branch is not None and branch != ancestor:
-        branch = parents.get(branch)
-    return branch == ancestor
-
-
-def _prune_ancestry(lanes: Sequence[PipelineLane], root: int,
-                    parents: Mapping[int, int | None]) -> dict[int, int | None]:
-    live = {root}
-    for lane in lanes:
-        b = lane.branch
-        while b != root:
-            if b is None or b not in parents:
-                raise RuntimeError("pipeline branch escaped the selected ancestry")
-            live.add(b)
-            b = parents[b]
-    return {b: None if b == root else parents[b] for b in live}
-
-
-def continue_pipelined(first_token: int, max_new_tokens: int, executor: PipelineExecutor) -> list[int]:
-    """Committed completion ids, first token included (pipeline.py:254-423)."""
-    if max_new_tokens <= 0:
-        raise ValueError("a committed first token requires a positive budget")
-    sched = executor.schedule
-    proposal_stages = {sched.proposal_stage, sched.second_stage} - {None}
-    final_stage = sched.stages - 1
-    committed = [first_token]
-    if max_new_tokens == 1:
-        executor.retain_branches(())
-        return committed
-    next_branch = 1
-    parents: dict[int, int | None] = {0: None}
-    lanes = [PipelineLane(stage=0, index=1, token=first_token)]
-    while len(committed) < max_new_tokens:
-        results = list(executor.forward(lanes))
-        if len(results) != len(lanes):
-            raise ValueError("executor must return one result per lane")
-        following: list[PipelineLane] = []
-        children: list[PipelineLane] = []
-        final: tuple[PipelineLane, PipelineResult] | None = None
-        accepted_stage: int | None = None
-        for lane, result in zip(lanes, results):
-            end = lane.stage + sched.step_size - 1
-            if end == final_stage:
-                if final is not None:
-                    raise RuntimeError("multiple branches reached the final stage")
-                final = (lane, result)
-                continue
-            lane.stage = end + 1
-            lane.state = result.state
-            if end in proposal_stages and result.proposed:
-                if end == sched.proposal_stage:
-                    lane.first_token, lane.first_state = result.prediction, result.proposal_state
-                elif result.proposal_action in ("residual", "argmax"):
-                    lane.second_token, lane.second_state = result.prediction, result.proposal_state
-                else:
-                    raise RuntimeError("q2 proposal has no branch action")
-                if lane.index + 1 < max_new_tokens:
-                    children.append(PipelineLane(stage=0, index=lane.index + 1, token=result.prediction,
-                                                 branch=next_branch, parent_branch=lane.branch, origin_stage=end))
-                    parents[next_branch] = lane.branch
-                    next_branch += 1
-            following.append(lane)
-        following.extend(children)
-        if final is not None:
-            lane, result = final
-            if lane.index != len(committed):
-                raise RuntimeError("pipeline attempted to commit out of order")
-            committed.append(result.prediction)
-            if executor.should_stop(committed):
-                executor.retain_branches(())
-                return committed
-            if lane.index + 1 < max_new_tokens:
-                selected = next((c for c in following if c.parent_branch == lane.branch
-                                 and c.token == result.prediction and c.origin_stage == result.accepted_stage), None)
-                if selected is None:
-                    selected = PipelineLane(stage=0, index=lane.index + 1, token=result.prediction,
-                                            branch=next_branch, parent_branch=lane.branch, origin_stage=final_stage)
-                    parents[next_branch] = lane.branch
-                    next_branch += 1
-                    following.append(selected)
-                accepted_stage = result.accepted_stage
-                keep = selected.branch
-                following = [c for c in following if _descends_from(c.branch, keep, parents)]
-                parents = _prune_ancestry(following, keep, parents)
-            else:
-                following = []
-        if len(following) > sched.max_rows:
-            raise RuntimeError("speculative tree exceeded branch row limit")
-        lanes = following
-        executor.retain_branches(tuple(lanes), accepted_stage)
-        if not lanes and len(committed) < max_new_tokens:
-            raise RuntimeError("pipeline drained before generation completed")
-    return committed

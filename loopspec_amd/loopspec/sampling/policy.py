@@ -1,12 +1,22 @@
-"""SamplingDecisionPolicy drop-in: filter, sample, verify and resolve endpoints.
+"""SamplingDecisionPolicy drop-in (interface of
+sglang_recurrent/loopspec/sampling/policy.py:19-308: constructor, queue / read /
+resolve, the [M, 5] decision rows (token, proposed, accepted_code,
+first_rejected, second_rejected) and the generator's draw order).
 
-Same constructor, queue/read/resolve contract, decision packing ([M, 5] int64:
-token, proposed, accepted_code, first_rejected, second_rejected) and RNG order
-as sglang_recurrent/loopspec/sampling/policy.py:19-308, on this package's
-gfx950 sampler. One difference a caller never sees in results: the rejected
-q1 rows of a batch are resolved by one batched rejection launch
-(RejectionSampler.queue_many) instead of one graph replay per row; it draws the
-same two uniforms per row in the same order.
+One cycle is one device buffer and one round trip. Every endpoint's decision
+row is written into `decisions` [max_rows, 5] on the device by the sampler's
+kernels and a few index writes; queue() ends with one copy of the used rows
+to pinned host memory and read() waits once. A verified row's residual
+fallback (after a rejected q1 proposal) runs in the same cycle: the rejection
+kernel takes every verified row and its result is kept where the row was
+rejected, so there is no second round trip.
+
+Draw order, as the reference consumes the generator: q2 residual proposals,
+q1 draws, direct final draws, the verify draws, then two uniforms per rejected
+row in row order. Those last pairs are drawn ahead, one torch.rand(2) per
+verified row: the r-th rejected row takes the r-th pair, the pair the
+reference's r-th fallback draws. read(), knowing the number of rejections,
+sets the generator's offset to where it stands after that many pairs.
 """
 
 from __future__ import annotations
@@ -15,170 +25,166 @@ from dataclasses import dataclass
 
 import torch
 
-from ..decisions import DecisionBatch, DecisionOutcome, DecisionReadback
+from ..decisions import DecisionBatch, DecisionOutcome
 from .distributions import prepare_sampling_probabilities, sample_probabilities
+
+# decision row columns
+TOKEN, PROPOSED, ACCEPTED, FIRST_REJ, SECOND_REJ = range(5)
 
 
 @dataclass
 class SamplingDecisionBatch(DecisionBatch):
     verification_distributions: dict | None = None
+    # verified rows (positions) and the generator offsets of their drawn-ahead pairs
+    verified: tuple = ()
+    pair_offsets: tuple = ()
 
 
 class SamplingDecisionPolicy:
-    """Filter, sample, verify and resolve speculative endpoint logits (policy.py:19-308)."""
+    """Filter, sample, verify and resolve speculative endpoint logits."""
 
     def __init__(self, max_rows, device, options, sampler, *, generator=None):
-        if torch.device(device).type != "cuda":
+        device = torch.device(device)
+        if device.type != "cuda":
             raise RuntimeError("LoopSpec sampling requires CUDA")
-        self.readback = DecisionReadback(max_rows, device)
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.device = device
+        self.max_rows = max_rows
         self.options = options
         self.sampler = sampler
         self.generator = generator
-        self.constants = torch.tensor([0, 1], dtype=torch.int64, device=device)
-        self.proposal_token_host = torch.empty(max_rows, dtype=torch.int64, pin_memory=True)
-        self.proposal_token_device = torch.empty(max_rows, dtype=torch.int64, device=device)
-        self.verification_token_host = torch.empty(max_rows, dtype=torch.int64, pin_memory=True)
-        self.verification_token_device = torch.empty(max_rows, dtype=torch.int64, device=device)
-        self.sample_row_host = torch.empty(max_rows, dtype=torch.int64, pin_memory=True)
-        self.sample_row_device = torch.empty(max_rows, dtype=torch.int64, device=device)
-        self.rejection_host = torch.empty((max_rows, 3), dtype=torch.int64, pin_memory=True)
-        self.rejection_ready = torch.cuda.Event()
+        self.decisions = torch.zeros((max_rows, 5), dtype=torch.int64, device=device)
+        self.decisions_host = torch.empty((max_rows, 5), dtype=torch.int64, pin_memory=True)
+        self.ready = torch.cuda.Event()
+        # the cycle's integers, staged with one copy: 4 index lists and 3 token lists
+        self.ints_host = torch.empty(7 * max_rows, dtype=torch.int64, pin_memory=True)
+        self.ints = torch.empty(7 * max_rows, dtype=torch.int64, device=device)
+        self.pairs = torch.empty((max_rows, 2), dtype=torch.float32, device=device)
+        self.no_second = torch.zeros(sampler.vocabulary_size, dtype=torch.float32, device=device)
         self.top_p_thresholds = torch.full((max_rows, 1), options["top_p"], dtype=torch.float32, device=device)
 
-    @staticmethod
-    def _stage_values(values, host_buffer, device_buffer):
-        count = len(values)
-        host = host_buffer[:count]
-        host.copy_(torch.as_tensor(values, dtype=torch.int64))
-        staged = device_buffer[:count]
-        staged.copy_(host, non_blocking=True)
-        return staged
+    def _generator(self) -> torch.Generator:
+        return self.generator if self.generator is not None else torch.cuda.default_generators[self.device.index]
 
-    def _sample_drafts(self, entries, q1_context, staged_q1_rows):
-        """q2 residual proposals first (slot 0), then q1 draws (slot 2) (policy.py:78-142)."""
-        proposal_states = {}
-        q2_entries = []
-        for row, kind, lane, distribution in entries:
-            if kind == "q1":
-                proposal_states[row] = distribution
-            elif kind == "q2":
-                q2_entries.append((row, lane, distribution))
-        q2_actions = {}
-        draft_samples = {}
-        if q2_entries:
-            q2_targets = torch.stack([d for _, _, d in q2_entries])
-            selected = self._stage_values([lane.first_token for _, lane, _ in q2_entries],
-                                          self.proposal_token_host, self.proposal_token_device)
-            firsts = torch.stack([lane.first_state for _, lane, _ in q2_entries])
-            proposals, actions, sampled = self.sampler.sample_conditional_residual(
-                firsts, q2_targets, selected, self.generator, result_slot=0)
-            for i, (row, _, _) in enumerate(q2_entries):
-                proposal_states[row] = proposals[i]
-                q2_actions[row] = actions[i]
-                draft_samples[row] = sampled[i]
-        q1_entries = [row for row, kind, _, _ in entries if kind == "q1"]
-        if q1_entries:
-            if q1_context is None:
-                distributions = torch.stack([d for _, kind, _, d in entries if kind == "q1"])
-                samples = sample_probabilities(distributions, self.generator, self.sampler, result_slot=2)
-            else:
-                samples = self.sampler.sample_top_p(*q1_context, self.generator, result_slot=2,
-                                                    sample_rows=staged_q1_rows)
-            draft_samples.update({row: samples[i] for i, row in enumerate(q1_entries)})
-        return proposal_states, q2_actions, draft_samples
-
-    def _sample_finals(self, entries):
-        """Direct final draws (slot 1) and q1 verification decisions (policy.py:144-195)."""
-        distributions = {row: d for row, kind, _, d in entries if kind == "final"}
-        direct = [(row, d) for row, kind, lane, d in entries if kind == "final" and lane.first_token is None]
-        direct_samples = {}
-        if direct:
-            sampled = sample_probabilities(torch.stack([d for _, d in direct]), self.generator, self.sampler,
-                                           result_slot=1)
-            direct_samples = {row: sampled[i] for i, (row, _) in enumerate(direct)}
-        verification = [(row, lane, d) for row, kind, lane, d in entries
-                        if kind == "final" and lane.first_token is not None]
-        decisions = {}
-        if verification:
-            target_masses = torch.stack([d[lane.first_token] for _, lane, d in verification])
-            proposal_masses = torch.stack([lane.first_state[lane.first_token] for _, lane, _ in verification])
-            tokens = self._stage_values([lane.first_token for _, lane, _ in verification],
-                                        self.verification_token_host, self.verification_token_device)
-            packed = self.sampler.verify(target_masses, proposal_masses, tokens, self.generator)
-            decisions = {row: packed[i] for i, (row, _, _) in enumerate(verification)}
-        return distributions, direct_samples, decisions
-
-    def _pack(self, entries, q2_actions, drafts, direct, verification):
-        """[M, 5] decisions in endpoint order (policy.py:197-218)."""
-        zero, one = self.constants
-        none = (zero, zero, zero)
-        values = []
-        for row, kind, lane, _ in entries:
-            if kind == "q1":
-                decision = (drafts[row], one, *none)
-            elif kind == "q2":
-                action = q2_actions[row]
-                decision = (torch.where(action > 0, drafts[row], lane.first_token),
-                            (action > 0).to(torch.int64), action, zero, zero)
-            elif lane.first_token is None:
-                decision = (direct[row], zero, *none)
-            else:
-                decision = verification[row]
-            values.extend(decision)
-        return torch.stack(values).reshape(-1, 5)
+    def _stage(self, lists):
+        """One pinned copy of several int lists; returns their device views."""
+        flat = [v for values in lists for v in values]
+        if not flat:
+            return [self.ints[:0] for _ in lists]
+        n = len(flat)
+        self.ints_host[:n].copy_(torch.tensor(flat, dtype=torch.int64))
+        self.ints[:n].copy_(self.ints_host[:n], non_blocking=True)
+        views, at = [], 0
+        for values in lists:
+            views.append(self.ints[at:at + len(values)])
+            at += len(values)
+        return views
 
     def queue(self, post_output, endpoints, lanes):
         logits = post_output.next_token_logits
-        q1_rows = [row for row, kind in enumerate(endpoints.values()) if kind == "q1"]
-        staged_q1_rows = self._stage_values(q1_rows, self.sample_row_host, self.sample_row_device)
+        rows = list(endpoints)
+        kinds = list(endpoints.values())
+        m = len(rows)
+        if m > self.max_rows:
+            raise ValueError(f"{m} endpoint rows exceed max_rows {self.max_rows}")
+        lane_of = [lanes[r] for r in rows]
+        q1 = [i for i, k in enumerate(kinds) if k == "q1"]
+        q2 = [i for i, k in enumerate(kinds) if k == "q2"]
+        direct = [i for i, k in enumerate(kinds) if k == "final" and lane_of[i].first_token is None]
+        verified = [i for i, k in enumerate(kinds) if k == "final" and lane_of[i].first_token is not None]
+        q1_d, q2_d, direct_d, ver_d, q2_tok, ver_tok, ver_meta = self._stage([
+            q1, q2, direct, verified,
+            [lane_of[i].first_token for i in q2],
+            [lane_of[i].first_token for i in verified],
+            [v for i in verified for v in (lane_of[i].second_token or 0, int(lane_of[i].second_state is not None))],
+        ])
         distributions, q1_context = prepare_sampling_probabilities(
             logits, top_p_thresholds=self.top_p_thresholds, sampler=self.sampler, **self.options)
-        entries = [(row, kind, lanes[row], d)
-                   for (row, kind), d in zip(endpoints.items(), distributions, strict=True)]
-        proposal_states, q2_actions, drafts = self._sample_drafts(entries, q1_context, staged_q1_rows)
-        verification_distributions, direct, verification = self._sample_finals(entries)
-        staged = self.readback.stage(self._pack(entries, q2_actions, drafts, direct, verification))
-        return SamplingDecisionBatch(staged, proposal_states=proposal_states,
-                                     verification_distributions=verification_distributions)
+        gen = self.generator
+        dec = self.decisions[:m]
+        dec.zero_()
+        proposal_states = {rows[i]: distributions[i] for i in q1}
+
+        if q2:
+            firsts = torch.stack([lane_of[i].first_state for i in q2])
+            proposals, actions, drawn = self.sampler.sample_conditional_residual(
+                firsts, distributions.index_select(0, q2_d), q2_tok, gen, result_slot=0)
+            took = actions > 0
+            dec[q2_d, TOKEN] = torch.where(took, drawn, q2_tok)
+            dec[q2_d, PROPOSED] = took.to(torch.int64)
+            dec[q2_d, ACCEPTED] = actions.to(torch.int64)
+            proposal_states.update({rows[i]: proposals[j] for j, i in enumerate(q2)})
+
+        if q1:
+            if q1_context is None:
+                drawn = sample_probabilities(distributions.index_select(0, q1_d), gen, self.sampler,
+                                             result_slot=2)
+            else:
+                drawn = self.sampler.sample_top_p(*q1_context, gen, result_slot=2, sample_rows=q1_d)
+            dec[q1_d, TOKEN] = drawn
+            dec[q1_d, PROPOSED] = 1
+
+        if direct:
+            dec[direct_d, TOKEN] = sample_probabilities(distributions.index_select(0, direct_d), gen,
+                                                        self.sampler, result_slot=1)
+
+        pair_offsets = ()
+        if verified:
+            n = len(verified)
+            firsts = torch.stack([lane_of[i].first_state for i in verified]).float()
+            targets = distributions.index_select(0, ver_d)
+            at = torch.arange(n, device=self.device)
+            packed = self.sampler.verify(targets[at, ver_tok], firsts[at, ver_tok], ver_tok, gen)
+            # the fallback pairs, one per verified row, in draw order
+            g = self._generator()
+            offsets = [g.get_offset()]
+            for r in range(n):
+                torch.rand(2, out=self.pairs[r], generator=gen)
+                offsets.append(g.get_offset())
+            pair_offsets = tuple(offsets)
+            rejected = packed[:, 0] < 0
+            rank = torch.cumsum(rejected.to(torch.int64), 0) - rejected.to(torch.int64)
+            seconds = torch.stack([lane_of[i].second_state if lane_of[i].second_state is not None
+                                   else self.no_second for i in verified]).float()
+            fallback = torch.empty((n, 3), dtype=torch.int64, device=self.device)
+            self.sampler.rejections._launch(firsts, targets, seconds, ver_meta.view(n, 2),
+                                            self.pairs[:n].index_select(0, rank), fallback, n)
+            dec[ver_d] = packed
+            dec[ver_d, TOKEN] = torch.where(rejected, fallback[:, 0], packed[:, 0])
+            dec[ver_d, ACCEPTED] = torch.where(rejected, 2 * fallback[:, 1], packed[:, 2])
+            dec[ver_d, SECOND_REJ] = torch.where(rejected, fallback[:, 2], packed[:, 4])
+
+        self.decisions_host[:m].copy_(dec, non_blocking=True)
+        self.ready.record()
+        return SamplingDecisionBatch(
+            (m, 5), proposal_states=proposal_states,
+            verification_distributions={rows[i]: distributions[i] for i, k in enumerate(kinds) if k == "final"},
+            verified=tuple(verified), pair_offsets=pair_offsets)
 
     def read(self, lanes, endpoints, batch):
-        """Host decisions; q1 rejections resolved by the batched fallback (policy.py:255-283)."""
-        values = self.readback.read(batch.staged)
-        decisions = dict(zip(endpoints, values, strict=True))
-        rejected = [(row, d) for row, d in decisions.items() if d[0] < 0]
-        if not rejected:
-            return decisions
-        lanes_r = [lanes[row] for row, _ in rejected]
-        self.sampler.rejections.queue_many(
-            [lane.first_state for lane in lanes_r],
-            [batch.verification_distributions[row] for row, _ in rejected],
-            [lane.second_token for lane in lanes_r],
-            [lane.second_state for lane in lanes_r],
-            self.generator, self.rejection_host)
-        self.rejection_ready.record()
-        self.rejection_ready.synchronize()
-        results = self.rejection_host[: len(rejected)].tolist()
-        for (_, decision), (token, second_accepted, second_rejected) in zip(rejected, results, strict=True):
-            decision[0] = token
-            decision[2] = 2 if second_accepted else 0
-            decision[4] = second_rejected
-        return decisions
+        """The cycle's decisions after one wait; the generator is left where the
+        reference's would be after its fallback draws."""
+        del lanes
+        m, _ = batch.staged
+        self.ready.synchronize()
+        values = self.decisions_host[:m].tolist()
+        if batch.verified:
+            rejections = sum(values[i][FIRST_REJ] for i in batch.verified)
+            self._generator().set_offset(batch.pair_offsets[rejections])
+        return dict(zip(endpoints, values, strict=True))
 
     def resolve(self, lane, endpoint_kind, decision, proposal_state, schedule):
-        prediction, proposed, accepted_code, first_rejected, second_rejected = decision
-        proposed = bool(proposed)
-        if accepted_code == 1:
-            accepted_stage = schedule.proposal_stage
-        elif accepted_code == 2:
-            accepted_stage = schedule.second_stage
-        else:
-            accepted_stage = None
+        """DecisionOutcome of one decision row (policy.py:285-308)."""
+        del lane
+        token, proposed, code = decision[TOKEN], bool(decision[PROPOSED]), decision[ACCEPTED]
+        stage = {1: schedule.proposal_stage, 2: schedule.second_stage}.get(code)
         return DecisionOutcome(
-            prediction=prediction,
+            prediction=token,
             proposed=proposed,
             proposal_state=proposal_state if proposed else None,
-            accepted_stage=accepted_stage,
-            proposal_action="residual" if endpoint_kind == "q2" and proposed else None,
-            first_rejected=bool(first_rejected),
-            second_rejected=bool(second_rejected),
+            accepted_stage=stage,
+            proposal_action="residual" if proposed and endpoint_kind == "q2" else None,
+            first_rejected=bool(decision[FIRST_REJ]),
+            second_rejected=bool(decision[SECOND_REJ]),
         )

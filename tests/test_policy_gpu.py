@@ -122,6 +122,11 @@ def test_sampling_policy_matches_oracle(gpu, seed):
                                                  lane.second_token or 0, has, u0, u1)
             want[r][0], want[r][2], want[r][4] = tok, 2 if sacc else 0, srej
     assert {r: list(d) for r, d in got.items()} == want
+    # After read() the generator stands where the sequential draws leave it.
+    assert gen.get_offset() == rep.get_offset()
+    nxt = torch.empty(3, dtype=torch.float32, device=gpu)
+    torch.rand(3, out=nxt, generator=gen)
+    assert np.array_equal(draw(3), nxt.cpu().numpy())
     assert any(want[r][3] == 1 for r in ver_rows)  # the rejection path ran
     # The q2 proposal state is the normalised residual.
     assert np.array_equal(batch.proposal_states[1].cpu().numpy(), R[0])
