@@ -91,6 +91,22 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride,
                      ls_stream_t stream);
 uint64_t ls_greedy_verify_workspace(int64_t batch, int64_t k, int64_t vocab);
 
+/* Sticky status of a workspace used by ls_argmax_rows / ls_greedy_verify.
+ * Workgroups of a split row publish their keys to the workspace and the last
+ * one to finish polls for them a bounded number of times; a poll that runs out
+ * (a key never became visible) sets bit 0 (LS_GREEDY_KEY_TIMEOUT) in a status
+ * word at byte ls_greedy_status_offset() of the workspace, and the rows of
+ * that launch may be wrong. ls_greedy_workspace_status waits for `stream`,
+ * copies the word to *status and clears it. Callers that keep one round trip
+ * per step can instead copy the word with their results (4 bytes at the
+ * offset) and treat a nonzero value as a failed step.
+ * No reference counterpart: the reference's torch.argmax has no cross-
+ * workgroup handshake that could time out. */
+#define LS_GREEDY_KEY_TIMEOUT 1u
+uint64_t ls_greedy_status_offset(void);
+int ls_greedy_workspace_status(void* workspace, uint64_t workspace_bytes, uint32_t* status,
+                               ls_stream_t stream);
+
 /* Vocabulary head fused with the greedy argmax: out[m] = argmax_n of
  * sum_k hidden[m][k] * weight[n][k] (bf16 inputs, fp32 MFMA accumulation;
  * first index of the maximum, NaN first), without materialising the

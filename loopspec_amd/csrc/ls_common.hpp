@@ -280,6 +280,9 @@ __device__ __forceinline__ uint32_t atomic_arrive(uint32_t* p) {
 __device__ __forceinline__ uint32_t atomic_add_u32(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint32_t atomic_or_u32(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t atomic_exchange_u32(uint32_t* p, uint32_t v) {
   return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

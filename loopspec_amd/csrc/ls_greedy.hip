@@ -30,6 +30,13 @@ constexpr int kUnroll = 8;
 // a call with another shape never overlap them.
 constexpr int kCounterStride = 16;
 constexpr int64_t kMaxGroups = 16384;
+// Workspace: the counter lines, one 256-byte line holding the sticky status
+// word, then the key slots.
+constexpr uint64_t kStatusOffset = static_cast<uint64_t>(kMaxGroups) * kCounterStride * 4u;
+constexpr uint64_t kSlotsOffset = kStatusOffset + 256u;
+// Status bit: some split's key was not visible within the poll limit, so a
+// row's maximum was taken without it.
+constexpr uint32_t kStatusKeyTimeout = 1u;
 constexpr int kMaxSplits = 16;
 constexpr int kMaxRowsPerGroup = 2 * 64 + 1;
 
@@ -52,6 +59,7 @@ struct GreedyParams {
   int64_t* row_argmax;
   uint64_t* slots;           // workspace: one key per (row, split)
   uint32_t* counters;        // workspace: one arrival counter per group, kCounterStride apart
+  uint32_t* status;          // workspace: sticky status bits (kStatusKeyTimeout)
 };
 
 // Row j of group g (verify rows: target positions 0..k, then draft positions
@@ -141,15 +149,17 @@ __device__ __forceinline__ uint64_t thread_argmax_scalar(const char* row, int64_
 // to complete before the arrival: the last arriver polls each slot until its
 // key is visible (every store it waits for was issued before the matching
 // arrival, so the wait ends; the poll count is bounded regardless) and clears
-// it for the next call.
+// it for the next call. A poll that runs out sets kStatusKeyTimeout in the
+// sticky status word, which ls_greedy_workspace_status reports and clears.
 constexpr int kPollLimit = 1 << 22;
 
-__device__ __forceinline__ uint64_t take_key(uint64_t* slot) {
+__device__ __forceinline__ uint64_t take_key(uint64_t* slot, uint32_t* status) {
   uint64_t v = load_sc64(slot);
   for (int n = 0; v == 0 && n < kPollLimit; ++n) {
     __builtin_amdgcn_s_sleep(1);
     v = load_sc64(slot);
   }
+  if (v == 0) atomic_or_u32(status, kStatusKeyTimeout);
   store_sc64(slot, 0);
   return v;
 }
@@ -175,7 +185,7 @@ __device__ void finalize_group(const GreedyParams& p, int64_t g, int own, uint64
     if (t >= kWave) return;
     const int64_t dtok = (k > 0 && !p.draft && lane < k) ? p.draft_tokens[g * k + lane] : -1;
     // this workgroup's own key is taken from registers (its store may still be in flight)
-    const uint64_t key = lane == own ? own_key : (lane < nkeys ? take_key(slots + lane) : 0);
+    const uint64_t key = lane == own ? own_key : (lane < nkeys ? take_key(slots + lane, p.status) : 0);
     uint64_t best = 0;
     for (int s = 0; s < splits; ++s) {
       const uint64_t o = __shfl(key, lane < rpg ? lane * splits + s : 0);
@@ -201,7 +211,7 @@ __device__ void finalize_group(const GreedyParams& p, int64_t g, int own, uint64
   }
   // caller-supplied draft ids go where the draft rows' argmax would be
   if (k > 0 && !p.draft && t < k) ids[k + 1 + t] = p.draft_tokens[g * k + t];
-  for (int i = t; i < nkeys; i += BLOCK) keys[i] = i == own ? own_key : take_key(slots + i);
+  for (int i = t; i < nkeys; i += BLOCK) keys[i] = i == own ? own_key : take_key(slots + i, p.status);
   __syncthreads();
   for (int j = t; j < rpg; j += BLOCK) {
     uint64_t best = 0;
@@ -274,11 +284,18 @@ __global__ __launch_bounds__(BLOCK) void greedy_kernel(GreedyParams p) {
   if (last) finalize_group<BLOCK>(p, g, own, key, ids, keys);
 }
 
-// Workspace: kMaxGroups counter lines, then rows * kMaxSplits key slots.
+// Workspace: kMaxGroups counter lines, the status line, then rows * kMaxSplits
+// key slots.
 uint64_t workspace_bytes(int64_t rows) {
-  const uint64_t counters = static_cast<uint64_t>(kMaxGroups) * kCounterStride * 4u;
   const uint64_t slots = static_cast<uint64_t>(rows) * kMaxSplits * 8u;
-  return (counters + slots + 255u) & ~255ull;
+  return (kSlotsOffset + slots + 255u) & ~255ull;
+}
+
+void bind_workspace(GreedyParams& p, void* workspace) {
+  char* base = static_cast<char*>(workspace);
+  p.counters = reinterpret_cast<uint32_t*>(base);
+  p.status = reinterpret_cast<uint32_t*>(base + kStatusOffset);
+  p.slots = reinterpret_cast<uint64_t*>(base + kSlotsOffset);
 }
 
 struct Shape {
@@ -410,10 +427,7 @@ int ls_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab, i
   p.out = out;
   p.nvec = vocab * eb / 16;
   p.seg = vec ? (p.nvec + p.splits - 1) / p.splits : (vocab + p.splits - 1) / p.splits;
-  if (!p.direct) {
-    p.counters = static_cast<uint32_t*>(workspace);
-    p.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kMaxGroups * kCounterStride * 4);
-  }
+  if (!p.direct) bind_workspace(p, workspace);
   return launch(p, dtype, shape, rows, vec, static_cast<hipStream_t>(stream));
 }
 
@@ -465,9 +479,26 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int
   p.accept_len = accept_len;
   p.tokens = tokens;
   p.row_argmax = row_argmax;
-  p.counters = static_cast<uint32_t*>(workspace);
-  p.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kMaxGroups * kCounterStride * 4);
+  bind_workspace(p, workspace);
   return launch(p, dtype, shape, batch, vec, static_cast<hipStream_t>(stream));
+}
+
+uint64_t ls_greedy_status_offset(void) { return kStatusOffset; }
+
+int ls_greedy_workspace_status(void* workspace, uint64_t ws_bytes, uint32_t* status, ls_stream_t stream) {
+  if (workspace == nullptr || status == nullptr) return fail(LS_ERR_VALUE, "greedy_status: NULL pointer");
+  if (ws_bytes < kSlotsOffset) return fail(LS_ERR_VALUE, "greedy_status: not a greedy workspace");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  uint32_t* word = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kStatusOffset);
+  hipError_t err = hipStreamSynchronize(st);
+  if (err != hipSuccess) return hip_fail(err, "greedy_status: stream");
+  err = hipMemcpy(status, word, sizeof(uint32_t), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_fail(err, "greedy_status: copy");
+  if (*status != 0) {
+    err = hipMemset(word, 0, sizeof(uint32_t));
+    if (err != hipSuccess) return hip_fail(err, "greedy_status: clear");
+  }
+  return LS_OK;
 }
 
 }  // extern "C"

@@ -16,7 +16,7 @@ from typing import Any
 import torch
 
 from .. import _lib
-from ..verify import argmax_rows
+from ..verify import argmax_rows, greedy_status_word
 from .pipeline import PipelineLane, PipelineSchedule
 
 
@@ -70,6 +70,9 @@ class GreedyDecisionPolicy:
         self.readback = DecisionReadback(max_rows, device)
         _lib.load()
         self.choices = torch.empty(max_rows, dtype=torch.int64, device=torch.device(device))
+        # the argmax workspace's status word, read back with the decisions
+        self.status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.status_word: torch.Tensor | None = None
 
     def queue(self, post_output: Any, endpoints: Mapping[int, str], lanes: Sequence[PipelineLane]) -> DecisionBatch:
         del endpoints, lanes
@@ -77,12 +80,21 @@ class GreedyDecisionPolicy:
         rows = logits.shape[0]
         out = self.choices[:rows] if rows <= self.choices.numel() else None
         choices = argmax_rows(logits, out=out)
+        self.status_word = greedy_status_word(_lib.WORKSPACE.get(logits.device, 0, "argmax"))
+        if self.status_word is None:
+            self.status_host.zero_()
+        else:
+            self.status_host.copy_(self.status_word, non_blocking=True)
         return DecisionBatch(self.readback.stage(choices.view(rows, 1)))
 
     def read(self, lanes: Sequence[PipelineLane], endpoints: Mapping[int, str],
              batch: DecisionBatch) -> dict[int, list[int]]:
         del lanes
         decisions = self.readback.read(batch.staged)
+        if int(self.status_host[0]):
+            self.status_word.zero_()
+            raise RuntimeError("greedy argmax: a split key was not visible within the kernel's poll limit; "
+                               "this cycle's decisions are not valid")
         return dict(zip(endpoints, decisions, strict=True))
 
     def resolve(self, lane: PipelineLane, endpoint_kind: str, decision: list[int],

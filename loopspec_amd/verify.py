@@ -8,6 +8,8 @@ which, over k draft positions, is exactly an accept-prefix scan.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -138,6 +140,36 @@ def greedy_verify(
         ws.data_ptr(), ws.numel(), _lib.stream(dev),
     )
     return accept_len, tokens
+
+
+def greedy_status_word(workspace: torch.Tensor) -> torch.Tensor | None:
+    """int32 view of the sticky status word of an argmax / greedy-verify
+    workspace, or None for a workspace too small to hold one (no launch with
+    split rows used it). Bit 0 (LS_GREEDY_KEY_TIMEOUT): a split's key did not
+    become visible within the kernel's poll limit, so rows of the launches since
+    the word was last cleared may be wrong."""
+    off = _lib.query("ls_greedy_status_offset")
+    if workspace.numel() < off + 4:
+        return None
+    return workspace[off:off + 4].view(torch.int32)
+
+
+def check_greedy_status(device: torch.device | str, workspace: torch.Tensor | None = None) -> None:
+    """Wait for the device's stream and raise RuntimeError if the status word
+    of `workspace` (default: the argmax and greedy-verify workspaces cached for
+    the device) is set; the word is cleared."""
+    device = torch.device(device)
+    spaces = [workspace] if workspace is not None else [
+        _lib.WORKSPACE.get(device, 0, tag) for tag in ("argmax", "greedy")]
+    for ws in spaces:
+        if greedy_status_word(ws) is None:
+            continue
+        status = ctypes.c_uint32(0)
+        _lib.call("ls_greedy_workspace_status", ws.data_ptr(), ws.numel(), ctypes.addressof(status),
+                  _lib.stream(device))
+        if status.value:
+            raise RuntimeError(f"greedy argmax: a split key was not visible within the poll limit "
+                               f"(status {status.value:#x}); the results of these launches are not valid")
 
 
 def greedy_verify_workspace_bytes(batch: int, k: int, vocab: int) -> int:

@@ -169,3 +169,19 @@ def test_empty_batch(gpu):
     acc, tok = verify.greedy_verify(target, draft)
     torch.cuda.synchronize()
     assert acc.shape == (0,) and tok.shape == (0, 3)
+
+
+def test_status_word_clear_after_runs_and_reported_when_set(gpu):
+    """The workspace's sticky status stays clear over ordinary launches; a
+    planted bit is reported by check_greedy_status and cleared by it."""
+    target, draft = workloads.greedy_inputs(workloads.C2, 0)
+    verify.greedy_verify(target.to(gpu), draft.to(gpu))
+    verify.check_greedy_status(gpu)
+    ws = _lib.WORKSPACE.get(torch.device(gpu), 0, "greedy")
+    word = verify.greedy_status_word(ws)
+    assert word is not None and int(word.item()) == 0
+    word.fill_(1)
+    with pytest.raises(RuntimeError, match="poll limit"):
+        verify.check_greedy_status(gpu, ws)
+    assert int(word.item()) == 0
+    verify.check_greedy_status(gpu, ws)

@@ -34,6 +34,23 @@ def test_greedy_policy_queue_read(gpu):
     assert batch.staged == (m, 1)
 
 
+def test_greedy_policy_raises_on_key_timeout_status(gpu):
+    """A set status word (the kernel's poll-limit bit, planted from the host)
+    fails the cycle and is cleared; the next cycle reads normally."""
+    m, v = 5, 49152
+    logits = torch.randn(m, v, generator=torch.Generator().manual_seed(4)).to(gpu)
+    endpoints = {r: "q1" for r in range(m)}
+    pol = GreedyDecisionPolicy(8, gpu)
+    out = SimpleNamespace(next_token_logits=logits)
+    pol.read([], endpoints, pol.queue(out, endpoints, []))
+    assert pol.status_word is not None and int(pol.status_word.item()) == 0
+    pol.status_word.fill_(1)
+    with pytest.raises(RuntimeError, match="poll limit"):
+        pol.read([], endpoints, pol.queue(out, endpoints, []))
+    got = pol.read([], endpoints, pol.queue(out, endpoints, []))
+    assert [got[r][0] for r in range(m)] == torch.argmax(logits, dim=1).tolist()
+
+
 def test_greedy_resolve_rules(gpu):
     pol = GreedyDecisionPolicy(4, gpu)
     s = PipelineSchedule(12, 2, 3)
