@@ -6,7 +6,10 @@ NSETS input sets (together larger than the 256 MB Infinity Cache) that are
 already resident in HBM. Steps are submitted through one captured HIP graph of
 NSETS launches replayed K/NSETS times; the timed region is bracketed by HIP
 events on the stream the kernels run on, with device synchronisation on both
-sides. Prints one JSON line.
+sides. Prints one JSON line. The metric names both halves of the path, so the
+default line also carries a "sampling" object: C3 (lossless speculative
+sampling, B=64, k=2, V=49152, fp32, T=1, top_p=0.7) timed the same way in the
+same run, with its own roofline and CPU baseline (--no-sampling leaves it out).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H|SLOTS]
 
@@ -612,6 +615,8 @@ def main() -> int:
     ap.add_argument("--config", default="C2")
     ap.add_argument("--sets", type=int, default=10, help="distinct input sets rotated through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sampling", action="store_true",
+                    help="C2 only: leave out the C3 sampling leg that the default line carries")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="N",
                     help="after timing, run N plain 256 MiB copies (for rocprofv3 --pmc byte scaling)")
     args = ap.parse_args()
@@ -661,9 +666,23 @@ def main() -> int:
                    "C2H": "lm_head_argmax"}.get(args.config)
     if kernel_name:
         result["roofline"]["traffic"] = traffic_from_profile(kernel_name, args.config)
+        result["roofline"]["traffic_source"] = f"profiles/{kernel_name}_{args.config}_traffic.md (rocprofv3 --pmc)"
     if args.copy_calibration:
         copy_calibration(device, args.copy_calibration)
     result.update(_LAST_PERCENTILES)
+    if args.config == "C2" and not args.no_sampling:
+        # the metric's other half: C3 (lossless speculative sampling at the same
+        # V, B and k, fp32) measured in the same run, carried as one more object
+        _log("timing the C3 sampling leg")
+        spec = bench_spec(workloads.C3, args.steps, args.warmup, device, args.sets)
+        spec.update(_LAST_PERCENTILES)
+        spec["roofline"]["traffic"] = traffic_from_profile("spec_verify", "C3")
+        spec["roofline"]["traffic_source"] = "profiles/spec_verify_C3_traffic.md (rocprofv3 --pmc)"
+        if not args.no_cpu_baseline:
+            spec["cpu_baseline"] = cpu_baseline_spec(workloads.C3)
+        result["sampling"] = {key: spec[key] for key in (
+            "value", "unit", "steps", "ms_per_step", "ms_per_step_p10", "ms_per_step_p50", "ms_per_step_p90",
+            "dtype", "config", "tokens_per_s", "acceptance_rate", "roofline", "cpu_baseline") if key in spec}
     if not args.no_cpu_baseline:
         _log("timing CPU baseline")
         if args.config == "C2":
