@@ -9,7 +9,8 @@
 //   * stages its chunk in LDS, decodes it, sets penalised tokens aside;
 //   * computes the chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk
 //     mass M_j in the declared pairwise order; the penalised tokens' own max
-//     and mass (pm_j, PM_j) from a sparse pass over them (x / r or x * r);
+//     and mass (pm_j, PM_j) from a list of them in index order that the
+//     wave's lanes share (x / r or x * r);
 //   * keeps the candidates: every element with RN32(x c - mref) >= -L, mref =
 //     max(mc_j, pmc_j), L from a binary search on the chunk's vector maxima
 //     (at most `cap` vectors reach it), lowered until at most `cap` elements
@@ -232,7 +233,6 @@ __device__ __forceinline__ float lane_tree_sum(float (&a)[N]) {
 template <int DT>
 struct StreamSh {
   u32x4 stage[kNW][kChunk / Elem<DT>::kPerVec];  // the chunk's 16-byte vectors
-  uint32_t pcount[kNW];
 };
 
 
@@ -386,9 +386,43 @@ __device__ __forceinline__ float exp2q_finite(float t) {
 
 // One chunk item, processed by wave w: its candidates and its record are
 // stored (read by fin_kernel, after this kernel). The item is wave-uniform.
+// The chunk's penalised elements (bits hb[u] of lane t's vector u) listed in
+// index order into hl (chunk element indices); returns their number. Element
+// e of vector u of lane t is chunk element (64 u + t) EPV + e, so index order
+// is (u, lane, e): one packed wave scan of the per-vector counts (16-bit
+// fields, four vectors per 64-bit word) places every lane's elements.
+template <int EPV, int NVC>
+__device__ __forceinline__ uint32_t list_hits(const uint32_t (&hb)[NVC], uint16_t* hl) {
+  static_assert(NVC % 4 == 0 || NVC == 4, "vectors per lane");
+  const int t = threadIdx.x & (kWave - 1);
+  uint32_t base = 0;
+#pragma unroll
+  for (int u0 = 0; u0 < NVC; u0 += 4) {
+    uint64_t packed = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) packed |= static_cast<uint64_t>(__builtin_popcount(hb[u0 + q])) << (16 * q);
+    const uint64_t incl = wave_scan_add_u64(packed);
+    const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
+    const uint64_t excl = incl - packed;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t pos = base + static_cast<uint32_t>((excl >> (16 * q)) & 0xffffu);
+      uint32_t bits = hb[u0 + q];
+      while (bits) {
+        const int e = __builtin_ctz(bits);
+        bits &= bits - 1u;
+        hl[pos++] = static_cast<uint16_t>(((u0 + q) * kWave + t) * EPV + e);
+      }
+      base += static_cast<uint32_t>((tot >> (16 * q)) & 0xffffu);
+    }
+  }
+  return base;
+}
+
 template <int DT, bool PEN>
 __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, int w, const Item& I,
-                                            const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4], uint32_t pw) {
+                                            const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4], uint32_t pw,
+                                            uint16_t* hl) {
   constexpr int EPV = Elem<DT>::kPerVec;
   constexpr int NVC = kChunk / (kWave * EPV);
   constexpr int NE = NVC * EPV;
@@ -478,18 +512,21 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   const float c = p.c;
   const float mc = m * c;
 
-  // 5. penalised sub-chunk: max of the penalised logits
+  // 5. penalised sub-chunk: the hits listed in index order, hit h handled by
+  //    lane h mod 64 (its penalised value kept in a register for the first
+  //    64 hits, recomputed for later ones); the max of the penalised logits
   float pm = -__builtin_inff();
+  uint32_t nh = 0;
+  float xp0 = -__builtin_inff();  // the penalised value of hit t
   if constexpr (PEN) {
     if (any_hit) {
+      nh = list_hits<EPV, NVC>(hb, hl);
       float lm = -__builtin_inff();
-#pragma unroll
-      for (int u = 0; u < NVC; ++u) {
-        uint32_t bits = hb[u];
-        while (bits) {
-          const int e = __builtin_ctz(bits);
-          bits &= bits - 1u;
-          const float xp = penalise(staged<DT>(st, (u * kWave + t) * EPV + e), p.pen);
+      for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+        const uint32_t h = h0 + t;
+        if (h < nh) {
+          const float xp = penalise(staged<DT>(st, hl[h]), p.pen);
+          if (h0 == 0) xp0 = xp;
           lm = xp > lm ? xp : lm;
         }
       }
@@ -579,22 +616,16 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
       mask = (mq[0] << 24) | (mq[1] << 16) | (mq[2] << 8) | mq[3];
       cnt = static_cast<uint32_t>(__builtin_popcount(mask));
       uint32_t own = cnt;
+      uint32_t pen_cnt = 0;
       if constexpr (PEN) {
         // the penalised candidates at this level count against the same slots
-        if (any_hit) {
-#pragma unroll
-          for (int u = 0; u < NVC; ++u) {
-            uint32_t bits = hb[u];
-            while (bits) {
-              const int e = __builtin_ctz(bits);
-              bits &= bits - 1u;
-              const float xp = penalise(staged<DT>(st, (u * kWave + t) * EPV + e), p.pen);
-              own += __builtin_fmaf(xp, c, nref) >= th ? 1u : 0u;
-            }
-          }
+        for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+          const uint32_t h = h0 + t;
+          const float xp = h0 == 0 ? xp0 : (h < nh ? penalise(staged<DT>(st, hl[h]), p.pen) : -__builtin_inff());
+          pen_cnt += static_cast<uint32_t>(__builtin_popcountll(__ballot(h < nh && __builtin_fmaf(xp, c, nref) >= th)));
         }
       }
-      const uint32_t tot = lane_bcast_u32(wave_scan_add_u32(own), kWave - 1);
+      const uint32_t tot = lane_bcast_u32(wave_scan_add_u32(own), kWave - 1) + pen_cnt;
       if (tot <= static_cast<uint32_t>(cap)) {
         cnt = tot;
         break;
@@ -649,30 +680,27 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   bool overflow = L < 0 && mref > -__builtin_inff();
   if constexpr (PEN) {
     if (any_hit) {
-      if (t == 0) sh.pcount[w] = 0;
+      // PM_j: hit h added by lane h mod 64 in hit order, then the lanes
+      // pairwise; the penalised candidates appended in hit order
       const float npmc = -pmc;
       const float nref = -mref;
       const float th = -static_cast<float>(L);
       float acc = 0.0f;
-#pragma unroll
-      for (int u = 0; u < NVC; ++u) {
-        uint32_t bits = hb[u];
-        while (bits) {
-          const int e = __builtin_ctz(bits);
-          bits &= bits - 1u;
-          const int li = (u * kWave + t) * EPV + e;
-          const float xp = penalise(staged<DT>(st, li), p.pen);
-          acc = acc + exp2q(__builtin_fmaf(xp, c, npmc));
-          if (L >= 0 && __builtin_fmaf(xp, c, nref) >= th) {
-            const uint32_t q = __hip_atomic_fetch_add(&sh.pcount[w], 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (nA + q < static_cast<uint32_t>(cap))
-              out[nA + q] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp);
-          }
-        }
+      uint32_t nB = 0;
+      for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+        const uint32_t h = h0 + t;
+        const bool in = h < nh;
+        const uint32_t li = in ? hl[h] : 0u;
+        const float xp = h0 == 0 ? xp0 : (in ? penalise(staged<DT>(st, li), p.pen) : -__builtin_inff());
+        if (in) acc = acc + exp2q(__builtin_fmaf(xp, c, npmc));
+        const bool cand = in && L >= 0 && __builtin_fmaf(xp, c, nref) >= th;
+        const uint64_t m = __ballot(cand);
+        const uint32_t q = nB + static_cast<uint32_t>(__builtin_popcountll(m & ((1ull << t) - 1ull)));
+        if (cand && nA + q < static_cast<uint32_t>(cap))
+          out[nA + q] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp);
+        nB += static_cast<uint32_t>(__builtin_popcountll(m));
       }
       pmass = wave_tree_sum(acc);
-      const uint32_t nB = __hip_atomic_load(&sh.pcount[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (nA + nB > static_cast<uint32_t>(cap)) overflow = true;
       nA += nB;
     }
@@ -710,6 +738,7 @@ template <int DT, bool PEN>
 __global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
   constexpr int NVC = kChunk / (kWave * Elem<DT>::kPerVec);
   __shared__ StreamSh<DT> sh;
+  __shared__ uint16_t hits[PEN ? kNW : 1][PEN ? kChunk : 1];  // each wave's penalised elements
   // the wave's item, wave-uniform (its decomposition runs on the scalar unit)
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int it = static_cast<int>(blockIdx.x) * kNW + w;
@@ -718,7 +747,7 @@ __global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
   u32x4 d[NVC];
   uint32_t pw;
   load_item<DT, NVC>(p, I, d, pw);
-  stream_item<DT, PEN>(p, sh, w, I, d, pw);
+  stream_item<DT, PEN>(p, sh, w, I, d, pw, hits[PEN ? w : 0]);
 }
 
 // ===========================================================================

@@ -29,9 +29,10 @@
  *   tree_j: lane t of 64 owns the 16-byte vectors u*64 + t of the chunk
  *   (epv elements each, epv = 4 for 4-byte logits and 8 for 2-byte ones);
  *   each lane sums its 32 values pairwise in (u, element) order, then the
- *   64 lane sums are summed pairwise in lane order. seq_j: each lane adds
- *   its B_j values one by one in (u, element) order starting from 0, then
- *   the lane sums pairwise as in tree_j.
+ *   64 lane sums are summed pairwise in lane order. seq_j: the B_j values in
+ *   index order, value h to lane h mod 64; each lane adds its values one by
+ *   one in that order starting from 0, then the lane sums pairwise as in
+ *   tree_j.
  *     mcmax = max over j of mc_j and pmc_j
  *     slot[2j] = RN(exp2m(RN(mc_j - mcmax)) * M_j),
  *     slot[2j+1] = RN(exp2m(RN(pmc_j - mcmax)) * PM_j), slots >= 2 nch = 0
@@ -143,23 +144,25 @@ int ls_o_row_softmax(const float* x, const uint8_t* pen, int64_t v, double cd, i
     float lane_a[LANES], lane_b[LANES];
     for (int t = 0; t < LANES; ++t) {
       float a[32];
-      float acc = 0.0f;
       for (int u = 0; u < nvc; ++u) {
         for (int e = 0; e < epv; ++e) {
           const int64_t g = c0 + (int64_t)(u * LANES + t) * epv + e;
           float ev = 0.0f;
-          if (g < v) {
-            if (pen && pen[g]) {
-              acc = acc + ls_o_exp2m(fmaf(x[g], c, -pmc));
-            } else {
-              ev = ls_o_exp2m(fmaf(x[g], c, -mc));
-            }
-          }
+          if (g < v && !(pen && pen[g])) ev = ls_o_exp2m(fmaf(x[g], c, -mc));
           a[u * epv + e] = ev;
         }
       }
       lane_a[t] = tree_sum(a, nvc * epv);
-      lane_b[t] = acc;
+      lane_b[t] = 0.0f;
+    }
+    if (pen) {
+      int h = 0;  /* penalised values in index order, value h to lane h mod 64 */
+      for (int i = 0; i < CHUNK && c0 + i < v; ++i) {
+        if (pen[c0 + i]) {
+          lane_b[h % LANES] = lane_b[h % LANES] + ls_o_exp2m(fmaf(x[c0 + i], c, -pmc));
+          ++h;
+        }
+      }
     }
     st[j].m = m;
     st[j].pm = pm;

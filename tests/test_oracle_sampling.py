@@ -171,8 +171,9 @@ def test_penalty_bit_equal_to_reference_formulation():
 
 
 def test_penalised_subchunk_mass_order():
-    """PM_j: each lane adds its penalised e' (relative to the penalised max)
-    one by one in (vector, element) order, then the lanes pairwise."""
+    """PM_j: the penalised e' (relative to the penalised max) in index order,
+    value h to lane h mod 64, each lane adding its values one by one, then
+    the lanes pairwise (the same for either element width)."""
     rng = np.random.default_rng(13)
     for epv in (4, 8):
         x = (rng.standard_normal(2048) * 3).astype(np.float32)
@@ -183,17 +184,12 @@ def test_penalised_subchunk_mass_order():
         pm = np.max(pr.x[pen])
         pmc = np.float32(pm * pr.c)
         ep = nm.exp2m(nm.fma32(pr.x, pr.c, -pmc))
-        nvc = 2048 // (64 * epv)
         lanes = np.zeros(64, np.float32)
-        for t in range(64):
-            acc = np.float32(0)
-            for u in range(nvc):
-                for e in range(epv):
-                    i = (u * 64 + t) * epv + e
-                    if pen[i]:
-                        acc = np.float32(acc + ep[i])
-            lanes[t] = acc
+        for h, i in enumerate(np.flatnonzero(pen)):
+            lanes[h % 64] = np.float32(lanes[h % 64] + ep[i])
         assert soft.pmass_chunks[0] == nm.tree_sum_f32(lanes), epv
+        # more than 64 penalised values: lanes take several, in order
+        assert np.count_nonzero(pen) > 64
         assert soft.pm_chunks[0] == pm and soft.m_chunks[0] == np.max(pr.x[~pen])
         # the penalised tokens' p is a function of their processed logit too
         assert np.array_equal(soft.p, os_.p_of(soft, pr.x))
