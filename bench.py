@@ -11,12 +11,13 @@ default line also carries a "sampling" object: C3 (lossless speculative
 sampling, B=64, k=2, V=49152, fp32, T=1, top_p=0.7) timed the same way in the
 same run, with its own roofline and CPU baseline (--no-sampling leaves it out).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H|SLOTS]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4|C5|C2H|SLOTS|READ]
 
 C2H is the vocabulary head fused with the greedy argmax (hidden states of C2's
 320 endpoint rows, Ouro-1.4B head: H=2048, V=49152, bf16 weight). SLOTS is the
 GPU-resident decode-slot pool at C5's shape: per step, the 384 slots of the
-previous step are released and 384 rows allocate.
+previous step are released and 384 rows allocate. READ times the greedy
+kernel's reads alone on C2's input sets (the measured floor under C2).
 """
 
 from __future__ import annotations
@@ -104,6 +105,40 @@ def bench_greedy(steps: int, warmup: int, device: torch.device, nsets: int) -> d
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
         },
+    }
+
+
+def bench_read_ceiling(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
+    """READ: the greedy kernel's reads alone (ls_stream_read_probe) on C2's
+    input sets, one launch per step timed like C2: the floor under C2's
+    kernel time for this access pattern."""
+    from loopspec_amd import verify, workloads
+
+    cfg = workloads.C2
+    _log(f"generating {nsets} input sets for {cfg.name} (read ceiling)")
+    sets = [workloads.greedy_inputs(cfg, seed=1000 + i, device=device) for i in range(nsets)]
+    outs = [verify.stream_read_probe(t, d) for t, d in sets]
+
+    def step(i: int) -> None:
+        t, d = sets[i]
+        verify.stream_read_probe(t, d, out=outs[i])
+
+    ms_per_step, timed_steps, wsteps = _time_graph(step, nsets, steps, warmup)
+    nbytes = cfg.batch * (2 * cfg.k + 1) * cfg.vocab * 2
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": "streaming read of C2's logits (greedy kernel's grid and loads, no reduction or epilogue)",
+        "value": achieved,
+        "unit": "GB/s",
+        "steps": timed_steps,
+        "warmup": wsteps,
+        "ms_per_step": ms_per_step,
+        "dtype": "bf16",
+        "config": {"workload": "READ-" + cfg.name, "batch": cfg.batch, "k": cfg.k, "vocab": cfg.vocab,
+                   "input_sets": nsets, "input_set_bytes": nbytes, "kernel": "ls::read_probe_kernel<256,6>",
+                   "submission": "hipGraph of one launch per step"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
     }
 
 
@@ -644,6 +679,9 @@ def main() -> int:
         args.no_cpu_baseline = True
     elif args.config == "C2H":
         result = bench_lm_head(args.steps, args.warmup, device, args.sets)
+    elif args.config == "READ":
+        result = bench_read_ceiling(args.steps, args.warmup, device, args.sets)
+        args.no_cpu_baseline = True
     elif args.config == "SLOTS":
         result = bench_slots(args.steps, args.warmup, device, args.sets)
     else:
@@ -657,6 +695,7 @@ def main() -> int:
         "C5": "synthetic (C3 logits at B=128, drafts sampled from q; random bf16 KV pool, context U(512,8192))",
         "C2H": "synthetic (seeded N(0,1) bf16 hidden states, two N(0,1/H) bf16 head weights alternated)",
         "SLOTS": "synthetic (every row valid; all 384 slots of the previous step released)",
+        "READ": "synthetic (the C2 input sets)",
     }[args.config]
     result.update({"n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": data})
     # Traffic summaries are per launch unit: the greedy kernel (C2), or the

@@ -107,6 +107,22 @@ uint64_t ls_greedy_status_offset(void);
 int ls_greedy_workspace_status(void* workspace, uint64_t workspace_bytes, uint32_t* status,
                                ls_stream_t stream);
 
+/* Read-ceiling calibration for ls_greedy_verify: reads the same target and
+ * draft rows with the greedy kernel's grid, workgroup shape and loads (every
+ * lane's non-temporal 16-byte loads issued at once) and keeps only an
+ * exclusive-or of the words, one 32-bit word per wave in out (out_words >=
+ * ls_stream_read_probe_words(batch, k)). Its duration is the floor for any
+ * kernel that reads those bytes in that pattern; bench.py --config READ times
+ * it on the C2 input sets. Needs aligned rows whose segments are whole
+ * multiples of 256 vectors (as C2's are); LS_ERR_VALUE otherwise.
+ * No reference counterpart: a measurement kernel of this build. */
+uint64_t ls_stream_read_probe_words(int64_t batch, int64_t k);
+int ls_stream_read_probe(const void* target_logits, int64_t target_batch_stride,
+                         int64_t target_pos_stride, const void* draft_logits,
+                         int64_t draft_batch_stride, int64_t draft_pos_stride, int dtype,
+                         int64_t batch, int64_t k, int64_t vocab, uint32_t* out,
+                         uint64_t out_words, ls_stream_t stream);
+
 /* Vocabulary head fused with the greedy argmax: out[m] = argmax_n of
  * sum_k hidden[m][k] * weight[n][k] (bf16 inputs, fp32 MFMA accumulation;
  * first index of the maximum, NaN first), without materialising the

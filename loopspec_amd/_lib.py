@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ls_greedy_verify_workspace": (_U64, [_I64, _I64, _I64]),
     "ls_greedy_status_offset": (_U64, []),
+    "ls_stream_read_probe_words": (_U64, [_I64, _I64]),
+    "ls_stream_read_probe": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _U64, _P]),
     "ls_greedy_workspace_status": (_I32, [_P, _U64, _P, _P]),
     "ls_lm_head_argmax": (_I32, [_P, _I64, _P, _I64, _I32, _I64, _I64, _I64, _P, _P, _U64, _P]),
     "ls_lm_head_argmax_workspace": (_U64, [_I64, _I64]),

@@ -164,8 +164,59 @@ __device__ __forceinline__ uint64_t take_key(uint64_t* slot, uint32_t* status) {
   return v;
 }
 
+// Wave 0 of the last workgroup of group g when the group has at most 64
+// keys: lane i holds key i (this workgroup's own from registers, the others
+// from `pre` when already loaded, else polled for). Row j's key is the maximum over its splits' keys; the accept-prefix
+// scan is lane-parallel (lane i compares draft position i, one ballot finds
+// the first mismatch, lane i writes output position i).
+__device__ __forceinline__ void finalize_small(const GreedyParams& p, int64_t g, int own, uint64_t own_key,
+                                               uint64_t pre) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int k = p.k;
+  const int rpg = p.rows_per_group, splits = p.splits;
+  const int nkeys = rpg * splits;
+  uint64_t* slots = p.slots + g * nkeys;
+  const int64_t dtok = (k > 0 && !p.draft && lane < k) ? p.draft_tokens[g * k + lane] : -1;
+  uint64_t key = 0;
+  if (lane == own) {
+    key = own_key;
+  } else if (lane < nkeys) {
+    // take_key polls until the key is visible and clears the slot; a key
+    // already loaded is visible, so clearing it now comes after its store
+    if (pre != 0) {
+      key = pre;
+      store_sc64(slots + lane, 0);
+    } else {
+      key = take_key(slots + lane, p.status);
+    }
+  }
+  // this workgroup's slot is cleared by the lane that stored it (program order)
+  if (lane == 0) store_sc64(slots + own, 0);
+  uint64_t best = 0;
+  for (int s = 0; s < splits; ++s) {
+    const uint64_t o = __shfl(key, lane < rpg ? lane * splits + s : 0);
+    best = o > best ? o : best;
+  }
+  const int64_t id = lane < rpg ? static_cast<int64_t>(argmax_key_index(best)) : -1;
+  if (lane == 0) store_sc(p.counters + g * kCounterStride, 0u);
+  if (k == 0) {
+    if (lane == 0) p.out[g] = id;
+    return;
+  }
+  // draft id of position lane: the draft row's argmax or the caller's id
+  const int64_t d = p.draft ? __shfl(id, lane < k ? k + 1 + lane : 0) : dtok;
+  const uint64_t bad = __ballot(lane < k && d != id);
+  const int a = bad ? __builtin_ctzll(bad) : k;
+  if (lane <= k) p.tokens[g * (k + 1) + lane] = lane <= a ? id : -1;
+  if (p.row_argmax) {
+    if (lane <= k) p.row_argmax[g * (2 * k + 1) + lane] = id;
+    if (lane < k) p.row_argmax[g * (2 * k + 1) + k + 1 + lane] = d;
+  }
+  if (lane == 0) p.accept_len[g] = a;
+}
+
 // Runs on every lane of the last workgroup of group g (a block-uniform
-// branch). Row j's key is the maximum over its splits' keys. The
+// branch), when the group has more than 64 keys. Row j's key is the maximum over its splits' keys. The
 // accept-prefix scan is lane-parallel: lane i compares draft position i, the
 // first mismatch comes from one ballot, and lane i writes output position i,
 // so no store waits on another. When the group has at most 64 keys, wave 0
@@ -275,13 +326,66 @@ __global__ __launch_bounds__(BLOCK) void greedy_kernel(GreedyParams p) {
     return;
   }
   const int own = j * p.splits + split;
+  const int nkeys = p.rows_per_group * p.splits;
+  if (nkeys <= kWave) {
+    // Wave 0 alone (the other waves are done): thread 0 publishes the key and
+    // arrives; the last arriver takes the other keys. (Loading them in every
+    // workgroup alongside the arrival, to save the last one a round trip,
+    // measured slower: 20 workgroups then read the lines others store to.)
+    if (threadIdx.x >= kWave) return;
+    uint32_t prev = 0;
+    if (threadIdx.x == 0) {
+      store_sc64(p.slots + g * nkeys + own, key);
+      prev = atomic_arrive(p.counters + g * kCounterStride);
+    }
+    prev = lane_bcast_u32(prev, 0);
+    if (prev != static_cast<uint32_t>(nkeys - 1)) return;
+    finalize_small(p, g, own, key, 0);
+    return;
+  }
   if (threadIdx.x == 0) {
-    store_sc64(p.slots + g * p.rows_per_group * p.splits + own, key);
+    store_sc64(p.slots + g * nkeys + own, key);
     const uint32_t prev = atomic_arrive(p.counters + g * kCounterStride);
-    last = prev == static_cast<uint32_t>(p.rows_per_group * p.splits - 1);
+    last = prev == static_cast<uint32_t>(nkeys - 1);
   }
   __syncthreads();
   if (last) finalize_group<BLOCK>(p, g, own, key, ids, keys);
+}
+
+// Read-ceiling calibration: greedy_kernel's grid, row addressing and loads
+// (every lane issues its J non-temporal 16-byte loads at once), with only an
+// exclusive-or of the loaded words kept, one word per wave. It bounds from
+// below what any kernel reading the same rows in the same pattern can take.
+template <int BLOCK, int J>
+__global__ __launch_bounds__(BLOCK) void read_probe_kernel(GreedyParams p, uint32_t* out) {
+  int64_t tbs = p.t_bstride, tps = p.t_pstride, dbs = p.d_bstride, dps = p.d_pstride;
+  int kk = p.k;
+  asm volatile("" : "+s"(tbs), "+s"(tps), "+s"(dbs), "+s"(dps), "+s"(kk));
+  const int split = static_cast<int>(blockIdx.x);
+  const int j = static_cast<int>(blockIdx.y);
+  const int64_t g = static_cast<int64_t>(blockIdx.z);
+  const bool is_t = j <= kk;
+  const char* row = (is_t ? p.target : p.draft) + g * (is_t ? tbs : dbs) +
+                    static_cast<int64_t>(is_t ? j : j - kk - 1) * (is_t ? tps : dps);
+  const int64_t v0 = split * p.seg;
+  const int64_t v1 = v0 + p.seg < p.nvec ? v0 + p.seg : p.nvec;
+  const int64_t first = v0 + threadIdx.x;
+  uint32_t acc = 0;
+  if (first < v1) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(row) + first;
+    u32x4 d[J];
+#pragma unroll
+    for (int u = 0; u < J; ++u) d[u] = __builtin_nontemporal_load(src + static_cast<int64_t>(u) * BLOCK);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < J; ++u) acc ^= d[u][0] ^ d[u][1] ^ d[u][2] ^ d[u][3];
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) acc ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), m));
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    const int64_t wg = (g * p.rows_per_group + j) * p.splits + split;
+    out[wg * (BLOCK / kWave) + threadIdx.x / kWave] = acc;
+  }
 }
 
 // Workspace: kMaxGroups counter lines, the status line, then rows * kMaxSplits
@@ -481,6 +585,57 @@ int ls_greedy_verify(const void* target_logits, int64_t target_batch_stride, int
   p.row_argmax = row_argmax;
   bind_workspace(p, workspace);
   return launch(p, dtype, shape, batch, vec, static_cast<hipStream_t>(stream));
+}
+
+uint64_t ls_stream_read_probe_words(int64_t batch, int64_t k) {
+  if (batch <= 0 || k < 1) return 0;
+  return static_cast<uint64_t>(batch * (2 * k + 1)) * kMaxSplits * 4u;
+}
+
+int ls_stream_read_probe(const void* target_logits, int64_t target_batch_stride, int64_t target_pos_stride,
+                         const void* draft_logits, int64_t draft_batch_stride, int64_t draft_pos_stride, int dtype,
+                         int64_t batch, int64_t k, int64_t vocab, uint32_t* out, uint64_t out_words,
+                         ls_stream_t stream) {
+  const int eb = dtype_bytes(dtype);
+  if (eb == 0) return fail(LS_ERR_VALUE, "unsupported logits dtype");
+  if (batch <= 0 || batch > kMaxGroups || k < 1 || k > 64 || vocab <= 0 || vocab > 0x7fffffffLL)
+    return fail(LS_ERR_VALUE, "stream_read_probe: need 0 < batch <= 16384, 1 <= k <= 64, 0 < vocab < 2^31");
+  if (!target_logits || !draft_logits || !out) return fail(LS_ERR_VALUE, "stream_read_probe: NULL pointer");
+  if (out_words < ls_stream_read_probe_words(batch, k))
+    return fail(LS_ERR_VALUE, "stream_read_probe: output too small");
+  GreedyParams p{};
+  p.target = static_cast<const char*>(target_logits);
+  p.t_bstride = target_batch_stride * eb;
+  p.t_pstride = target_pos_stride * eb;
+  p.draft = static_cast<const char*>(draft_logits);
+  p.d_bstride = draft_batch_stride * eb;
+  p.d_pstride = draft_pos_stride * eb;
+  p.k = static_cast<int>(k);
+  p.rows_per_group = static_cast<int>(2 * k + 1);
+  const bool vec = aligned16(target_logits) && aligned16(draft_logits) && (p.t_bstride % 16 == 0) &&
+                   (p.t_pstride % 16 == 0) && (p.d_bstride % 16 == 0) && (p.d_pstride % 16 == 0) &&
+                   ((vocab * eb) % 16 == 0);
+  const Shape shape = choose_shape(batch * p.rows_per_group, vocab, eb, p.rows_per_group);
+  if (!vec || shape.block != 256 || shape.j == 0)
+    return fail(LS_ERR_VALUE, "stream_read_probe: needs the greedy kernel's exact vector shape (aligned rows, "
+                              "segments of 256..2048 vectors)");
+  p.splits = shape.splits;
+  p.nvec = vocab * eb / 16;
+  p.seg = p.nvec / p.splits;
+  const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(p.rows_per_group),
+                  static_cast<unsigned>(batch));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (shape.j) {
+    case 1: hipLaunchKernelGGL((read_probe_kernel<256, 1>), grid, dim3(256), 0, st, p, out); break;
+    case 2: hipLaunchKernelGGL((read_probe_kernel<256, 2>), grid, dim3(256), 0, st, p, out); break;
+    case 3: hipLaunchKernelGGL((read_probe_kernel<256, 3>), grid, dim3(256), 0, st, p, out); break;
+    case 4: hipLaunchKernelGGL((read_probe_kernel<256, 4>), grid, dim3(256), 0, st, p, out); break;
+    case 5: hipLaunchKernelGGL((read_probe_kernel<256, 5>), grid, dim3(256), 0, st, p, out); break;
+    case 6: hipLaunchKernelGGL((read_probe_kernel<256, 6>), grid, dim3(256), 0, st, p, out); break;
+    case 7: hipLaunchKernelGGL((read_probe_kernel<256, 7>), grid, dim3(256), 0, st, p, out); break;
+    default: hipLaunchKernelGGL((read_probe_kernel<256, 8>), grid, dim3(256), 0, st, p, out); break;
+  }
+  return check_launch("stream read probe launch");
 }
 
 uint64_t ls_greedy_status_offset(void) { return kStatusOffset; }

@@ -247,6 +247,29 @@ def speculative_verify(
     return accept_len, tokens
 
 
+def stream_read_probe(target_logits: torch.Tensor, draft_logits: torch.Tensor, out: torch.Tensor | None = None
+                      ) -> torch.Tensor:
+    """Read-ceiling calibration (ls_stream_read_probe): reads greedy_verify's
+    rows with its kernel's grid and loads and keeps only an exclusive-or of
+    the words (int32, one per wave). Its duration bounds greedy_verify's from
+    below."""
+    _check_rows(target_logits, "stream_read_probe")
+    _check_rows(draft_logits, "stream_read_probe")
+    batch, kp1, vocab = target_logits.shape
+    k = kp1 - 1
+    words = _lib.query("ls_stream_read_probe_words", batch, k)
+    if out is None:
+        out = torch.zeros(words, dtype=torch.int32, device=target_logits.device)  # words past the grid stay 0
+    _lib.call(
+        "ls_stream_read_probe",
+        target_logits.data_ptr(), target_logits.stride(0), target_logits.stride(1),
+        draft_logits.data_ptr(), draft_logits.stride(0), draft_logits.stride(1),
+        _lib.dtype_code(target_logits), batch, k, vocab, out.data_ptr(), out.numel(),
+        _lib.stream(target_logits.device),
+    )
+    return out
+
+
 def spec_verify_workspace_bytes(batch: int, k: int, vocab: int) -> int:
     return _lib.query("ls_spec_verify_workspace", batch, k, vocab)
 

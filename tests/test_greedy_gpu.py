@@ -185,3 +185,17 @@ def test_status_word_clear_after_runs_and_reported_when_set(gpu):
         verify.check_greedy_status(gpu, ws)
     assert int(word.item()) == 0
     verify.check_greedy_status(gpu, ws)
+
+
+def test_stream_read_probe_reads_every_word_once(gpu):
+    """The read-ceiling kernel's outputs combine to the exclusive-or of every
+    word of the target and draft rows (each word is read exactly once)."""
+    cfg = workloads.GreedyConfig("probe", 64, 2, 49152, torch.bfloat16)
+    target, draft = workloads.greedy_inputs(cfg, seed=4, device=gpu)
+    announce("stream_read_probe C2 shape")
+    out = verify.stream_read_probe(target, draft)
+    torch.cuda.synchronize()
+    got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+    words = np.concatenate([target.contiguous().view(torch.int32).cpu().numpy().ravel(),
+                            draft.contiguous().view(torch.int32).cpu().numpy().ravel()]).view(np.uint32)
+    assert got == np.bitwise_xor.reduce(words)
