@@ -880,14 +880,14 @@ __device__ __forceinline__ uint32_t hash_find(const FinSh& f, uint32_t x) {
   return kNone;
 }
 
-// Rebuilds the hash after slot 1's entries changed; entries a refill dropped
-// (p bits 0) stay out, so an index is found at its live entry.
-__device__ __forceinline__ void hash_rebuild(FinSh& f) {
-  for (int i = threadIdx.x; i < kHash; i += kFW) f.hash[i] = 0u;
-  __syncthreads();
+// Builds the hash over slot 1's support entries (p >= its cutoff): the only
+// ones whose filtered probability is not zero. The hash is zero on entry.
+__device__ __forceinline__ void hash_support(FinSh& f) {
   const uint32_t n = f.aux[1].n;
+  const float cut = f.aux[1].cut;
   for (uint32_t e = threadIdx.x; e < n; e += kFW) {
-    if (f.ent[1].pbits[e] != 0u) hash_insert(f, f.ent[1].eidx[e], e);
+    const uint32_t pb = f.ent[1].pbits[e];
+    if (pb != 0u && __uint_as_float(pb) >= cut) hash_insert(f, f.ent[1].eidx[e], e);
   }
   __syncthreads();
 }
@@ -1411,7 +1411,6 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
   bool ok[2] = {false, false};
   if (mask) select_entries(f, mask, thr, cut, mass, ok, true);
   uint32_t flags[2] = {f.aux[0].flags & kRowEmpty, f.aux[1].flags & kRowEmpty};
-  bool changed1 = false;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (!((mask >> s) & 1u)) continue;  // unfiltered: P = p over the whole row
@@ -1431,13 +1430,11 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
         cut[s] = c1[s];
         mass[s] = m1[s];
       }
-      if (s == 1) changed1 = true;
     }
     if (!ok[s]) {
       flags[s] = kRowFiltered | kRowSlow;
       select_row<DT>(p, f, rows[s], K[s], thr[s], &cut[s], &mass[s]);
       if (collect_support<DT>(p, f, s, rows[s], K[s], cut[s])) flags[s] |= kRowList;
-      if (s == 1) changed1 = true;
     }
   }
   if (threadIdx.x == 0) {
@@ -1458,7 +1455,6 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
     }
   }
   __syncthreads();
-  if (nr == 2 && changed1 && (f.aux[1].flags & kRowList)) hash_rebuild(f);
 }
 
 // Filtered probability of a row at p (P = p when unfiltered).
@@ -1808,7 +1804,7 @@ void fin_kernel(const Params p) {
   if (nr == 2) place_slots(p, f, 1, sl[1]);
   __syncthreads();
   entry_p(p, f, 0, false);
-  if (nr == 2) entry_p(p, f, 1, true);
+  if (nr == 2) entry_p(p, f, 1, false);
   __syncthreads();
   RowK K[2];
   for (int s = 0; s < 2; ++s) K[s] = RowK{f.aux[s < nr ? s : 0].mcmax, f.aux[s < nr ? s : 0].s, p.cd};
@@ -1826,6 +1822,8 @@ void fin_kernel(const Params p) {
       const float P = a0.has_tok ? filtered_of(a0, pval(K[0], a0.xtok)) : 0.0f;
       const float Q = a1.has_tok ? filtered_of(a1, pval(K[1], a1.xtok)) : 0.0f;
       acc = accept_draw(u_acc, P, Q);
+      // the draft's support by vocabulary index, for the residual's Q lookups
+      if (!acc && (a1.flags & kRowList)) hash_support(f);
       token = acc ? xdraft : draw_residual<DT>(p, f, rows[0], rows[1], K[0], K[1], u_draw);
     }
     // publish, then the last of the batch element's k+1 units writes the outputs
