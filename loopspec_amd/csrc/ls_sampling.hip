@@ -58,7 +58,6 @@ constexpr int kBins = 1 << kRadixBits;     // radix digits per round
 constexpr int kMaxLevel = 31;              // candidate levels: e >= 2^-L, L in [0, 31]
 constexpr int64_t kMaxRows = 65536;
 constexpr int64_t kMaxSpecBatch = 16384;
-constexpr int64_t kMaxK = 64;
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum Mode : int { kModeSpec = 0, kModeSample = 1, kModeDense = 2 };
@@ -767,6 +766,7 @@ struct RowAux {
   uint64_t mass_fx;
   float bmax;                    // largest non-candidate bound
   float xtok;
+  float ptok;                    // p of the draft token (0 without one)
   uint32_t n;                    // LDS entries
   uint32_t flags;
   uint32_t has_tok;
@@ -781,8 +781,8 @@ struct FinSh {
       uint64_t cum[kRowCap];     // a draw's exclusive prefix masses by entry
     } dr;
     struct {
-      uint32_t sup[kRowCap];     // a residual draw's support entries, compacted
-      float dv[kRowCap];         // and max(P - Q, 0) at them, by entry
+      float pv[kRowCap];         // a residual draw's P by entry
+      float dv[kRowCap];         // and max(P - Q, 0)
     } res;
   } u;
   uint32_t gbits[2][kGather];    // a select's crossing bucket: bits of p and masses
@@ -801,6 +801,7 @@ struct FinSh {
   RowAux aux[2];
   uint64_t red[4][2 * kFNW];     // block scan slots (callers alternate buffers)
   uint32_t sel[2];               // radix select: crossing digit per row
+  uint32_t selok[2];             // 0: the row's entries hold less than thr
   uint64_t sel64[2][2];          // (mass above the digit, the digit's mass)
   uint32_t fbits[2];             // a finished select's cutoff bits and retained mass
   uint64_t fmass[2];
@@ -809,6 +810,12 @@ struct FinSh {
   uint32_t last;                 // spec: this unit completes its batch element
   int64_t token;
 };
+
+// Lanes below this one whose bit is set in a wave mask.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
 
 // Block-wide inclusive scan of one u64 per thread; tot receives the total.
 // red must not be in use by a scan whose reads may still be pending.
@@ -919,7 +926,7 @@ __device__ __forceinline__ RecPair load_recs(const Params& p, int row) {
 }
 
 // Row constants and per-chunk data of row slot s from its records (wave s).
-__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, const RecPair& rp) {
+__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, const RecPair& rp, float top_p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int nch = p.nch;
   const float c = p.c;
@@ -984,6 +991,7 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, cons
   float xt = ta ? ra.xtok : (tb2 ? rb.xtok : 0.0f);
   const int tl = tk ? __builtin_ctzll(tk) : 0;
   xt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(xt), tl));
+  const float pt = tk ? p_of(xt, p.cd, mcmax, S) : 0.0f;
   if (lane == 0) {
     RowAux& a = f.aux[s];
     a.mcmax = mcmax;
@@ -992,48 +1000,57 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, cons
     a.n = ntot;
     a.has_tok = tk != 0;
     a.xtok = xt;
+    a.ptok = pt;
     a.flags = S > 0.0f ? 0u : kRowEmpty;
     a.cut = 0.0f;
     a.mass_f = 1.0f;
     a.mass_fx = 0;
-    a.top_p = 1.0f;
+    a.top_p = top_p;
   }
 }
 
-// Candidate slot i = t + q kFW of row slot s, loaded before the records were
-// known, into the LDS entries when the record's count covers it: entry
-// cstart + k holds (bits of x, index) until entry_p replaces x by p.
-__device__ __forceinline__ void place_slots(const Params& p, FinSh& f, int s, const uint64_t (&sl)[kEPT]) {
+// Candidate slots i = t + q kFW of the unit's rows, loaded before the records
+// were known, placed into the LDS entries when the record's count covers
+// them: entry cstart + k holds (bits of p, vocabulary index). The bits of p
+// and their masses stay in eb / ew (zero for an unused slot); the rows in
+// `hist` add their masses to the bins of the first select round (bits 29..19
+// of p), which are zero on entry.
+__device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr, const uint64_t (&sl)[2][kEPT],
+                                              uint32_t hist, uint32_t (&eb)[2][kEPT], uint64_t (&ew)[2][kEPT]) {
   const int t = threadIdx.x;
   const int nslot = p.nch * p.cap;
   const int lc = __builtin_ctz(static_cast<unsigned>(p.cap));
 #pragma unroll
-  for (int q = 0; q < kEPT; ++q) {
-    const int i = t + q * kFW;
-    if (i < nslot) {
-      const int j = i >> lc;
-      const uint32_t k = static_cast<uint32_t>(i & (p.cap - 1));
-      if (k < f.ccount[s][j]) {
-        const uint32_t e = f.cstart[s][j] + k;
-        f.ent[s].pbits[e] = static_cast<uint32_t>(sl[q]);
-        f.ent[s].eidx[e] = static_cast<uint32_t>(sl[q] >> 32);
+  for (int s = 0; s < 2; ++s) {
+    const RowK K{f.aux[s].mcmax, f.aux[s].s, p.cd};
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      eb[s][q] = 0u;
+      ew[s][q] = 0u;
+      const int i = t + q * kFW;
+      if (s < nr && i < nslot) {
+        const int j = i >> lc;
+        const uint32_t k = static_cast<uint32_t>(i & (p.cap - 1));
+        if (k < f.ccount[s][j]) {
+          const uint32_t e = f.cstart[s][j] + k;
+          const uint32_t idx = static_cast<uint32_t>(sl[s][q] >> 32);
+          const bool ok = idx < static_cast<uint32_t>(p.vocab);  // always, for a well-formed workspace
+          const uint32_t pb = ok ? __float_as_uint(pval(K, __uint_as_float(static_cast<uint32_t>(sl[s][q])))) : 0u;
+          f.ent[s].pbits[e] = pb;
+          f.ent[s].eidx[e] = ok ? idx : 0u;
+          eb[s][q] = pb;
+          ew[s][q] = fx46(__uint_as_float(pb));
+        }
       }
     }
-  }
-}
-
-// p of row slot s's placed entries, spread evenly over the workgroup; slot 1's
-// entries also go into the hash.
-__device__ __forceinline__ void entry_p(const Params& p, FinSh& f, int s, bool hash) {
-  const RowK K{f.aux[s].mcmax, f.aux[s].s, p.cd};
-  const uint32_t n = f.aux[s].n;
-  for (uint32_t e = threadIdx.x; e < n; e += kFW) {
-    const float x = __uint_as_float(f.ent[s].pbits[e]);
-    const uint32_t idx = f.ent[s].eidx[e];
-    const bool ok = idx < static_cast<uint32_t>(p.vocab);  // always, for a well-formed workspace
-    f.ent[s].pbits[e] = ok ? __float_as_uint(pval(K, x)) : 0u;
-    f.ent[s].eidx[e] = ok ? idx : 0u;
-    if (hash && ok) hash_insert(f, idx, e);
+    if ((hist >> s) & 1u) {
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) {
+        if (ew[s][q] && (eb[s][q] >> 30) == 0u)
+          __hip_atomic_fetch_add(&f.u.bins[s][eb[s][q] >> 19], ew[s][q], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
   }
 }
 
@@ -1041,21 +1058,30 @@ __device__ __forceinline__ void entry_p(const Params& p, FinSh& f, int s, bool h
 // Top-p cutoffs
 // ---------------------------------------------------------------------------
 
-// Exact top-p cutoffs over the LDS entries of the rows in `mask` (bit s for
-// slot s), in shared rounds: c_s = max{v : sum over entries with p >= v of
-// fx46(p) >= thr_s}. Radix rounds on the bits of p (p <= 1, so bits < 2^30):
-// bits 29..19, 18..8 and 7..0; after each round the entries of the crossing
-// digit are gathered and, when at most kGather, finished by one wave (wave s
-// for row s). ok[s] is false when the entries hold less than thr_s. Entries of
-// zero mass never decide the cutoff and are skipped. f.u.bins must be zero on
-// entry, unless zeroed = false (then they are cleared here first).
-__device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const uint64_t (&thr)[2], float (&cut)[2],
-                                               uint64_t (&mass)[2], bool (&ok)[2], bool zeroed) {
+// Exact top-p cutoffs over the entries of the rows in `mask` (bit s for slot
+// s): c_s = max{v : sum over entries with p >= v of fx46(p) >= thr_s}. Every
+// thread holds kEPT entries of each row in registers (eb: bits of p, ew: their
+// masses; zero for an unused slot), any partition of the row's entries over
+// the threads. Radix rounds on the bits of p (p <= 1, so bits < 2^30): bits
+// 29..19, 18..8 and 7..0. In each round wave s alone finds row s's crossing
+// digit (lane l sums the 32 bins below kSelBins - 32 l, one wave scan finds
+// the lane and a second one the digit); the entries of that digit are then
+// gathered and, when at most kGather, finished by wave s, which also stores
+// the row's cutoff and retained mass in f.aux[s] (set[s]). ok[s] is false
+// when the entries hold less than thr_s. Entries of zero mass never decide
+// the cutoff and are skipped. hist: round 0's masses are already in the bins
+// (which are otherwise cleared here first).
+__device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const uint64_t (&thr)[2],
+                                               const uint32_t (&eb)[2][kEPT], const uint64_t (&ew)[2][kEPT],
+                                               bool hist, float (&cut)[2], uint64_t (&mass)[2],
+                                               bool (&ok)[2], bool (&set)[2]) {
   const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
   bool live[2] = {(mask & 1u) != 0, (mask & 2u) != 0};
   ok[0] = live[0];
   ok[1] = live[1];
-  if (!zeroed) {
+  set[0] = false;
+  set[1] = false;
+  if (!hist) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (live[s]) {
@@ -1065,7 +1091,6 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
     }
     __syncthreads();
   }
-  const uint32_t n[2] = {f.aux[0].n, f.aux[1].n};
   uint32_t prefix[2] = {0u, 0u};  // the resolved high bits: bits >> hshift
   uint64_t above[2] = {0u, 0u};   // mass strictly above the resolved prefix
   for (int round = 0; round < 3 && (live[0] || live[1]); ++round) {
@@ -1073,90 +1098,101 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
     const int width = round == 2 ? 8 : 11;
     const int hshift = shift + width;
     // 1. masses into the bins of this round's digit
+    if (round > 0 || !hist) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (!live[s]) continue;
-      for (uint32_t e = t; e < n[s]; e += kFW) {
-        const uint32_t b = f.ent[s].pbits[e];
-        const uint64_t w = fx46(__uint_as_float(b));
-        if (w && (b >> hshift) == prefix[s])
-          __hip_atomic_fetch_add(&f.u.bins[s][(b >> shift) & ((1u << width) - 1u)], w, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int s = 0; s < 2; ++s) {
+        if (!live[s]) continue;
+#pragma unroll
+        for (int q = 0; q < kEPT; ++q) {
+          if (ew[s][q] && (eb[s][q] >> hshift) == prefix[s])
+            __hip_atomic_fetch_add(&f.u.bins[s][(eb[s][q] >> shift) & ((1u << width) - 1u)], ew[s][q],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
-    // 2. thread t holds digits kSelBins - 1 - (kSelPer t + q), descending;
-    //    the gather counts restart (their last reads precede the last barrier)
-    if (t < 2) f.gcount[t] = 0;
-    uint64_t v[2][kSelPer], sum[2] = {0u, 0u}, inc[2] = {0u, 0u};
-    uint64_t* red = f.red[round & 1];
+    // 2. the crossing digit of row s, by wave s
+    if (wid < 2 && live[wid]) {
+      const int s = wid;
+      const uint64_t* bs = f.u.bins[s];
+      const int lo = kSelBins - kWave / 2 * (lane + 1);  // this lane's lowest bin
+      // the lanes start at different bins, so one read of the wave touches
+      // every bank about evenly (32 bins per lane: lane stride 256 bytes)
+      uint64_t own = 0;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (!live[s]) continue;
-#pragma unroll
-      for (int q = 0; q < kSelPer; ++q) {
-        v[s][q] = f.u.bins[s][kSelBins - 1 - (kSelPer * t + q)];
-        sum[s] += v[s][q];
-      }
-      inc[s] = wave_scan_add_u64(sum[s]);
-      if (lane == kWave - 1) red[s * kFNW + wid] = inc[s];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (!live[s]) continue;
-      uint64_t base = 0, tot = 0;
-#pragma unroll
-      for (int i = 0; i < kFNW; ++i) {
-        const uint64_t x = red[s * kFNW + i];
-        base += i < wid ? x : 0;
-        tot += x;
-      }
+      for (int i = 0; i < kWave / 2; ++i) own += bs[lo + ((i + lane) & (kWave / 2 - 1))];
+      const uint64_t incl = wave_scan_add_u64(own);
+      const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
       const uint64_t need = thr[s] - above[s];  // > 0: above < thr
       if (tot < need) {
+        if (lane == 0) f.selok[s] = 0u;
+      } else {
+        const int c = __builtin_ctzll(__ballot(incl >= need));
+        const uint64_t before = lane_bcast_u64(incl - own, c);
+        const int bin = kSelBins - 1 - kWave / 2 * c - lane;
+        const uint64_t v = lane < kWave / 2 ? bs[bin] : 0u;
+        const uint64_t inc2 = wave_scan_add_u64(v);
+        const int d = __builtin_ctzll(__ballot(lane < kWave / 2 && before + inc2 >= need));
+        if (lane == d) {
+          f.sel[s] = static_cast<uint32_t>(bin);
+          f.sel64[s][0] = above[s] + before + inc2 - v;
+          f.sel64[s][1] = v;
+          f.selok[s] = 1u;
+        }
+      }
+      if (lane == 0) f.gcount[s] = 0;
+    }
+    __syncthreads();
+    // 3. the crossing digit's entries gathered (ballot-compacted, one LDS
+    //    atomic per wave and row); the bins cleared for the next round (their
+    //    reads are all before the last barrier)
+    uint64_t binmass[2] = {0u, 0u};
+    uint64_t gm[2][kEPT];
+    uint32_t gcnt[2] = {0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s]) continue;
+      if (!f.selok[s]) {
         // the entries hold less than thr (uniform over the workgroup)
         live[s] = false;
         ok[s] = false;
         continue;
       }
-      uint64_t before = base + inc[s] - sum[s];
-      if (before < need && before + sum[s] >= need) {
-#pragma unroll
-        for (int q = 0; q < kSelPer; ++q) {
-          if (before < need && before + v[s][q] >= need) {
-            f.sel[s] = static_cast<uint32_t>(kSelBins - 1 - (kSelPer * t + q));
-            f.sel64[s][0] = above[s] + before;
-            f.sel64[s][1] = v[s][q];
-          }
-          before += v[s][q];
-        }
-      }
-    }
-    __syncthreads();
-    // 3. the crossing digit; its entries gathered; the bins cleared for the
-    //    next round (their reads are all before the last barrier)
-    uint64_t binmass[2] = {0u, 0u};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (!live[s]) continue;
       prefix[s] = (prefix[s] << width) | f.sel[s];
       above[s] = f.sel64[s][0];
       binmass[s] = f.sel64[s][1];
-      for (uint32_t e = t; e < n[s]; e += kFW) {
-        const uint32_t b = f.ent[s].pbits[e];
-        if ((b >> shift) == prefix[s] && fx46(__uint_as_float(b))) {
-          const uint32_t k = __hip_atomic_fetch_add(&f.gcount[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          if (k < kGather) {
-            f.gbits[s][k] = b;
-            f.gw[s][k] = fx46(__uint_as_float(b));
-          }
-        }
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) {
+        gm[s][q] = __ballot(ew[s][q] && (eb[s][q] >> shift) == prefix[s]);
+        gcnt[s] += static_cast<uint32_t>(__builtin_popcountll(gm[s][q]));
       }
 #pragma unroll
       for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
     }
+    uint32_t gbase[2] = {0u, 0u};
+    if (lane == 0) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (live[s] && gcnt[s])
+          gbase[s] = __hip_atomic_fetch_add(&f.gcount[s], gcnt[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (!live[s] || !gcnt[s]) continue;
+      uint32_t at = lane_bcast_u32(gbase[s], 0);
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) {
+        const uint32_t k = at + lanes_below(gm[s][q]);
+        if (((gm[s][q] >> lane) & 1ull) && k < static_cast<uint32_t>(kGather)) {
+          f.gbits[s][k] = eb[s][q];
+          f.gw[s][k] = ew[s][q];
+        }
+        at += static_cast<uint32_t>(__builtin_popcountll(gm[s][q]));
+      }
+    }
     __syncthreads();
-    // 4. a small bucket is finished by one wave: lane l holds entry l, its
+    // 4. a small bucket is finished by wave s: lane l holds entry l, its
     //    mass at and above it A_l; the cutoff is the largest p with A >= thr
     bool fin[2] = {false, false};
 #pragma unroll
@@ -1187,6 +1223,11 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
           if (lane == 0) {
             f.fbits[s] = static_cast<uint32_t>(best);
             f.fmass[s] = at;
+            RowAux& a = f.aux[s];
+            a.flags = kRowFiltered | kRowList;
+            a.cut = __uint_as_float(static_cast<uint32_t>(best));
+            a.mass_fx = at;
+            a.mass_f = mass_to_f32(at);
           }
         }
       } else if (round == 2) {
@@ -1204,10 +1245,10 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
         cut[s] = __uint_as_float(f.fbits[s]);
         mass[s] = f.fmass[s];
         live[s] = false;
+        set[s] = true;
       }
     }
   }
-  __syncthreads();
 }
 
 // Passes over a whole row for the slow path: fn(index, x) for every element,
@@ -1388,28 +1429,18 @@ __device__ __forceinline__ bool collect_support(const Params& p, FinSh& f, int s
 
 // Resolves the cutoffs of the unit's nr rows: list mode (kRowList: the support
 // is in the LDS entries) or dense (the support is {p >= cut} of the whole
-// row). The rows' first selects share their rounds.
+// row). The rows in `mask` are filtered (thr: their thresholds); their first
+// selects share their rounds, over the entries in eb / ew, whose first-round
+// masses are in the bins already. Unfiltered rows keep row_setup's state.
 template <int DT>
-__device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, const int (&rows)[2], const RowK (&K)[2]) {
-  uint32_t mask = 0;
-  uint64_t thr[2] = {0u, 0u};
-  float top_p[2] = {1.0f, 1.0f};
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s >= nr) break;
-    top_p[s] = row_top_p(p, rows[s]);
-    if (top_p[s] < 1.0f && !(f.aux[s].flags & kRowEmpty)) {
-      mask |= 1u << s;
-      // a threshold of 0 (top_p < 2^-46) selects the largest p, as 1 does
-      // whenever that p has a nonzero mass
-      const uint64_t tf = fx46(top_p[s]);
-      thr[s] = tf > 0 ? tf : 1;
-    }
-  }
+__device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, const int (&rows)[2], const RowK (&K)[2],
+                                            uint32_t mask, const uint64_t (&thr)[2], const uint32_t (&eb)[2][kEPT],
+                                            const uint64_t (&ew)[2][kEPT]) {
   float cut[2] = {0.0f, 0.0f};
   uint64_t mass[2] = {0u, 0u};
-  bool ok[2] = {false, false};
-  if (mask) select_entries(f, mask, thr, cut, mass, ok, true);
+  bool ok[2] = {false, false}, set[2] = {false, false};
+  if (mask) select_entries(f, mask, thr, eb, ew, true, cut, mass, ok, set);
+  bool generic = false;  // a row whose state thread 0 stores below
   uint32_t flags[2] = {f.aux[0].flags & kRowEmpty, f.aux[1].flags & kRowEmpty};
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -1422,10 +1453,22 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
         if (f.bound[s][j] >= cut[s]) ok[s] = refill_chunk<DT>(p, f, s, rows[s], K[s], j, cut[s]);
       }
       if (ok[s]) {
+        uint32_t eb1[2][kEPT];
+        uint64_t ew1[2][kEPT];
+        const uint32_t n = f.aux[s].n;
+#pragma unroll
+        for (int s1 = 0; s1 < 2; ++s1) {
+#pragma unroll
+          for (int q = 0; q < kEPT; ++q) {
+            const uint32_t e = static_cast<uint32_t>(threadIdx.x + kFW * q);
+            eb1[s1][q] = (s1 == s && e < n) ? f.ent[s].pbits[e] : 0u;
+            ew1[s1][q] = fx46(__uint_as_float(eb1[s1][q]));
+          }
+        }
         float c1[2];
         uint64_t m1[2];
-        bool o1[2];
-        select_entries(f, 1u << s, thr, c1, m1, o1, false);
+        bool o1[2], set1[2];
+        select_entries(f, 1u << s, thr, eb1, ew1, false, c1, m1, o1, set1);
         ok[s] = o1[s];
         cut[s] = c1[s];
         mass[s] = m1[s];
@@ -1436,25 +1479,23 @@ __device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, 
       select_row<DT>(p, f, rows[s], K[s], thr[s], &cut[s], &mass[s]);
       if (collect_support<DT>(p, f, s, rows[s], K[s], cut[s])) flags[s] |= kRowList;
     }
+    if (flags[s] != (kRowFiltered | kRowList) || !set[s]) generic = true;
   }
-  if (threadIdx.x == 0) {
+  if (generic) {
+    __syncthreads();  // every read of the rows' state above precedes the stores
+    if (threadIdx.x == 0) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (s >= nr) break;
-      RowAux& a = f.aux[s];
-      a.flags = flags[s];
-      a.top_p = top_p[s];
-      if (flags[s] & kRowFiltered) {
+      for (int s = 0; s < 2; ++s) {
+        if (s >= nr || !((mask >> s) & 1u)) continue;
+        RowAux& a = f.aux[s];
+        a.flags = flags[s];
         a.cut = cut[s];
         a.mass_fx = mass[s];
         a.mass_f = mass_to_f32(mass[s]);
-      } else {
-        a.cut = 0.0f;
-        a.mass_f = 1.0f;
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
 }
 
 // Filtered probability of a row at p (P = p when unfiltered).
@@ -1532,7 +1573,7 @@ __device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64
 // among entries of nonzero weight) and scanned there.
 __device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t (&wl)[kEPT], float u,
                                              bool ordered) {
-  const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+  const int t = threadIdx.x;
   const uint32_t n = f.aux[0].n;
   uint32_t js;
   uint64_t rem;
@@ -1665,44 +1706,59 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
   const RowAux& a = f.aux[0];
   if (a.flags & kRowList) {
     const uint32_t n = a.n;
-    // P at this thread's entries; the support entries (P > 0) compacted
-    float pl[kEPT];
-    uint32_t own = 0;
+    const RowAux& a1 = f.aux[1];
+    // P and d = max(P - Q, 0) at the entries t + kFW q (every wave takes a
+    // share), Q where P > 0; in list mode the first hash probes of all of
+    // them go out together and only a collision walks on
+    float P[kEPT], Q[kEPT];
+    uint32_t ix[kEPT];
 #pragma unroll
     for (int q = 0; q < kEPT; ++q) {
-      const uint32_t e = kEPT * t + q;
-      pl[q] = e < n ? filtered_of(a, __uint_as_float(f.ent[0].pbits[e])) : 0.0f;
-      own += pl[q] > 0.0f ? 1u : 0u;
+      const uint32_t e = t + kFW * q;
+      P[q] = e < n ? filtered_of(a, __uint_as_float(f.ent[0].pbits[e])) : 0.0f;
+      ix[q] = e < n ? f.ent[0].eidx[e] : 0u;
+      Q[q] = 0.0f;
     }
-    uint64_t nsup;
-    const uint64_t incl = block_incl_scan(own, f.red[0], &nsup);
-    uint32_t k = static_cast<uint32_t>(incl) - own;
+    if ((a1.flags & kRowList) && !(a1.flags & kRowEmpty)) {
+      uint32_t v[kEPT], m[kEPT];
 #pragma unroll
-    for (int q = 0; q < kEPT; ++q) {
-      if (pl[q] > 0.0f) f.u.res.sup[k++] = kEPT * t + q;
+      for (int q = 0; q < kEPT; ++q) v[q] = P[q] > 0.0f ? f.hash[hash_slot(ix[q])] : 0u;
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) m[q] = v[q] ? f.ent[1].eidx[v[q] - 1u] : 0u;
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) {
+        if (v[q] && m[q] != ix[q]) v[q] = hash_find(f, ix[q]) + 1u;  // kNone + 1 = 0: absent
+        if (v[q]) Q[q] = filtered_of(a1, __uint_as_float(f.ent[1].pbits[v[q] - 1u]));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kEPT; ++q) {
+        if (P[q] > 0.0f) Q[q] = q_at<DT>(p, f, K1, row1, ix[q]);
+      }
     }
-    __syncthreads();
-    // d = max(P - Q, 0) at the support entries, Q through the draft's hash
     uint64_t dsum = 0, psum = 0;
-    for (uint32_t j = t; j < static_cast<uint32_t>(nsup); j += kFW) {
-      const uint32_t e = f.u.res.sup[j];
-      const float P = filtered_of(a, __uint_as_float(f.ent[0].pbits[e]));
-      const float Q = q_at<DT>(p, f, K1, row1, f.ent[0].eidx[e]);
-      float d = P - Q;
-      d = d > 0.0f ? d : 0.0f;
-      f.u.res.dv[e] = d;
+#pragma unroll
+    for (int q = 0; q < kEPT; ++q) {
+      float d = P[q] - Q[q];
+      d = P[q] > 0.0f && d > 0.0f ? d : 0.0f;
+      const uint32_t e = t + kFW * q;
+      if (e < n) {
+        f.u.res.pv[e] = P[q];
+        f.u.res.dv[e] = d;
+      }
       dsum += fx46(d);
-      psum += fx46(P);
+      psum += fx46(P[q]);
     }
     uint64_t dtot, ptot;
     block_sum2(dsum, psum, f.red[1], &dtot, &ptot);
     const bool use_d = dtot > 0;
     const float den = use_d ? mass_to_f32(dtot) : (ptot > 0 ? mass_to_f32(ptot) : 1.0f);
+    // the draw's weights at this thread's entries kEPT t + q
     uint64_t wl[kEPT];
 #pragma unroll
     for (int q = 0; q < kEPT; ++q) {
-      const float d = pl[q] > 0.0f ? f.u.res.dv[kEPT * t + q] : 0.0f;
-      wl[q] = fx46((use_d ? d : pl[q]) / den);
+      const uint32_t e = kEPT * t + q;
+      wl[q] = e < n ? fx46((use_d ? f.u.res.dv[e] : f.u.res.pv[e]) / den) : 0u;
     }
     return draw_list(p, f, wl, u, !(a.flags & kRowRefilled));
   }
@@ -1774,6 +1830,8 @@ void fin_kernel(const Params p) {
   } else if (p.mode == kModeSample) {
     u_draw = p.row_uniforms[rows[0]];
   }
+  const float tp0 = row_top_p(p, rows[0]);
+  const float tp1 = nr == 2 ? row_top_p(p, rows[1]) : 1.0f;
   // every load of the set-up issued before any result is used: the records
   // (wave s < nr, row s) first, then every candidate slot of both rows
   RecPair rp;
@@ -1798,17 +1856,29 @@ void fin_kernel(const Params p) {
     f.u.bins[0][kSelPer * t + q] = 0;
     f.u.bins[1][kSelPer * t + q] = 0;
   }
-  if (w < nr) row_setup(p, f, w, rp);
+  if (w < nr) row_setup(p, f, w, rp, w == 0 ? tp0 : tp1);
   __syncthreads();
-  place_slots(p, f, 0, sl[0]);
-  if (nr == 2) place_slots(p, f, 1, sl[1]);
-  __syncthreads();
-  entry_p(p, f, 0, false);
-  if (nr == 2) entry_p(p, f, 1, false);
+  // the filtered rows and their thresholds
+  uint32_t mask = 0;
+  uint64_t thr[2] = {0u, 0u};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const float tp = s == 0 ? tp0 : tp1;
+    if (s < nr && tp < 1.0f && !(f.aux[s].flags & kRowEmpty)) {
+      mask |= 1u << s;
+      // a threshold of 0 (top_p < 2^-46) selects the largest p, as 1 does
+      // whenever that p has a nonzero mass
+      const uint64_t tf = fx46(tp);
+      thr[s] = tf > 0 ? tf : 1;
+    }
+  }
+  uint32_t eb[2][kEPT];
+  uint64_t ew[2][kEPT];
+  place_entries(p, f, nr, sl, mask, eb, ew);
   __syncthreads();
   RowK K[2];
   for (int s = 0; s < 2; ++s) K[s] = RowK{f.aux[s < nr ? s : 0].mcmax, f.aux[s < nr ? s : 0].s, p.cd};
-  resolve_rows<DT>(p, f, nr, rows, K);
+  resolve_rows<DT>(p, f, nr, rows, K, mask, thr, eb, ew);
 
   if (p.mode == kModeSpec) {
     const int k = p.k;
@@ -1819,8 +1889,8 @@ void fin_kernel(const Params p) {
     } else {
       const RowAux& a0 = f.aux[0];
       const RowAux& a1 = f.aux[1];
-      const float P = a0.has_tok ? filtered_of(a0, pval(K[0], a0.xtok)) : 0.0f;
-      const float Q = a1.has_tok ? filtered_of(a1, pval(K[1], a1.xtok)) : 0.0f;
+      const float P = a0.has_tok ? filtered_of(a0, a0.ptok) : 0.0f;
+      const float Q = a1.has_tok ? filtered_of(a1, a1.ptok) : 0.0f;
       acc = accept_draw(u_acc, P, Q);
       // the draft's support by vocabulary index, for the residual's Q lookups
       if (!acc && (a1.flags & kRowList)) hash_support(f);
