@@ -65,12 +65,13 @@ static_assert(kLmBM * 4 * 8 <= kLmABytes, "epilogue keys fit an A buffer");
 
 
 // Direct global-to-LDS load of 16 bytes per lane: lane l's bytes land at LDS
-// address lds + 16 l (lds wave-uniform). Issued as an instruction the compiler
-// does not track, so that its own LDS-hazard waits do not stall reads of the
-// other buffers while the load is in flight; the caller waits for it
-// explicitly (vmcnt) before the workgroup reads the buffer.
+// address lds + 16 l (lds wave-uniform, passed in M0, which the compiler sets
+// for the statement as an operand). Issued as an instruction the compiler does
+// not track, so that its own LDS-hazard waits do not stall reads of the other
+// buffers while the load is in flight; the caller waits for it explicitly
+// (vmcnt) before the workgroup reads the buffer.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds) : "memory");
 }
 
 // Byte offset of 16-byte chunk c of row r in an A block.
