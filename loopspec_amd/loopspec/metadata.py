@@ -1,0 +1,146 @@
+"""Decode metadata for the graph ops: one upload per step of int64 rows [8, B]
+(one column per pipeline lane) followed by int32 original lengths [B].
+
+Keeps the layout, row meanings and names of
+sglang_recurrent/loopspec/metadata.py (MetadataRow :14-25, payload_size
+:31-41, payload_views :44-56, DecodeStagingSlot :85-193,
+DirectMetadataStagingSlot :196-232): the graphs index these rows, so the
+layout is the interface. The rows a decode stages come from each lane's
+timeline: the request row, the new length, the position of the token, and,
+for a timeline forked since its last decode, the parent's row and the prefix
+length to copy from it (update_request_mapping copies it once, then appends
+the new KV ID; graph_ops.py:175-271).
+
+Timelines are read through either this build's field names
+(branching.timelines.Timeline: row, seq_len, pending_parent_row) or the
+reference's (TimelineCursor: req_pool_idx, seq_len,
+pending_parent_req_pool_idx).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+from enum import IntEnum
+from typing import Any
+
+import torch
+
+
+class MetadataRow(IntEnum):
+    REQUEST = 0              # row of the request-to-token mapping the token is decoded into
+    SEQUENCE_LENGTH = 1      # cached prefix length plus the decoded token
+    POSITION = 2             # position of the decoded token (the prefix length)
+    TOKEN = 3                # input token id
+    PARENT_REQUEST = 4       # mapping row a newly forked timeline copies its prefix from
+    MAPPING_COPY_LENGTH = 5  # prefix entries to copy (0: append only)
+    STATE_INPUT = 6          # state-bank row to gather (-1: none)
+    STATE_OUTPUT = 7         # state-bank row to scatter into (-1: none)
+
+
+DECODE_METADATA_ROWS = len(MetadataRow)
+_I64 = torch.int64.itemsize
+_I32 = torch.int32.itemsize
+
+
+def payload_size(batch_size: int) -> int:
+    """Bytes of one upload: eight int64 and one int32 per lane."""
+    return batch_size * (DECODE_METADATA_ROWS * _I64 + _I32)
+
+
+def payload_views(payload: torch.Tensor, batch_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(int64 rows [8, B], int32 original lengths [B]) sharing a contiguous
+    uint8 payload of payload_size(batch_size) bytes, on its device."""
+    split = DECODE_METADATA_ROWS * batch_size * _I64
+    rows = payload[:split].view(torch.int64).view(DECODE_METADATA_ROWS, batch_size)
+    return rows, payload[split:].view(torch.int32)
+
+
+def _row_of(tl: Any) -> int:
+    return int(tl.row if hasattr(tl, "row") else tl.req_pool_idx)
+
+
+def _parent_of(tl: Any):
+    return tl.pending_parent_row if hasattr(tl, "pending_parent_row") else tl.pending_parent_req_pool_idx
+
+
+class _Upload:
+    """A pinned host payload whose last asynchronous upload must finish
+    before the host overwrites it (the next stage() waits on its event)."""
+
+    def __init__(self) -> None:
+        self._done = torch.cuda.Event()
+        self._pending = False
+
+    def _before_write(self) -> None:
+        if self._pending:
+            self._done.synchronize()
+            self._pending = False
+
+    def _after_upload(self, device) -> None:
+        self._done.record(torch.cuda.current_stream(device))
+        self._pending = True
+
+
+class DecodeStagingSlot(_Upload):
+    """Pinned staging for one decode batch of batch_size lanes."""
+
+    def __init__(self, batch_size: int) -> None:
+        super().__init__()
+        self.batch_size = batch_size
+        self.payload_nbytes = payload_size(batch_size)
+        # [uploaded rows + original lengths | host-only sequence lengths]
+        self.host = torch.empty(self.payload_nbytes + batch_size * _I32, dtype=torch.uint8, pin_memory=True)
+        self.host_rows, self.host_original_lengths = payload_views(self.host[: self.payload_nbytes], batch_size)
+        self.host_sequence_lengths = self.host[self.payload_nbytes:].view(torch.int32)
+
+    def stage(self, timelines: Sequence[Any], token_ids: Sequence[int], direct_graph_payload: torch.Tensor,
+              state_input_slots: Sequence[int] | None = None,
+              state_output_slots: Sequence[int] | None = None):
+        """Fill and upload the rows for one decode of each timeline (lane b =
+        timelines[b], token_ids[b]); timelines are read, not advanced.
+        Returns (device rows [8, B], device original lengths [B], device
+        token ids [B], host sequence lengths [B]) as reusable views; the
+        upload is asynchronous on the current stream."""
+        b = self.batch_size
+        if len(timelines) != b or len(token_ids) != b:
+            raise ValueError("stage: one timeline and one token per lane")
+        cols = []
+        for tl in timelines:
+            parent = _parent_of(tl)
+            row, n = _row_of(tl), int(tl.seq_len)
+            cols.append((row, n + 1, n, int(parent) if parent is not None else row, n if parent is not None else 0))
+        ins = [-1] * b if state_input_slots is None else list(state_input_slots)
+        outs = [-1] * b if state_output_slots is None else list(state_output_slots)
+        table = torch.tensor(
+            [[c[0] for c in cols], [c[1] for c in cols], [c[2] for c in cols], list(token_ids),
+             [c[3] for c in cols], [c[4] for c in cols], ins, outs], dtype=torch.int64)
+        lengths = torch.tensor([c[1] for c in cols], dtype=torch.int32)
+        self._before_write()
+        self.host_rows.copy_(table)
+        self.host_original_lengths.copy_(lengths)
+        self.host_sequence_lengths.copy_(lengths)
+        direct_graph_payload.copy_(self.host[: self.payload_nbytes], non_blocking=True)
+        self._after_upload(direct_graph_payload.device)
+        rows, original = payload_views(direct_graph_payload, b)
+        return rows, original, rows[MetadataRow.TOKEN], self.host_sequence_lengths
+
+
+class DirectMetadataStagingSlot(_Upload):
+    """Pinned staging for an attention-free role graph: the same layout,
+    only the rows the caller names are updated (the others keep their
+    values, zero at first)."""
+
+    def __init__(self, batch_size: int) -> None:
+        super().__init__()
+        self.batch_size = batch_size
+        self.host = torch.zeros(payload_size(batch_size), dtype=torch.uint8, pin_memory=True)
+        self.host_rows, _ = payload_views(self.host, batch_size)
+
+    def stage(self, rows: Mapping[MetadataRow, Sequence[int]], device_payload: torch.Tensor) -> torch.Tensor:
+        self._before_write()
+        for r, values in rows.items():
+            self.host_rows[int(r)].copy_(torch.as_tensor(list(values), dtype=torch.int64))
+        device_payload.copy_(self.host, non_blocking=True)
+        self._after_upload(device_payload.device)
+        rows_view, _ = payload_views(device_payload, self.batch_size)
+        return rows_view

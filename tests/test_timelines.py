@@ -69,3 +69,21 @@ def test_fork_rows_exhaust_like_the_reference():
     dev.timelines("core", [0, 0], [1, 2], [0, 0])
     with pytest.raises(RuntimeError, match="ran out of request-pool rows"):
         dev.timelines("core", [0], [3], [0])
+
+
+def test_metadata_payload_layout():
+    from loopspec_amd.loopspec.metadata import DECODE_METADATA_ROWS, MetadataRow, payload_size, payload_views
+
+    assert DECODE_METADATA_ROWS == 8 and [r.name for r in MetadataRow] == [
+        "REQUEST", "SEQUENCE_LENGTH", "POSITION", "TOKEN", "PARENT_REQUEST", "MAPPING_COPY_LENGTH",
+        "STATE_INPUT", "STATE_OUTPUT"]
+    b = 5
+    assert payload_size(b) == b * (8 * 8 + 4)
+    payload = torch.zeros(payload_size(b), dtype=torch.uint8)
+    rows, lengths = payload_views(payload, b)
+    assert rows.shape == (8, b) and rows.dtype == torch.int64 and lengths.shape == (b,) and lengths.dtype == torch.int32
+    rows[MetadataRow.TOKEN] = torch.arange(b)
+    lengths[:] = 7
+    # the lengths follow the rows, in the same storage
+    assert payload[8 * 8 * b:].view(torch.int32).tolist() == [7] * b
+    assert payload[3 * 8 * b: 4 * 8 * b].view(torch.int64).tolist() == list(range(b))
