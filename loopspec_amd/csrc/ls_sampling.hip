@@ -5,7 +5,8 @@
 // then, for dense outputs only, dense_kernel.
 //
 // stream_kernel reads every logit once: one wave per (row, 2048-element
-// chunk) item, four independent waves per workgroup. A wave
+// chunk) item, four independent waves per workgroup (stream_reg_kernel
+// without a penalty: the chunk held in registers only). A wave
 //   * stages its chunk in LDS, decodes it, sets penalised tokens aside;
 //   * computes the chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk
 //     mass M_j in the declared pairwise order; the penalised tokens' own max
@@ -729,6 +730,211 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   }
 }
 
+// The same item without a penalty, the chunk held in registers only (no LDS):
+// the raw logits stay in x[], the exponents are recomputed where they are
+// needed, and a candidate's value is selected among its vector's registers.
+// Same results as stream_item<DT, false>; at most 64 VGPRs, so eight waves
+// per SIMD fit where the staged form fits five.
+template <int DT>
+__device__ __forceinline__ void stream_item_reg(const Params& p, const Item& I,
+                                                const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4]) {
+  constexpr int EPV = Elem<DT>::kPerVec;
+  constexpr int NVC = kChunk / (kWave * EPV);
+  constexpr int NE = NVC * EPV;
+  static_assert(NE == 32, "32 elements per lane");
+  int t = threadIdx.x & (kWave - 1);
+  asm volatile("" : "+v"(t));
+  const int c0 = I.chunk * kChunk;
+  const int nel = p.vocab - c0 < kChunk ? p.vocab - c0 : kChunk;
+  const int nvc = nel / EPV;
+  const bool full = nel == kChunk;
+
+  // decoded logits, lanes past the row end at -inf
+  float x[NE];
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) x[u * EPV + e] = vec_elem<DT>(d[u], e);
+  }
+  if (!full) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      if (u * kWave + t >= nvc) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) x[u * EPV + e] = -__builtin_inff();
+      }
+    }
+  }
+
+  // vector maxima and the chunk max (NaN-propagating; a NaN chunk is redone
+  // ignoring NaN)
+  float vm[NVC];
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) {
+    float mv = x[u * EPV];
+#pragma unroll
+    for (int e = 1; e < EPV; ++e) mv = nmax(mv, x[u * EPV + e]);
+    vm[u] = mv;
+  }
+  float mx = vm[0];
+#pragma unroll
+  for (int u = 1; u < NVC; ++u) mx = nmax(mx, vm[u]);
+  float m = wave_max_f32(mx);
+  if (m != m) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      float mv = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) mv = x[u * EPV + e] > mv ? x[u * EPV + e] : mv;
+      vm[u] = mv;
+    }
+    mx = vm[0];
+#pragma unroll
+    for (int u = 1; u < NVC; ++u) mx = mx > vm[u] ? mx : vm[u];
+    m = wave_max_f32(mx);
+  }
+  const float c = p.c;
+  const float mc = m * c;
+  const float nmc = -mc;
+  const int cap = p.cap;
+
+  // a start for the level L (no penalty: mref = mc): the largest L in
+  // [0, kMaxLevel] at which at most cap of the lane vectors hold a candidate
+  // (binary search; the count only grows with L). Every vector that holds a
+  // candidate at L adds one to the element count, so the L the element passes
+  // below settle on is the largest at which at most cap elements qualify.
+  int lo = 0;
+  if (mc > -__builtin_inff()) {
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) vm[u] = __builtin_fmaf(vm[u], c, nmc);
+    int hi = kMaxLevel;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      const float th = -static_cast<float>(mid);
+      uint32_t nv = 0;
+#pragma unroll
+      for (int u = 0; u < NVC; ++u) nv += __builtin_popcountll(__ballot(vm[u] >= th));
+      if (nv <= static_cast<uint32_t>(cap)) lo = mid; else hi = mid - 1;
+    }
+  }
+
+  // the chunk mass: e = exp2m(fma(x, c, -mc)) in the declared lane tree,
+  // summed four elements at a time (the tree's subtrees of four, then of 8,
+  // 16 and 32); each group's exponents wait for the previous group's sum, so
+  // at most four values are in flight beside x
+  float mass;
+  {
+    float nv = nmc;
+    float s8[NE / 8], s16 = 0.0f, s4p = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NE / 4; ++g) {
+      float e4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e4[q] = exp2q_finite(__builtin_fmaf(x[4 * g + q], c, nv));
+      const float s4 = (e4[0] + e4[1]) + (e4[2] + e4[3]);
+      if (g & 1) {
+        s8[g / 2] = s4p + s4;
+        if ((g / 2) & 1) {
+          const float a16 = s8[g / 2 - 1] + s8[g / 2];
+          s16 = (g / 4) & 1 ? s16 + a16 : a16;
+        }
+      } else {
+        s4p = s4;
+      }
+      asm volatile("" : "+v"(nv) : "v"(s4));
+    }
+    mass = wave_tree_sum(s16);
+  }
+  if (mass != mass) {
+    float ea[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) ea[i] = exp2q(__builtin_fmaf(x[i], c, nmc));
+    mass = wave_tree_sum(lane_tree_sum(ea));
+  }
+
+  // the level L: from the start down, the first at which at most cap
+  // elements satisfy RN32(x c - mc) >= -L
+  int L = -1;
+  uint32_t mask = 0;  // bit 31 - i <-> element i
+  if (mc > -__builtin_inff()) {
+    for (L = lo; L >= 0; --L) {
+      const float th = -static_cast<float>(L);
+      // the exponent is formed inside the same asm (one temporary per
+      // element at a time): fma, compare into VCC, add with carry
+      uint32_t mq[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < NE / 4; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float tx;
+          asm("v_fma_f32 %1, %2, %3, %4\n\tv_cmp_ge_f32_e32 vcc, %1, %5\n\t"
+              "v_addc_co_u32_e32 %0, vcc, %0, %0, vcc"
+              : "+v"(mq[q]), "=&v"(tx) : "v"(x[(NE / 4) * q + i]), "s"(c), "v"(nmc), "v"(th) : "vcc");
+        }
+      }
+      mask = (mq[0] << 24) | (mq[1] << 16) | (mq[2] << 8) | mq[3];
+      const uint32_t tot = lane_bcast_u32(wave_scan_add_u32(static_cast<uint32_t>(__builtin_popcount(mask))), kWave - 1);
+      if (tot <= static_cast<uint32_t>(cap)) break;
+    }
+    if (L < 0) mask = 0;
+  }
+
+  // candidates in index order, (chunk index << 32 | bits(x)); a candidate's
+  // value is picked among its vector's EPV registers
+  uint64_t* out = p.cands + (static_cast<int64_t>(I.row) * p.nch + I.chunk) * p.cap;
+  uint32_t nA = 0;
+  if (L >= 0) {
+    uint64_t packed = 0;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      const uint32_t vb = (mask >> (32 - (u + 1) * EPV)) & ((1u << EPV) - 1u);
+      packed |= static_cast<uint64_t>(__builtin_popcount(vb)) << (8 * u);
+    }
+    const uint64_t incl = wave_scan_add_u64(packed);
+    const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
+    const uint64_t excl = incl - packed;
+    uint32_t base = 0;
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) {
+      uint32_t vb = (mask >> (32 - (u + 1) * EPV)) & ((1u << EPV) - 1u);
+      uint32_t pos = base + static_cast<uint32_t>((excl >> (8 * u)) & 0xffu);
+      while (vb) {
+        const int e = __builtin_clz(vb) - (32 - EPV);
+        vb &= ~(1u << (EPV - 1 - e));
+        float xv = x[u * EPV];
+#pragma unroll
+        for (int q = 1; q < EPV; ++q) xv = e == q ? x[u * EPV + q] : xv;
+        const int li = (u * kWave + t) * EPV + e;
+        out[pos] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xv);
+        ++pos;
+      }
+      base += static_cast<uint32_t>((tot >> (8 * u)) & 0xffu);
+    }
+    nA = base;
+  }
+  const bool overflow = L < 0 && mc > -__builtin_inff();
+
+  // the row's draft token: element li of lane (li / EPV) mod 64
+  float xtok = 0.0f;
+  const bool has_tok = I.tok >= c0 && I.tok < c0 + nel;
+  if (has_tok) {
+    const int li = static_cast<int>(I.tok - c0);
+    const int r = (li / (EPV * kWave)) * EPV + li % EPV;  // register index, wave-uniform
+    float xv = x[0];
+#pragma unroll
+    for (int q = 1; q < NE; ++q) xv = r == q ? x[q] : xv;
+    xtok = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(xv), (li / EPV) & (kWave - 1)));
+  }
+
+  if (t == 0) {
+    ChunkRec* rec = p.recs + static_cast<int64_t>(I.row) * p.nch + I.chunk;
+    u32x4* r128 = reinterpret_cast<u32x4*>(rec);
+    const uint32_t flags = (overflow ? kChunkOverflow : 0u) | (has_tok ? kChunkHasTok : 0u);
+    r128[0] = u32x4{__float_as_uint(m), __float_as_uint(mass), __float_as_uint(-__builtin_inff()), 0u};
+    r128[1] = u32x4{static_cast<uint32_t>(overflow ? -1 : L), overflow ? 0u : nA, __float_as_uint(xtok), flags};
+  }
+}
+
 // ===========================================================================
 // stream_kernel: one (row, chunk) item per wave, four independent waves per
 // workgroup
@@ -749,6 +955,30 @@ __global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
   stream_item<DT, PEN>(p, sh, w, I, d, pw, hits[PEN ? w : 0]);
 }
 
+// Without a penalty: the register-only item, eight waves per SIMD.
+template <int DT>
+__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(8, 8))) void stream_reg_kernel(const Params p) {
+  constexpr int NVC = kChunk / (kWave * Elem<DT>::kPerVec);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int it = static_cast<int>(blockIdx.x) * kNW + w;
+  if (it >= p.items) return;
+  const Item I = item_of(p, it);
+  u32x4 d[NVC];
+  const int c0 = I.chunk * kChunk;
+  const u32x4* src = reinterpret_cast<const u32x4*>(I.rowp) + c0 / Elem<DT>::kPerVec;
+  const int t = threadIdx.x & (kWave - 1);
+  if (p.vocab - c0 >= kChunk) {
+    // a whole chunk: one lane address, the vectors at fixed offsets
+#pragma unroll
+    for (int u = 0; u < NVC; ++u) d[u] = __builtin_nontemporal_load(src + t + u * kWave);
+  } else {
+    uint32_t pw;
+    load_item<DT, NVC>(p, I, d, pw);
+  }
+  stream_item_reg<DT>(p, I, d);
+}
+
+
 // ===========================================================================
 // Finaliser: fin_kernel, one workgroup per unit
 // ===========================================================================
@@ -759,6 +989,7 @@ constexpr int kPosPT = kChunk / kFW;   // chunk positions per thread in a draw
 constexpr int kHash = 4096;            // draft-entry hash slots (at most half in use)
 constexpr int kSelBins = 2048;         // radix digits per select round (11 bits)
 constexpr int kSelPer = kSelBins / kFW;
+constexpr int kCoarse = kSelBins / (kWave / 2);  // coarse bins of 32 radix bins (one per lane)
 constexpr int kGather = kWave;         // a crossing bucket this small is finished by one wave
 
 struct RowAux {
@@ -785,6 +1016,7 @@ struct FinSh {
       float dv[kRowCap];         // and max(P - Q, 0)
     } res;
   } u;
+  uint64_t coarse[2][kCoarse];   // sums of 32 consecutive bins (zero between selects)
   uint32_t gbits[2][kGather];    // a select's crossing bucket: bits of p and masses
   uint64_t gw[2][kGather];
   uint32_t gcount[2];
@@ -1046,9 +1278,12 @@ __device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr,
     if ((hist >> s) & 1u) {
 #pragma unroll
       for (int q = 0; q < kEPT; ++q) {
-        if (ew[s][q] && (eb[s][q] >> 30) == 0u)
+        if (ew[s][q] && (eb[s][q] >> 30) == 0u) {
           __hip_atomic_fetch_add(&f.u.bins[s][eb[s][q] >> 19], ew[s][q], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_fetch_add(&f.coarse[s][eb[s][q] >> 24], ew[s][q], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
       }
     }
   }
@@ -1064,13 +1299,14 @@ __device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr,
 // masses; zero for an unused slot), any partition of the row's entries over
 // the threads. Radix rounds on the bits of p (p <= 1, so bits < 2^30): bits
 // 29..19, 18..8 and 7..0. In each round wave s alone finds row s's crossing
-// digit (lane l sums the 32 bins below kSelBins - 32 l, one wave scan finds
-// the lane and a second one the digit); the entries of that digit are then
-// gathered and, when at most kGather, finished by wave s, which also stores
-// the row's cutoff and retained mass in f.aux[s] (set[s]). ok[s] is false
+// digit (lane l reads the coarse sum of the 32 bins below kSelBins - 32 l,
+// which every mass added to a bin also went into; one wave scan finds the
+// lane and a second one, over those 32 bins, the digit); the entries of that
+// digit are then gathered and, when at most kGather, finished by wave s,
+// which also stores the row's cutoff and retained mass in f.aux[s] (set[s]). ok[s] is false
 // when the entries hold less than thr_s. Entries of zero mass never decide
 // the cutoff and are skipped. hist: round 0's masses are already in the bins
-// (which are otherwise cleared here first).
+// and coarse bins (which are otherwise cleared here first).
 __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const uint64_t (&thr)[2],
                                                const uint32_t (&eb)[2][kEPT], const uint64_t (&ew)[2][kEPT],
                                                bool hist, float (&cut)[2], uint64_t (&mass)[2],
@@ -1087,6 +1323,7 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
       if (live[s]) {
 #pragma unroll
         for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
+        if (t < kCoarse) f.coarse[s][t] = 0;
       }
     }
     __syncthreads();
@@ -1104,9 +1341,11 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
         if (!live[s]) continue;
 #pragma unroll
         for (int q = 0; q < kEPT; ++q) {
-          if (ew[s][q] && (eb[s][q] >> hshift) == prefix[s])
-            __hip_atomic_fetch_add(&f.u.bins[s][(eb[s][q] >> shift) & ((1u << width) - 1u)], ew[s][q],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (ew[s][q] && (eb[s][q] >> hshift) == prefix[s]) {
+            const uint32_t dg = (eb[s][q] >> shift) & ((1u << width) - 1u);
+            __hip_atomic_fetch_add(&f.u.bins[s][dg], ew[s][q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(&f.coarse[s][dg >> 5], ew[s][q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
         }
       }
       __syncthreads();
@@ -1115,12 +1354,8 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
     if (wid < 2 && live[wid]) {
       const int s = wid;
       const uint64_t* bs = f.u.bins[s];
-      const int lo = kSelBins - kWave / 2 * (lane + 1);  // this lane's lowest bin
-      // the lanes start at different bins, so one read of the wave touches
-      // every bank about evenly (32 bins per lane: lane stride 256 bytes)
-      uint64_t own = 0;
-#pragma unroll
-      for (int i = 0; i < kWave / 2; ++i) own += bs[lo + ((i + lane) & (kWave / 2 - 1))];
+      // lane l: the 32 bins below kSelBins - 32 l, whose sum is coarse[63 - l]
+      const uint64_t own = f.coarse[s][kCoarse - 1 - lane];
       const uint64_t incl = wave_scan_add_u64(own);
       const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
       const uint64_t need = thr[s] - above[s];  // > 0: above < thr
@@ -1168,6 +1403,7 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
       }
 #pragma unroll
       for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
+      if (t < kCoarse) f.coarse[s][t] = 0;
     }
     uint32_t gbase[2] = {0u, 0u};
     if (lane == 0) {
@@ -1856,6 +2092,10 @@ void fin_kernel(const Params p) {
     f.u.bins[0][kSelPer * t + q] = 0;
     f.u.bins[1][kSelPer * t + q] = 0;
   }
+  if (t < kCoarse) {
+    f.coarse[0][t] = 0;
+    f.coarse[1][t] = 0;
+  }
   if (w < nr) row_setup(p, f, w, rp, w == 0 ? tp0 : tp1);
   __syncthreads();
   // the filtered rows and their thresholds
@@ -2045,7 +2285,7 @@ void launch_dt(const Params& p, hipStream_t st) {
   if (p.use_pen) {
     hipLaunchKernelGGL((stream_kernel<DT, true>), sgrid, dim3(kWG), 0, st, p);
   } else {
-    hipLaunchKernelGGL((stream_kernel<DT, false>), sgrid, dim3(kWG), 0, st, p);
+    hipLaunchKernelGGL((stream_reg_kernel<DT>), sgrid, dim3(kWG), 0, st, p);
   }
   hipLaunchKernelGGL((fin_kernel<DT>), dim3(static_cast<unsigned>(p.units)), dim3(kFW), 0, st, p);
   if (p.mode == kModeDense && (p.probs_out || p.filt_out)) {
