@@ -991,6 +991,7 @@ constexpr int kSelBins = 2048;         // radix digits per select round (11 bits
 constexpr int kSelPer = kSelBins / kFW;
 constexpr int kCoarse = kSelBins / (kWave / 2);  // coarse bins of 32 radix bins (one per lane)
 constexpr int kGather = kWave;         // a crossing bucket this small is finished by one wave
+constexpr int kPackedUnits = 27;       // spec: up to this many units per batch element arrive with packed bits
 
 struct RowAux {
   float mcmax, s, cut, mass_f;   // cutoff (0 unfiltered), binary32 retained mass
@@ -2136,35 +2137,57 @@ void fin_kernel(const Params p) {
       if (!acc && (a1.flags & kRowList)) hash_support(f);
       token = acc ? xdraft : draw_residual<DT>(p, f, rows[0], rows[1], K[0], K[1], u_draw);
     }
-    // publish, then the last of the batch element's k+1 units writes the outputs
-    if (t == 0) {
-      store_sc64(p.words + static_cast<int64_t>(g) * (k + 1) + i,
-                 static_cast<uint64_t>(token) | (acc ? (1ull << 63) : 0ull));
-      drain_stores();
-      const uint32_t old = atomic_arrive(p.grp_cnt + g);
-      f.last = old == static_cast<uint32_t>(k) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (f.last && t < kWave) {
-      // accepted length: the first rejected position (k if none), 64 positions per pass
-      const uint64_t* wg = p.words + static_cast<int64_t>(g) * (k + 1);
-      int a = k;
-      for (int b0 = 0; b0 < k && a == k; b0 += kWave) {
-        const int pos = b0 + t;
-        const uint64_t wd = pos < k ? load_sc64(wg + pos) : (1ull << 63);
-        const uint64_t rej = __ballot(!(wd >> 63));
-        if (rej) a = b0 + __builtin_ctzll(rej);
-      }
-      for (int b0 = 0; b0 <= k; b0 += kWave) {
-        const int pos = b0 + t;
-        if (pos <= k) {
-          const int64_t tokv = pos <= a ? static_cast<int64_t>(load_sc64(wg + pos) & 0x7fffffffffffffffull) : -1;
-          p.tokens[static_cast<int64_t>(g) * (k + 1) + pos] = tokv;
+    // publish, then the last of the batch element's k+1 units completes the
+    // outputs
+    int64_t* tg = p.tokens + static_cast<int64_t>(g) * (k + 1);
+    if (k + 1 <= kPackedUnits) {
+      // each unit stores its token where it belongs and arrives with its
+      // rejection bit (bits 0..4 count the arrivals, bit 5 + i is position
+      // i's rejection): the last arrival holds every bit and only replaces
+      // the positions after the first rejection by -1
+      if (t == 0) {
+        store_sc64(reinterpret_cast<uint64_t*>(tg + i), static_cast<uint64_t>(token));
+        drain_stores();
+        const uint32_t mine = 1u + (acc || i == k ? 0u : 1u << (5 + i));
+        const uint32_t old = atomic_add_u32(p.grp_cnt + g, mine);
+        if ((old & 31u) == static_cast<uint32_t>(k)) {
+          const uint32_t rej = (old + mine) >> 5;
+          const int a = rej ? __builtin_ctz(rej) : k;
+          for (int pos = a + 1; pos <= k; ++pos) store_sc64(reinterpret_cast<uint64_t*>(tg + pos), ~0ull);
+          p.accept_len[g] = a;
+          atomic_store_u32(p.grp_cnt + g, 0u);
         }
       }
+    } else {
       if (t == 0) {
-        p.accept_len[g] = a;
-        atomic_store_u32(p.grp_cnt + g, 0u);
+        store_sc64(p.words + static_cast<int64_t>(g) * (k + 1) + i,
+                   static_cast<uint64_t>(token) | (acc ? (1ull << 63) : 0ull));
+        drain_stores();
+        const uint32_t old = atomic_arrive(p.grp_cnt + g);
+        f.last = old == static_cast<uint32_t>(k) ? 1u : 0u;
+      }
+      __syncthreads();
+      if (f.last && t < kWave) {
+        // accepted length: the first rejected position (k if none), 64 positions per pass
+        const uint64_t* wg = p.words + static_cast<int64_t>(g) * (k + 1);
+        int a = k;
+        for (int b0 = 0; b0 < k && a == k; b0 += kWave) {
+          const int pos = b0 + t;
+          const uint64_t wd = pos < k ? load_sc64(wg + pos) : (1ull << 63);
+          const uint64_t rej = __ballot(!(wd >> 63));
+          if (rej) a = b0 + __builtin_ctzll(rej);
+        }
+        for (int b0 = 0; b0 <= k; b0 += kWave) {
+          const int pos = b0 + t;
+          if (pos <= k) {
+            const int64_t tokv = pos <= a ? static_cast<int64_t>(load_sc64(wg + pos) & 0x7fffffffffffffffull) : -1;
+            tg[pos] = tokv;
+          }
+        }
+        if (t == 0) {
+          p.accept_len[g] = a;
+          atomic_store_u32(p.grp_cnt + g, 0u);
+        }
       }
     }
   } else if (p.mode == kModeSample) {

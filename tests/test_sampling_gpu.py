@@ -445,6 +445,8 @@ def test_spec_verify_large_draft_supports(gpu, support):
 
 @pytest.mark.parametrize("batch,k,vocab,dtype,top_p", [
     (1, 64, 4096, torch.float32, 0.8),        # the largest k: 65 draws per element
+    (2, 26, 4096, torch.float32, 0.8),        # 27 units: the last arrival's bits hold every rejection
+    (2, 27, 4096, torch.float32, 0.8),        # 28 units: published words read back instead
     (2, 1, 262144, torch.bfloat16, 0.9),      # the largest vocabulary: 128 chunks, 16 slots each
     (2, 2, 5000, torch.float32, 0.7),         # a partial last chunk
     (3, 3, 32000, torch.float16, 0.5),
