@@ -987,9 +987,6 @@ constexpr int kFNW = kFW / kWave;
 constexpr int kEPT = kRowCap / kFW;    // entries (and candidate slots) of one row per thread
 constexpr int kPosPT = kChunk / kFW;   // chunk positions per thread in a draw
 constexpr int kHash = 4096;            // draft-entry hash slots (at most half in use)
-constexpr int kSelBins = 2048;         // radix digits per select round (11 bits)
-constexpr int kSelPer = kSelBins / kFW;
-constexpr int kCoarse = kSelBins / (kWave / 2);  // coarse bins of 32 radix bins (one per lane)
 constexpr int kGather = kWave;         // a crossing bucket this small is finished by one wave
 constexpr int kPackedUnits = 27;       // spec: up to this many units per batch element arrive with packed bits
 
@@ -1005,9 +1002,16 @@ struct RowAux {
   float top_p;
 };
 
-struct FinSh {
+// SB: bits per select digit; rounds on bits 29 .. 30 - SB, then the next SB
+// bits, then the rest (11: 29..19, 18..8, 7..0; 10: 29..20, 19..10, 9..0).
+template <int SB>
+struct FinShT {
+  static constexpr int kBits = SB;
+  static constexpr int kBins = 1 << SB;         // radix digits per select round
+  static constexpr int kPer = kBins / kFW;      // bins cleared per thread
+  static constexpr int kCo = kBins / (kWave / 2);  // coarse bins of 32 radix bins (one per lane)
   union {
-    uint64_t bins[2][kSelBins];  // radix bins of the unit's two rows (zero between selects)
+    uint64_t bins[2][kBins];     // radix bins of the unit's two rows (zero between selects)
     uint64_t pos[kChunk];        // a draw's weights by position in the chosen chunk
     struct {
       uint64_t cum[kRowCap];     // a draw's exclusive prefix masses by entry
@@ -1017,7 +1021,7 @@ struct FinSh {
       float dv[kRowCap];         // and max(P - Q, 0)
     } res;
   } u;
-  uint64_t coarse[2][kCoarse];   // sums of 32 consecutive bins (zero between selects)
+  uint64_t coarse[2][kCo];       // sums of 32 consecutive bins (zero between selects)
   uint32_t gbits[2][kGather];    // a select's crossing bucket: bits of p and masses
   uint64_t gw[2][kGather];
   uint32_t gcount[2];
@@ -1043,6 +1047,8 @@ struct FinSh {
   uint32_t last;                 // spec: this unit completes its batch element
   int64_t token;
 };
+
+static_assert(sizeof(FinShT<10>) <= 80 * 1024, "two finaliser workgroups per CU");
 
 // Lanes below this one whose bit is set in a wave mask.
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
@@ -1100,7 +1106,8 @@ __device__ __forceinline__ void block_sum2(uint64_t a, uint64_t b, uint64_t* red
 static_assert(kHash == 4096 && kRowCap <= kHash / 2, "hash size");
 __device__ __forceinline__ uint32_t hash_slot(uint32_t x) { return (x * 2654435761u) >> 20; }
 
-__device__ __forceinline__ void hash_insert(FinSh& f, uint32_t x, uint32_t e) {
+template <class FS>
+__device__ __forceinline__ void hash_insert(FS& f, uint32_t x, uint32_t e) {
   uint32_t h = hash_slot(x);
   for (int probe = 0; probe < kHash; ++probe) {
     if (atomicCAS(&f.hash[h], 0u, e + 1u) == 0u) return;
@@ -1109,7 +1116,8 @@ __device__ __forceinline__ void hash_insert(FinSh& f, uint32_t x, uint32_t e) {
 }
 
 // The entry of slot 1 holding vocabulary index x, or kNone.
-__device__ __forceinline__ uint32_t hash_find(const FinSh& f, uint32_t x) {
+template <class FS>
+__device__ __forceinline__ uint32_t hash_find(const FS& f, uint32_t x) {
   uint32_t h = hash_slot(x);
   for (int probe = 0; probe < kHash; ++probe) {
     const uint32_t v = f.hash[h];
@@ -1122,7 +1130,8 @@ __device__ __forceinline__ uint32_t hash_find(const FinSh& f, uint32_t x) {
 
 // Builds the hash over slot 1's support entries (p >= its cutoff): the only
 // ones whose filtered probability is not zero. The hash is zero on entry.
-__device__ __forceinline__ void hash_support(FinSh& f) {
+template <class FS>
+__device__ __forceinline__ void hash_support(FS& f) {
   const uint32_t n = f.aux[1].n;
   const float cut = f.aux[1].cut;
   for (uint32_t e = threadIdx.x; e < n; e += kFW) {
@@ -1159,7 +1168,8 @@ __device__ __forceinline__ RecPair load_recs(const Params& p, int row) {
 }
 
 // Row constants and per-chunk data of row slot s from its records (wave s).
-__device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, const RecPair& rp, float top_p) {
+template <class FS>
+__device__ __forceinline__ void row_setup(const Params& p, FS& f, int s, const RecPair& rp, float top_p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int nch = p.nch;
   const float c = p.c;
@@ -1246,9 +1256,10 @@ __device__ __forceinline__ void row_setup(const Params& p, FinSh& f, int s, cons
 // were known, placed into the LDS entries when the record's count covers
 // them: entry cstart + k holds (bits of p, vocabulary index). The bits of p
 // and their masses stay in eb / ew (zero for an unused slot); the rows in
-// `hist` add their masses to the bins of the first select round (bits 29..19
-// of p), which are zero on entry.
-__device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr, const uint64_t (&sl)[2][kEPT],
+// `hist` add their masses to the bins of the first select round (bits 29..20
+// of p) and to their coarse sums, which are zero on entry.
+template <class FS>
+__device__ __forceinline__ void place_entries(const Params& p, FS& f, int nr, const uint64_t (&sl)[2][kEPT],
                                               uint32_t hist, uint32_t (&eb)[2][kEPT], uint64_t (&ew)[2][kEPT]) {
   const int t = threadIdx.x;
   const int nslot = p.nch * p.cap;
@@ -1280,9 +1291,9 @@ __device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr,
 #pragma unroll
       for (int q = 0; q < kEPT; ++q) {
         if (ew[s][q] && (eb[s][q] >> 30) == 0u) {
-          __hip_atomic_fetch_add(&f.u.bins[s][eb[s][q] >> 19], ew[s][q], __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(&f.u.bins[s][eb[s][q] >> (30 - FS::kBits)], ew[s][q], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-          __hip_atomic_fetch_add(&f.coarse[s][eb[s][q] >> 24], ew[s][q], __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(&f.coarse[s][eb[s][q] >> (35 - FS::kBits)], ew[s][q], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       }
@@ -1299,8 +1310,8 @@ __device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr,
 // thread holds kEPT entries of each row in registers (eb: bits of p, ew: their
 // masses; zero for an unused slot), any partition of the row's entries over
 // the threads. Radix rounds on the bits of p (p <= 1, so bits < 2^30): bits
-// 29..19, 18..8 and 7..0. In each round wave s alone finds row s's crossing
-// digit (lane l reads the coarse sum of the 32 bins below kSelBins - 32 l,
+// 29..20, 19..10 and 9..0. In each round wave s alone finds row s's crossing
+// digit (lane l < 32 reads the coarse sum of the 32 bins below FS::kBins - 32 l,
 // which every mass added to a bin also went into; one wave scan finds the
 // lane and a second one, over those 32 bins, the digit); the entries of that
 // digit are then gathered and, when at most kGather, finished by wave s,
@@ -1308,7 +1319,8 @@ __device__ __forceinline__ void place_entries(const Params& p, FinSh& f, int nr,
 // when the entries hold less than thr_s. Entries of zero mass never decide
 // the cutoff and are skipped. hist: round 0's masses are already in the bins
 // and coarse bins (which are otherwise cleared here first).
-__device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const uint64_t (&thr)[2],
+template <class FS>
+__device__ __forceinline__ void select_entries(FS& f, uint32_t mask, const uint64_t (&thr)[2],
                                                const uint32_t (&eb)[2][kEPT], const uint64_t (&ew)[2][kEPT],
                                                bool hist, float (&cut)[2], uint64_t (&mass)[2],
                                                bool (&ok)[2], bool (&set)[2]) {
@@ -1323,8 +1335,8 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
     for (int s = 0; s < 2; ++s) {
       if (live[s]) {
 #pragma unroll
-        for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
-        if (t < kCoarse) f.coarse[s][t] = 0;
+        for (int q = 0; q < FS::kPer; ++q) f.u.bins[s][FS::kPer * t + q] = 0;
+        if (t < FS::kCo) f.coarse[s][t] = 0;
       }
     }
     __syncthreads();
@@ -1332,8 +1344,8 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
   uint32_t prefix[2] = {0u, 0u};  // the resolved high bits: bits >> hshift
   uint64_t above[2] = {0u, 0u};   // mass strictly above the resolved prefix
   for (int round = 0; round < 3 && (live[0] || live[1]); ++round) {
-    const int shift = round == 0 ? 19 : (round == 1 ? 8 : 0);
-    const int width = round == 2 ? 8 : 11;
+    const int shift = round == 0 ? 30 - FS::kBits : (round == 1 ? 30 - 2 * FS::kBits : 0);
+    const int width = round == 2 ? 30 - 2 * FS::kBits : FS::kBits;
     const int hshift = shift + width;
     // 1. masses into the bins of this round's digit
     if (round > 0 || !hist) {
@@ -1355,8 +1367,9 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
     if (wid < 2 && live[wid]) {
       const int s = wid;
       const uint64_t* bs = f.u.bins[s];
-      // lane l: the 32 bins below kSelBins - 32 l, whose sum is coarse[63 - l]
-      const uint64_t own = f.coarse[s][kCoarse - 1 - lane];
+      // lane l < FS::kCo: the 32 bins below FS::kBins - 32 l, whose sum is
+      // coarse[FS::kCo - 1 - l]
+      const uint64_t own = lane < FS::kCo ? f.coarse[s][FS::kCo - 1 - lane] : 0u;
       const uint64_t incl = wave_scan_add_u64(own);
       const uint64_t tot = lane_bcast_u64(incl, kWave - 1);
       const uint64_t need = thr[s] - above[s];  // > 0: above < thr
@@ -1365,7 +1378,7 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
       } else {
         const int c = __builtin_ctzll(__ballot(incl >= need));
         const uint64_t before = lane_bcast_u64(incl - own, c);
-        const int bin = kSelBins - 1 - kWave / 2 * c - lane;
+        const int bin = FS::kBins - 1 - kWave / 2 * c - lane;
         const uint64_t v = lane < kWave / 2 ? bs[bin] : 0u;
         const uint64_t inc2 = wave_scan_add_u64(v);
         const int d = __builtin_ctzll(__ballot(lane < kWave / 2 && before + inc2 >= need));
@@ -1403,8 +1416,8 @@ __device__ __forceinline__ void select_entries(FinSh& f, uint32_t mask, const ui
         gcnt[s] += static_cast<uint32_t>(__builtin_popcountll(gm[s][q]));
       }
 #pragma unroll
-      for (int q = 0; q < kSelPer; ++q) f.u.bins[s][kSelPer * t + q] = 0;
-      if (t < kCoarse) f.coarse[s][t] = 0;
+      for (int q = 0; q < FS::kPer; ++q) f.u.bins[s][FS::kPer * t + q] = 0;
+      if (t < FS::kCo) f.coarse[s][t] = 0;
     }
     uint32_t gbase[2] = {0u, 0u};
     if (lane == 0) {
@@ -1509,8 +1522,8 @@ __device__ __forceinline__ void row_pass(const Params& p, const char* rowp, cons
 }
 
 // Whole-row exact cutoff by three radix passes over the row (slow path).
-template <int DT>
-__device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, const RowK& K, uint64_t thr, float* cut, uint64_t* mass) {
+template <int DT, class FS>
+__device__ __forceinline__ bool select_row(const Params& p, FS& f, int row, const RowK& K, uint64_t thr, float* cut, uint64_t* mass) {
   const int t = threadIdx.x;
   const char* rowp = row_ptr(p, row);
   const uint32_t* bm = row_bitmap(p, row);
@@ -1583,8 +1596,8 @@ __device__ __forceinline__ bool select_row(const Params& p, FinSh& f, int row, c
 
 // Appends the elements of chunk j with p >= cut to slot s's entries, in
 // index order, as the chunk's new range. Returns false if they do not fit.
-template <int DT>
-__device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, int row, const RowK& K, int j, float cut) {
+template <int DT, class FS>
+__device__ __forceinline__ bool refill_chunk(const Params& p, FS& f, int s, int row, const RowK& K, int j, float cut) {
   constexpr int EPV = Elem<DT>::kPerVec;
   // elements per thread, contiguous, whole vectors (threads past the chunk idle)
   constexpr int EPT = kChunk / kFW > EPV ? kChunk / kFW : EPV;
@@ -1649,8 +1662,8 @@ __device__ __forceinline__ bool refill_chunk(const Params& p, FinSh& f, int s, i
 
 // Collects the whole support {p >= cut} of a row into slot s's entries,
 // chunk by chunk (slow path); false if it does not fit.
-template <int DT>
-__device__ __forceinline__ bool collect_support(const Params& p, FinSh& f, int s, int row, const RowK& K, float cut) {
+template <int DT, class FS>
+__device__ __forceinline__ bool collect_support(const Params& p, FS& f, int s, int row, const RowK& K, float cut) {
   if (threadIdx.x == 0) f.aux[s].n = 0;
   __syncthreads();
   for (int j = 0; j < p.nch; ++j) {
@@ -1669,8 +1682,8 @@ __device__ __forceinline__ bool collect_support(const Params& p, FinSh& f, int s
 // row). The rows in `mask` are filtered (thr: their thresholds); their first
 // selects share their rounds, over the entries in eb / ew, whose first-round
 // masses are in the bins already. Unfiltered rows keep row_setup's state.
-template <int DT>
-__device__ __forceinline__ void resolve_rows(const Params& p, FinSh& f, int nr, const int (&rows)[2], const RowK (&K)[2],
+template <int DT, class FS>
+__device__ __forceinline__ void resolve_rows(const Params& p, FS& f, int nr, const int (&rows)[2], const RowK (&K)[2],
                                             uint32_t mask, const uint64_t (&thr)[2], const uint32_t (&eb)[2][kEPT],
                                             const uint64_t (&ew)[2][kEPT]) {
   float cut[2] = {0.0f, 0.0f};
@@ -1751,7 +1764,8 @@ __device__ __forceinline__ float filtered_of(const RowAux& a, float pv) {
 // Chunk j* holding the target, from f.csum: lane l of wave 0 holds chunks
 // 2l and 2l+1. Writes f.pick_rem = target - mass before j*, f.pick = j*
 // (kNone at zero total). Ends with a barrier.
-__device__ __forceinline__ void pick_chunk(const Params& p, FinSh& f, float u) {
+template <class FS>
+__device__ __forceinline__ void pick_chunk(const Params& p, FS& f, float u) {
   const int t = threadIdx.x;
   if (t < kWave) {
     const int ja = 2 * t, jb = ja + 1;
@@ -1779,7 +1793,8 @@ __device__ __forceinline__ void pick_chunk(const Params& p, FinSh& f, float u) {
 // Within a chunk of 2048 positions: thread t owns positions kPosPT t .. +
 // kPosPT - 1 with weights w; the first position whose inclusive mass exceeds
 // `rem` (the target minus the mass before the chunk) goes to f.token as c0 + pos.
-__device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64_t (&w)[kPosPT], uint64_t rem) {
+template <class FS>
+__device__ __forceinline__ void pick_in_chunk(FS& f, int64_t c0, const uint64_t (&w)[kPosPT], uint64_t rem) {
   const int t = threadIdx.x;
   uint64_t own = 0;
 #pragma unroll
@@ -1808,7 +1823,8 @@ __device__ __forceinline__ void pick_in_chunk(FinSh& f, int64_t c0, const uint64
 // order; otherwise (per-chunk sums find the chunk when not `ordered`) the
 // chunk's entries are scattered to their positions (indices are distinct
 // among entries of nonzero weight) and scanned there.
-__device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const uint64_t (&wl)[kEPT], float u,
+template <class FS>
+__device__ __forceinline__ int64_t draw_list(const Params& p, FS& f, const uint64_t (&wl)[kEPT], float u,
                                              bool ordered) {
   const int t = threadIdx.x;
   const uint32_t n = f.aux[0].n;
@@ -1878,8 +1894,8 @@ __device__ __forceinline__ int64_t draw_list(const Params& p, FinSh& f, const ui
 }
 
 // Dense-mode draw over the whole vocabulary with weights wfn(i) (slow path).
-template <int DT, typename WFn>
-__device__ __forceinline__ int64_t draw_dense(const Params& p, FinSh& f, const char* rowp, const uint32_t* bm, float u, WFn wfn) {
+template <int DT, typename WFn, class FS>
+__device__ __forceinline__ int64_t draw_dense(const Params& p, FS& f, const char* rowp, const uint32_t* bm, float u, WFn wfn) {
   const int t = threadIdx.x;
   for (int j = t; j < p.nch; j += kFW) f.csum[j] = 0;
   if (t == 0) f.token = 0;
@@ -1904,8 +1920,8 @@ __device__ __forceinline__ int64_t draw_dense(const Params& p, FinSh& f, const c
 }
 
 // Filtered draft probability Q at vocabulary index x (slot 1).
-template <int DT>
-__device__ __forceinline__ float q_at(const Params& p, const FinSh& f, const RowK& K1, int row1, uint32_t x) {
+template <int DT, class FS>
+__device__ __forceinline__ float q_at(const Params& p, const FS& f, const RowK& K1, int row1, uint32_t x) {
   const RowAux& a = f.aux[1];
   if (a.flags & kRowEmpty) return 0.0f;
   if (a.flags & kRowList) {
@@ -1917,8 +1933,8 @@ __device__ __forceinline__ float q_at(const Params& p, const FinSh& f, const Row
 }
 
 // Draw from slot 0's filtered distribution P (bonus / sample).
-template <int DT>
-__device__ __forceinline__ int64_t draw_target(const Params& p, FinSh& f, int row0, const RowK& K0, float u) {
+template <int DT, class FS>
+__device__ __forceinline__ int64_t draw_target(const Params& p, FS& f, int row0, const RowK& K0, float u) {
   const RowAux& a = f.aux[0];
   if (a.flags & kRowList) {
     uint64_t wl[kEPT];
@@ -1936,8 +1952,8 @@ __device__ __forceinline__ int64_t draw_target(const Params& p, FinSh& f, int ro
 
 // Residual draw at a rejected position: normalize(max(P - Q, 0)), falling
 // back to normalize(P) at zero mass (rejection.py:60-69).
-template <int DT>
-__device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int row0, int row1, const RowK& K0, const RowK& K1,
+template <int DT, class FS>
+__device__ __forceinline__ int64_t draw_residual(const Params& p, FS& f, int row0, int row1, const RowK& K0, const RowK& K1,
                                  float u) {
   const int t = threadIdx.x;
   const RowAux& a = f.aux[0];
@@ -2031,10 +2047,8 @@ __device__ __forceinline__ int64_t draw_residual(const Params& p, FinSh& f, int 
 // ---------------------------------------------------------------------------
 // fin_kernel: unit blockIdx.x, after stream_kernel wrote every record
 // ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(kFW) __attribute__((amdgpu_flat_work_group_size(kFW, kFW)))
-void fin_kernel(const Params p) {
-  __shared__ FinSh f;
+template <int DT, class FS>
+__device__ __forceinline__ void fin_unit(const Params& p, FS& f) {
   const int t = threadIdx.x, w = t / kWave;
   const int unit = blockIdx.x;
   int g, i, nr;
@@ -2089,11 +2103,11 @@ void fin_kernel(const Params p) {
     for (int h = t; h < kHash; h += kFW) f.hash[h] = 0u;
   }
 #pragma unroll
-  for (int q = 0; q < kSelPer; ++q) {
-    f.u.bins[0][kSelPer * t + q] = 0;
-    f.u.bins[1][kSelPer * t + q] = 0;
+  for (int q = 0; q < FS::kPer; ++q) {
+    f.u.bins[0][FS::kPer * t + q] = 0;
+    f.u.bins[1][FS::kPer * t + q] = 0;
   }
-  if (t < kCoarse) {
+  if (t < FS::kCo) {
     f.coarse[0][t] = 0;
     f.coarse[1][t] = 0;
   }
@@ -2211,6 +2225,23 @@ void fin_kernel(const Params p) {
     }
   }
 }
+
+// One workgroup per CU when every unit has a CU of its own.
+template <int DT>
+__global__ __launch_bounds__(kFW) __attribute__((amdgpu_flat_work_group_size(kFW, kFW)))
+void fin_kernel(const Params p) {
+  __shared__ FinShT<11> f;
+  fin_unit<DT>(p, f);
+}
+
+// Two workgroups per CU (the LDS is under 80 KB; at most 128 registers) for
+// calls with more units than CUs: one round instead of two.
+template <int DT>
+__global__ __launch_bounds__(kFW) __attribute__((amdgpu_flat_work_group_size(kFW, kFW), amdgpu_waves_per_eu(4, 4)))
+void fin2_kernel(const Params p) {
+  __shared__ FinShT<10> f;
+  fin_unit<DT>(p, f);
+}
 // ===========================================================================
 // dense_kernel: p and the filtered distribution for one (row, chunk) item
 // ===========================================================================
@@ -2310,7 +2341,11 @@ void launch_dt(const Params& p, hipStream_t st) {
   } else {
     hipLaunchKernelGGL((stream_reg_kernel<DT>), sgrid, dim3(kWG), 0, st, p);
   }
-  hipLaunchKernelGGL((fin_kernel<DT>), dim3(static_cast<unsigned>(p.units)), dim3(kFW), 0, st, p);
+  if (p.units > device_cu_count()) {
+    hipLaunchKernelGGL((fin2_kernel<DT>), dim3(static_cast<unsigned>(p.units)), dim3(kFW), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((fin_kernel<DT>), dim3(static_cast<unsigned>(p.units)), dim3(kFW), 0, st, p);
+  }
   if (p.mode == kModeDense && (p.probs_out || p.filt_out)) {
     hipLaunchKernelGGL((dense_kernel<DT>), dim3(static_cast<unsigned>(p.items)), dim3(kCB), 0, st, p);
   }
