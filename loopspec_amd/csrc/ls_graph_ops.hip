@@ -225,21 +225,36 @@ __global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
 
 // One workgroup per (token, group of planes): copy the token's row of every
 // plane in the group from its branch slot to its destination slot.
+constexpr int kKvPlanesPerWG = 8;  // planes one kv_copy workgroup moves
+
+// Every load of a thread is issued before any of its stores: the source and
+// destination share one buffer, so stores interleaved with the loads would
+// keep the compiler from moving the next load ahead of them (one memory
+// round trip per plane). The two rows of a plane are different token slots.
 __global__ __launch_bounds__(kCopyBlock) void kv_copy_kernel(char* __restrict__ kv, int64_t planes,
                                                              int64_t plane_stride, int64_t token_bytes,
                                                              int64_t num_slots, const int64_t* __restrict__ src_slots,
-                                                             const int64_t* __restrict__ dst_slots, int planes_per_wg) {
+                                                             const int64_t* __restrict__ dst_slots) {
   const int64_t tok = blockIdx.y;
   const int64_t d = dst_slots[tok];
   const int64_t s = src_slots[tok];
-  if (d < 0 || d >= num_slots || s < 0 || s >= num_slots) return;
-  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * planes_per_wg;
-  const int64_t p1 = p0 + planes_per_wg < planes ? p0 + planes_per_wg : planes;
+  if (d < 0 || d >= num_slots || s < 0 || s >= num_slots || d == s) return;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kKvPlanesPerWG;
+  const int np = planes - p0 < kKvPlanesPerWG ? static_cast<int>(planes - p0) : kKvPlanesPerWG;
   const int64_t vecs = token_bytes / 16;
-  for (int64_t p = p0; p < p1; ++p) {
-    const u32x4* from = reinterpret_cast<const u32x4*>(kv + p * plane_stride + s * token_bytes);
-    u32x4* to = reinterpret_cast<u32x4*>(kv + p * plane_stride + d * token_bytes);
-    for (int64_t v = threadIdx.x; v < vecs; v += kCopyBlock) __builtin_nontemporal_store(__builtin_nontemporal_load(from + v), to + v);
+  for (int64_t v = threadIdx.x; v < vecs; v += kCopyBlock) {
+    const u32x4* from = reinterpret_cast<const u32x4*>(kv + p0 * plane_stride + s * token_bytes) + v;
+    u32x4* to = reinterpret_cast<u32x4*>(kv + p0 * plane_stride + d * token_bytes) + v;
+    const int64_t pv = plane_stride / 16;
+    u32x4 buf[kKvPlanesPerWG];
+#pragma unroll
+    for (int q = 0; q < kKvPlanesPerWG; ++q) {
+      if (q < np) buf[q] = __builtin_nontemporal_load(from + q * pv);
+    }
+#pragma unroll
+    for (int q = 0; q < kKvPlanesPerWG; ++q) {
+      if (q < np) __builtin_nontemporal_store(buf[q], to + q * pv);
+    }
   }
 }
 
@@ -528,11 +543,10 @@ int ls_kv_commit(void* kv, int64_t planes, int64_t plane_stride_bytes, int64_t t
                      page_state, dst_slots, status);
   int rc = check_launch("kv_commit plan launch");
   if (rc || planes == 0) return rc;
-  const int ppw = 8;
-  const int64_t gx = (planes + ppw - 1) / ppw;
+  const int64_t gx = (planes + kKvPlanesPerWG - 1) / kKvPlanesPerWG;
   hipLaunchKernelGGL(kv_copy_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(batch * k)),
                      dim3(kCopyBlock), 0, st, static_cast<char*>(kv), planes, plane_stride_bytes, token_bytes,
-                     num_pages * page_size, branch_slots, dst_slots, ppw);
+                     num_pages * page_size, branch_slots, dst_slots);
   return check_launch("kv_commit copy launch");
 }
 
