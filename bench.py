@@ -329,7 +329,7 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
         "config": {"workload": cfg.name, "batch": cfg.batch, "k": cfg.k, "vocab": cfg.vocab,
                    "temperature": cfg.temperature, "top_p": cfg.top_p, "penalty": cfg.penalty,
                    "input_sets": nsets, "input_set_bytes": nbytes,
-                   "kernels": ("ls::bitmap_kernel + ls::stream_kernel<DT, true>" if cfg.penalty != 1.0
+                   "kernels": ("ls::bitmap_kernel + ls::stream_kernel<DT>" if cfg.penalty != 1.0
                                else "ls::stream_reg_kernel<DT>") + " + ls::fin_kernel<DT>",
                    "submission": "hipGraph of one ls_spec_verify call (%d launches) per step"
                    % (3 if cfg.penalty != 1.0 else 2)},

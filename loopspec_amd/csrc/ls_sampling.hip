@@ -1,12 +1,13 @@
 // (a) logit processing and (c) lossless speculative sampling for gfx950.
 //
-// Launches per call: bitmap_kernel (with a repetition penalty: each batch
-// element's token history as a vocabulary bitmap), stream_kernel, fin_kernel,
-// then, for dense outputs only, dense_kernel.
+// Launches per call: with a repetition penalty bitmap_kernel (each batch
+// element's token history as a vocabulary bitmap) and stream_kernel, without
+// one stream_reg_kernel; then fin_kernel (fin2_kernel when the units
+// outnumber the CUs); then, for dense outputs only, dense_kernel.
 //
-// stream_kernel reads every logit once: one wave per (row, 2048-element
-// chunk) item, four independent waves per workgroup (stream_reg_kernel
-// without a penalty: the chunk held in registers only). A wave
+// The stream kernels read every logit once: one wave per (row, 2048-element
+// chunk) item, four independent waves per workgroup (stream_reg_kernel holds
+// the chunk in registers only; stream_kernel stages it in LDS). A wave
 //   * stages its chunk in LDS, decodes it, sets penalised tokens aside;
 //   * computes the chunk max m_j, e = exp2m(fma(x, c, -mc_j)) and the chunk
 //     mass M_j in the declared pairwise order; the penalised tokens' own max
@@ -419,7 +420,7 @@ __device__ __forceinline__ uint32_t list_hits(const uint32_t (&hb)[NVC], uint16_
   return base;
 }
 
-template <int DT, bool PEN>
+template <int DT>
 __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, int w, const Item& I,
                                             const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4], uint32_t pw,
                                             uint16_t* hl) {
@@ -443,21 +444,16 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   //    bitmap words, which lane t loaded as word t)
   uint32_t hb[NVC];
   bool any_hit = false;
-  if constexpr (PEN) {
 #pragma unroll
-    for (int u = 0; u < NVC; ++u) {
-      const int i0 = (u * kWave + t) * EPV;
-      const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), i0 >> 5));
-      hb[u] = (u * kWave + t < nvc) ? (word >> (i0 & 31)) & ((1u << EPV) - 1u) : 0u;
-    }
-    uint32_t a = 0;
-#pragma unroll
-    for (int u = 0; u < NVC; ++u) a |= hb[u];
-    any_hit = __ballot(a != 0) != 0;
-  } else {
-#pragma unroll
-    for (int u = 0; u < NVC; ++u) hb[u] = 0;
+  for (int u = 0; u < NVC; ++u) {
+    const int i0 = (u * kWave + t) * EPV;
+    const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), i0 >> 5));
+    hb[u] = (u * kWave + t < nvc) ? (word >> (i0 & 31)) & ((1u << EPV) - 1u) : 0u;
   }
+  uint32_t a = 0;
+#pragma unroll
+  for (int u = 0; u < NVC; ++u) a |= hb[u];
+  any_hit = __ballot(a != 0) != 0;
 
   // 3. decoded logits, penalised ones and lanes past the row end at -inf
   float x[NE];
@@ -466,9 +462,7 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       float v = vec_elem<DT>(d[u], e);
-      if constexpr (PEN) {
-        if ((hb[u] >> e) & 1u) v = -__builtin_inff();
-      }
+      if ((hb[u] >> e) & 1u) v = -__builtin_inff();
       x[u * EPV + e] = v;
     }
   }
@@ -518,20 +512,18 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   float pm = -__builtin_inff();
   uint32_t nh = 0;
   float xp0 = -__builtin_inff();  // the penalised value of hit t
-  if constexpr (PEN) {
-    if (any_hit) {
-      nh = list_hits<EPV, NVC>(hb, hl);
-      float lm = -__builtin_inff();
-      for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
-        const uint32_t h = h0 + t;
-        if (h < nh) {
-          const float xp = penalise(staged<DT>(st, hl[h]), p.pen);
-          if (h0 == 0) xp0 = xp;
-          lm = xp > lm ? xp : lm;
-        }
+  if (any_hit) {
+    nh = list_hits<EPV, NVC>(hb, hl);
+    float lm = -__builtin_inff();
+    for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+      const uint32_t h = h0 + t;
+      if (h < nh) {
+        const float xp = penalise(staged<DT>(st, hl[h]), p.pen);
+        if (h0 == 0) xp0 = xp;
+        lm = xp > lm ? xp : lm;
       }
-      pm = wave_max_f32(lm);
     }
+    pm = wave_max_f32(lm);
   }
   const float pmc = pm * c;
 
@@ -542,22 +534,10 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   for (int i = 0; i < NE; ++i) x[i] = __builtin_fmaf(x[i], c, nmc);
   float ea[NE];
   float mass;
-  if constexpr (PEN) {
-    // penalised elements sit at -inf: the clamped form
+  // penalised elements sit at -inf: the clamped form
 #pragma unroll
-    for (int i = 0; i < NE; ++i) ea[i] = exp2q(x[i]);
-    mass = wave_tree_sum(lane_tree_sum(ea));
-  } else {
-#pragma unroll
-    for (int i = 0; i < NE; ++i) ea[i] = exp2q_finite(x[i]);
-    mass = wave_tree_sum(lane_tree_sum(ea));
-    if (mass != mass) {
-      // an infinite logit, or past-the-end lanes: the clamped form
-#pragma unroll
-      for (int i = 0; i < NE; ++i) ea[i] = exp2q(x[i]);
-      mass = wave_tree_sum(lane_tree_sum(ea));
-    }
-  }
+  for (int i = 0; i < NE; ++i) ea[i] = exp2q(x[i]);
+  mass = wave_tree_sum(lane_tree_sum(ea));
 
   // 7. the level L: candidates are the elements with RN32(x c - mref) >= -L,
   //    mref = max(mc, pmc)
@@ -569,19 +549,17 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   uint32_t cnt = 0;
   if (mref > -__builtin_inff()) {
     const float nref = -mref;
-    if constexpr (PEN) {
-      if (!same) {
-        // the penalised maximum lies above the rest (a penalty below 1, or
-        // no other finite logit): the exponents relative to mref
+    if (!same) {
+      // the penalised maximum lies above the rest (a penalty below 1, or
+      // no other finite logit): the exponents relative to mref
 #pragma unroll
-        for (int u = 0; u < NVC; ++u) {
+      for (int u = 0; u < NVC; ++u) {
 #pragma unroll
-          for (int e = 0; e < EPV; ++e) {
-            const int li = (u * kWave + t) * EPV + e;
-            float v = staged<DT>(st, li);
-            if (((hb[u] >> e) & 1u) || u * kWave + t >= nvc) v = -__builtin_inff();
-            x[u * EPV + e] = __builtin_fmaf(v, c, nref);
-          }
+        for (int e = 0; e < EPV; ++e) {
+          const int li = (u * kWave + t) * EPV + e;
+          float v = staged<DT>(st, li);
+          if (((hb[u] >> e) & 1u) || u * kWave + t >= nvc) v = -__builtin_inff();
+          x[u * EPV + e] = __builtin_fmaf(v, c, nref);
         }
       }
     }
@@ -617,13 +595,11 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
       cnt = static_cast<uint32_t>(__builtin_popcount(mask));
       uint32_t own = cnt;
       uint32_t pen_cnt = 0;
-      if constexpr (PEN) {
-        // the penalised candidates at this level count against the same slots
-        for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
-          const uint32_t h = h0 + t;
-          const float xp = h0 == 0 ? xp0 : (h < nh ? penalise(staged<DT>(st, hl[h]), p.pen) : -__builtin_inff());
-          pen_cnt += static_cast<uint32_t>(__builtin_popcountll(__ballot(h < nh && __builtin_fmaf(xp, c, nref) >= th)));
-        }
+      // the penalised candidates at this level count against the same slots
+      for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+        const uint32_t h = h0 + t;
+        const float xp = h0 == 0 ? xp0 : (h < nh ? penalise(staged<DT>(st, hl[h]), p.pen) : -__builtin_inff());
+        pen_cnt += static_cast<uint32_t>(__builtin_popcountll(__ballot(h < nh && __builtin_fmaf(xp, c, nref) >= th)));
       }
       const uint32_t tot = lane_bcast_u32(wave_scan_add_u32(own), kWave - 1) + pen_cnt;
       if (tot <= static_cast<uint32_t>(cap)) {
@@ -678,32 +654,30 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   const uint32_t nA_plain = nA;
   float pmass = 0.0f;
   bool overflow = L < 0 && mref > -__builtin_inff();
-  if constexpr (PEN) {
-    if (any_hit) {
-      // PM_j: hit h added by lane h mod 64 in hit order, then the lanes
-      // pairwise; the penalised candidates appended in hit order
-      const float npmc = -pmc;
-      const float nref = -mref;
-      const float th = -static_cast<float>(L);
-      float acc = 0.0f;
-      uint32_t nB = 0;
-      for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
-        const uint32_t h = h0 + t;
-        const bool in = h < nh;
-        const uint32_t li = in ? hl[h] : 0u;
-        const float xp = h0 == 0 ? xp0 : (in ? penalise(staged<DT>(st, li), p.pen) : -__builtin_inff());
-        if (in) acc = acc + exp2q(__builtin_fmaf(xp, c, npmc));
-        const bool cand = in && L >= 0 && __builtin_fmaf(xp, c, nref) >= th;
-        const uint64_t m = __ballot(cand);
-        const uint32_t q = nB + static_cast<uint32_t>(__builtin_popcountll(m & ((1ull << t) - 1ull)));
-        if (cand && nA + q < static_cast<uint32_t>(cap))
-          out[nA + q] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp);
-        nB += static_cast<uint32_t>(__builtin_popcountll(m));
-      }
-      pmass = wave_tree_sum(acc);
-      if (nA + nB > static_cast<uint32_t>(cap)) overflow = true;
-      nA += nB;
+  if (any_hit) {
+    // PM_j: hit h added by lane h mod 64 in hit order, then the lanes
+    // pairwise; the penalised candidates appended in hit order
+    const float npmc = -pmc;
+    const float nref = -mref;
+    const float th = -static_cast<float>(L);
+    float acc = 0.0f;
+    uint32_t nB = 0;
+    for (uint32_t h0 = 0; h0 < nh; h0 += kWave) {
+      const uint32_t h = h0 + t;
+      const bool in = h < nh;
+      const uint32_t li = in ? hl[h] : 0u;
+      const float xp = h0 == 0 ? xp0 : (in ? penalise(staged<DT>(st, li), p.pen) : -__builtin_inff());
+      if (in) acc = acc + exp2q(__builtin_fmaf(xp, c, npmc));
+      const bool cand = in && L >= 0 && __builtin_fmaf(xp, c, nref) >= th;
+      const uint64_t m = __ballot(cand);
+      const uint32_t q = nB + static_cast<uint32_t>(__builtin_popcountll(m & ((1ull << t) - 1ull)));
+      if (cand && nA + q < static_cast<uint32_t>(cap))
+        out[nA + q] = (static_cast<uint64_t>(c0 + li) << 32) | __float_as_uint(xp);
+      nB += static_cast<uint32_t>(__builtin_popcountll(m));
     }
+    pmass = wave_tree_sum(acc);
+    if (nA + nB > static_cast<uint32_t>(cap)) overflow = true;
+    nA += nB;
   }
 
   // 10. the row's draft token, processed
@@ -712,10 +686,8 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
   if (has_tok) {
     const int li = static_cast<int>(I.tok - c0);
     float xv = staged<DT>(st, li);
-    if constexpr (PEN) {
-      const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), li >> 5));
-      if ((word >> (li & 31)) & 1u) xv = penalise(xv, p.pen);
-    }
+    const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(pw), li >> 5));
+    if ((word >> (li & 31)) & 1u) xv = penalise(xv, p.pen);
     xtok = xv;
   }
 
@@ -733,8 +705,9 @@ __device__ __forceinline__ void stream_item(const Params& p, StreamSh<DT>& sh, i
 // The same item without a penalty, the chunk held in registers only (no LDS):
 // the raw logits stay in x[], the exponents are recomputed where they are
 // needed, and a candidate's value is selected among its vector's registers.
-// Same results as stream_item<DT, false>; at most 64 VGPRs, so eight waves
-// per SIMD fit where the staged form fits five.
+// Records and candidates as stream_item writes them for a row without
+// penalised tokens; at most 64 VGPRs, so eight waves per SIMD fit where a
+// staged form (32 KB of LDS per workgroup) fits five.
 template <int DT>
 __device__ __forceinline__ void stream_item_reg(const Params& p, const Item& I,
                                                 const u32x4 (&d)[Elem<DT>::kPerVec == 4 ? 8 : 4]) {
@@ -939,11 +912,11 @@ __device__ __forceinline__ void stream_item_reg(const Params& p, const Item& I,
 // stream_kernel: one (row, chunk) item per wave, four independent waves per
 // workgroup
 // ===========================================================================
-template <int DT, bool PEN>
+template <int DT>
 __global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
   constexpr int NVC = kChunk / (kWave * Elem<DT>::kPerVec);
   __shared__ StreamSh<DT> sh;
-  __shared__ uint16_t hits[PEN ? kNW : 1][PEN ? kChunk : 1];  // each wave's penalised elements
+  __shared__ uint16_t hits[kNW][kChunk];  // each wave's penalised elements
   // the wave's item, wave-uniform (its decomposition runs on the scalar unit)
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int it = static_cast<int>(blockIdx.x) * kNW + w;
@@ -952,7 +925,7 @@ __global__ __launch_bounds__(kWG) void stream_kernel(const Params p) {
   u32x4 d[NVC];
   uint32_t pw;
   load_item<DT, NVC>(p, I, d, pw);
-  stream_item<DT, PEN>(p, sh, w, I, d, pw, hits[PEN ? w : 0]);
+  stream_item<DT>(p, sh, w, I, d, pw, hits[w]);
 }
 
 // Without a penalty: the register-only item, eight waves per SIMD.
@@ -2337,7 +2310,7 @@ void launch_dt(const Params& p, hipStream_t st) {
   if (p.use_pen) hipLaunchKernelGGL(bitmap_kernel, dim3(static_cast<unsigned>(p.groups)), dim3(kBmB), 0, st, p);
   const dim3 sgrid(static_cast<unsigned>((p.items + kNW - 1) / kNW));
   if (p.use_pen) {
-    hipLaunchKernelGGL((stream_kernel<DT, true>), sgrid, dim3(kWG), 0, st, p);
+    hipLaunchKernelGGL((stream_kernel<DT>), sgrid, dim3(kWG), 0, st, p);
   } else {
     hipLaunchKernelGGL((stream_reg_kernel<DT>), sgrid, dim3(kWG), 0, st, p);
   }
