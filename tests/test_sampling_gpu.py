@@ -416,14 +416,16 @@ def test_spec_verify_alternating_shapes_share_workspace(gpu):
         assert np.array_equal(tok.cpu().numpy(), want.tokens), (b, k)
 
 
-@pytest.mark.parametrize("support", [300, 1000, 1900])
-def test_spec_verify_large_draft_supports(gpu, support):
+@pytest.mark.parametrize("support,batch", [(300, 3), (1000, 3), (1900, 3), (1000, 90)])
+def test_spec_verify_large_draft_supports(gpu, support, batch):
     """Rows whose top-p support is `support` near-equal tokens out of 65536
     (32 chunks, 2048 candidate slots). At 300 and 1000 every chunk's support
     fits its candidates (fast path, hundreds of residual terms); at 1900 some
     chunks hold more than 64 and the rows take the whole-row select, keeping
-    their support on the slots for the residual and bonus draws."""
-    vocab, batch, k = 65536, 3, 2
+    their support on the slots for the residual and bonus draws. At B=90 the
+    270 units outnumber the CUs: the two-workgroups-per-CU finaliser, whose
+    10-bit select digits meet buckets of near-equal p over several rounds."""
+    vocab, k = 65536, 2
     rng = np.random.default_rng(support)
     target = np.full((batch, k + 1, vocab), -30.0, dtype=np.float32)
     for b in range(batch):
@@ -436,7 +438,7 @@ def test_spec_verify_large_draft_supports(gpu, support):
            "uniforms": torch.from_numpy(philox.uniforms((batch, 2 * k + 1), seed=support)),
            "draft_uniforms": torch.from_numpy(philox.uniforms((batch, k), seed=support + 1))}
     drafts = draft_tokens_from(inp, cfg)
-    announce(f"spec large draft support {support}")
+    announce(f"spec large draft support {support} B={batch}")
     acc, tok = run_spec(cfg, inp, drafts, gpu)
     want = oracle_spec(cfg, inp, drafts)
     assert np.array_equal(acc, want.accept_len)
