@@ -252,6 +252,25 @@ def test_sample_logits_bitexact(gpu, dtype, vocab, temperature, top_p):
     assert got.cpu().tolist() == want
 
 
+def test_sample_and_filter_more_rows_than_cus(gpu):
+    """300 rows: more finaliser units than CUs, so the sample and filter
+    calls run the two-workgroups-per-CU build (10-bit select digits)."""
+    rows, vocab = 300, 8192
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(rows, vocab, generator=g) * 3
+    logits[::17, :64] = 4.0  # rows with a block of equal logits at the top
+    u = torch.from_numpy(philox.uniforms((rows,), seed=12))
+    announce(f"sample + filter {rows} rows V={vocab}")
+    got = verify.sample_logits(logits.to(gpu), u.to(gpu), 1.0, 0.8)
+    res = verify.filter_logits(logits.to(gpu), 1.0, 0.8, want_probs=False)
+    torch.cuda.synchronize()
+    for r in range(rows):
+        want = oracle_filter(logits[r].numpy(), 1.0, 0.8, epv=epv_of(torch.float32))
+        assert got[r].item() == osmp.categorical_pick(want.P, u[r].item()), r
+        assert np.array_equal(res["filtered"][r].cpu().numpy(), want.P), r
+        assert res["cutoff"][r].item() == want.cutoff, r
+
+
 def test_sample_logits_with_penalty(gpu):
     cfg = workloads.SamplingConfig("t", 6, 1, 32000, torch.bfloat16, 0.7, 0.9, penalty=1.1, target_std=4.0,
                                    hist_min=50, hist_max=400)
