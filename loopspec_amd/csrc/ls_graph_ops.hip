@@ -143,6 +143,60 @@ __device__ __forceinline__ void kv_row_need(const int32_t* accept_len, const int
   *fits = after <= max_pages;
 }
 
+// One row of the commit plan: its new pages from the free-page ring (at ring
+// position base + i), the checks, the page-table entries, the accepted
+// tokens' destination slots and the new context length.
+__device__ __forceinline__ void kv_plan_row(int64_t b, int64_t a, int64_t ctx, int64_t owned, int64_t need,
+                                            bool fits, bool enough, int64_t take, int64_t base, int k,
+                                            int page_size, int64_t max_pages, int64_t num_pages,
+                                            int32_t* __restrict__ page_table, int64_t* __restrict__ ctx_len,
+                                            const int64_t* __restrict__ free_pages, int64_t ring,
+                                            int64_t* __restrict__ dst_slots, int32_t* status) {
+  int32_t* pt = page_table + b * max_pages;
+  int32_t bits = 0;
+  bool bad = false;
+  if (!fits) {
+    bad = true;
+    bits |= 1;
+  } else if (need > 0 && !enough) {
+    bad = true;
+    bits |= 2;
+  }
+  auto ring_page = [&](int64_t i) -> int64_t {
+    int64_t ro = (base + i) % ring;
+    ro += ro < 0 ? ring : 0;
+    return free_pages[ro];
+  };
+  if (!bad) {
+    // every page the accepted tokens land on must lie in the pool
+    for (int64_t i = 0; i < take; ++i) {
+      const int64_t page = ring_page(i);
+      if (page < 0 || page >= num_pages) bad = true;
+    }
+    for (int j = 0; j < a; ++j) {
+      const int64_t pidx = (ctx + j) / page_size;
+      if (pidx < owned) {
+        const int64_t page = pt[pidx];
+        if (page < 0 || page >= num_pages) bad = true;
+      }
+    }
+    if (bad) bits |= 1;
+  }
+  if (!bad) {
+    for (int64_t i = 0; i < take; ++i) pt[owned + i] = static_cast<int32_t>(ring_page(i));
+  }
+  for (int j = 0; j < k; ++j) {
+    int64_t slot = -1;
+    if (!bad && j < a) {
+      const int64_t pos = ctx + j;
+      slot = static_cast<int64_t>(pt[pos / page_size]) * page_size + pos % page_size;
+    }
+    dst_slots[b * k + j] = slot;
+  }
+  if (!bad) ctx_len[b] = ctx + a;
+  if (bits && status) atomicOr(status, bits);
+}
+
 __global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
     const int32_t* __restrict__ accept_len, int64_t batch, int k, int page_size, int64_t max_pages,
     int64_t num_pages, int32_t* __restrict__ page_table, int64_t* __restrict__ ctx_len,
@@ -150,6 +204,23 @@ __global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
     int32_t* status) {
   __shared__ uint32_t red[kScanBlock / kWave];
   const int64_t next = page_state[0], end = page_state[1];
+  if (batch <= kScanBlock) {
+    // one row per thread: one scan serves both passes (with enough pages the
+    // rows take what they need, at the same prefixes; without, none takes any)
+    const int64_t b = threadIdx.x;
+    int64_t a = 0, ctx = 0, owned = 0, need = 0;
+    bool fits = true;
+    if (b < batch) kv_row_need(accept_len, ctx_len, b, k, page_size, max_pages, &a, &ctx, &owned, &need, &fits);
+    uint32_t total;
+    const uint32_t excl = block_excl_scan_u32(static_cast<uint32_t>(fits ? need : 0), red, &total);
+    const bool enough = next + total <= end;
+    if (b < batch)
+      kv_plan_row(b, a, ctx, owned, need, fits, enough, (fits && enough) ? need : 0, next + (enough ? excl : 0), k,
+                  page_size, max_pages, num_pages, page_table, ctx_len, free_pages, ring, dst_slots, status);
+    __syncthreads();
+    if (threadIdx.x == 0) page_state[0] = next + (enough ? total : 0);
+    return;
+  }
   // pass 1: pages wanted by the rows that fit their page table
   int64_t wanted = 0;
   for (int64_t b0 = 0; b0 < batch; b0 += kScanBlock) {
@@ -172,51 +243,9 @@ __global__ __launch_bounds__(kScanBlock) void kv_plan_kernel(
     const int64_t take = (fits && enough) ? need : 0;
     uint32_t total;
     const uint32_t excl = block_excl_scan_u32(static_cast<uint32_t>(take), red, &total);
-    if (b < batch) {
-      int32_t* pt = page_table + b * max_pages;
-      int32_t bits = 0;
-      bool bad = false;
-      if (!fits) {
-        bad = true;
-        bits |= 1;
-      } else if (need > 0 && !enough) {
-        bad = true;
-        bits |= 2;
-      }
-      auto ring_page = [&](int64_t i) -> int64_t {
-        int64_t ro = (next + carry + excl + i) % ring;
-        ro += ro < 0 ? ring : 0;
-        return free_pages[ro];
-      };
-      if (!bad) {
-        // every page the accepted tokens land on must lie in the pool
-        for (int64_t i = 0; i < take; ++i) {
-          const int64_t page = ring_page(i);
-          if (page < 0 || page >= num_pages) bad = true;
-        }
-        for (int j = 0; j < a; ++j) {
-          const int64_t pidx = (ctx + j) / page_size;
-          if (pidx < owned) {
-            const int64_t page = pt[pidx];
-            if (page < 0 || page >= num_pages) bad = true;
-          }
-        }
-        if (bad) bits |= 1;
-      }
-      if (!bad) {
-        for (int64_t i = 0; i < take; ++i) pt[owned + i] = static_cast<int32_t>(ring_page(i));
-      }
-      for (int j = 0; j < k; ++j) {
-        int64_t slot = -1;
-        if (!bad && j < a) {
-          const int64_t pos = ctx + j;
-          slot = static_cast<int64_t>(pt[pos / page_size]) * page_size + pos % page_size;
-        }
-        dst_slots[b * k + j] = slot;
-      }
-      if (!bad) ctx_len[b] = ctx + a;
-      if (bits && status) atomicOr(status, bits);
-    }
+    if (b < batch)
+      kv_plan_row(b, a, ctx, owned, need, fits, enough, take, next + carry + excl, k, page_size, max_pages,
+                  num_pages, page_table, ctx_len, free_pages, ring, dst_slots, status);
     carry += total;
   }
   __syncthreads();

@@ -174,6 +174,39 @@ def test_kv_commit_reports_overflow(gpu):
     assert state.cpu().tolist() == [1, 2]
 
 
+@pytest.mark.parametrize("short", [False, True])
+def test_kv_commit_plan_many_rows(gpu, short):
+    """2500 rows: more than one plan workgroup's worth, so the plan takes its
+    two passes (needs, then allocation) over row blocks; with a short ring
+    nothing is allocated. Plan only (no KV planes), against the oracle."""
+    rng = np.random.default_rng(2500 + short)
+    B, k, ps, max_pages = 2500, 3, 4, 8
+    ctx = rng.integers(0, 20, size=B).astype(np.int64)
+    acc = rng.integers(0, k + 1, size=B).astype(np.int32)
+    owned = [-(-int(c) // ps) for c in ctx]
+    pt = np.full((B, max_pages), -1, dtype=np.int32)
+    used = 0
+    for b in range(B):
+        pt[b, :owned[b]] = used + np.arange(owned[b])
+        used += owned[b]
+    num_pages = used + 4 * B + 64
+    ring = (used + rng.permutation(num_pages - used)).astype(np.int64)
+    branch = (num_pages * ps + np.arange(B * k, dtype=np.int64)).reshape(B, k)
+    state = (5, 5 + (10 if short else len(ring)))
+    want = og.kv_commit_plan(acc, branch, pt, ctx, ring, state, ps, num_pages)
+    t = {n: torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for n, a in
+         (("acc", acc), ("branch", branch), ("pt", pt), ("ctx", ctx), ("ring", ring))}
+    t_state = torch.tensor(state, dtype=torch.int64, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    announce(f"kv_commit plan B={B} short={short}")
+    dst = go.commit_kv(None, t["acc"], t["branch"], t["pt"], t["ctx"], t["ring"], t_state, ps, status=status)
+    assert np.array_equal(dst.cpu().numpy(), want[0])
+    assert np.array_equal(t["pt"].cpu().numpy(), want[1])
+    assert np.array_equal(t["ctx"].cpu().numpy(), want[2])
+    assert tuple(t_state.cpu().tolist()) == want[3]
+    assert status.item() == want[4]
+
+
 @pytest.mark.parametrize("avail", [0, 2, 3, 6])
 def test_kv_commit_ring_exhaustion(gpu, avail):
     """When the rows want more pages than the ring holds, nothing is allocated:
