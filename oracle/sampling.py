@@ -23,7 +23,10 @@ function:
   rejects repetition_penalty != 1, server/loopspec_scheduler.py:141-148).
 - top_k cutoff: only the joint top-k/top-p rule of distributions.py:72-86 is
   the reference's own; the top-k-only path calls sgl_kernel.top_k_renorm_prob
-  (absent) -- parity unpinned for that path.
+  (absent). Its support is pinned to the k largest for distinct values and
+  its weights to the renormalised p (tests/test_oracle_sampling.py); ties at
+  the k-th value are kept by this build's convention, and parity with
+  top_k_renorm_prob on ties stays unpinned.
 """
 
 from __future__ import annotations

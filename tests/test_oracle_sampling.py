@@ -267,6 +267,27 @@ def test_joint_top_k_top_p_matches_torch_reference():
         assert np.max(np.abs(got[nz] - ref[nz]) / ref[nz]) < 2e-6
 
 
+def test_top_k_only_keeps_the_k_largest():
+    """top-k without top-p: with distinct logits the support is exactly the k
+    largest (argsort), and the kept mass renormalised; a value tied at the
+    k-th keeps every tied token (the ties-kept convention of the top-p rule)."""
+    rng = np.random.default_rng(6)
+    for v, k in [(4096, 1), (4096, 7), (8192, 100), (1000, 999)]:
+        x = rng.permutation(v).astype(np.float32) * np.float32(0.01)  # distinct logits
+        row = os_.filter_row(x, 1.0, k)
+        want = np.zeros(v, dtype=bool)
+        want[np.argsort(-x)[:k]] = True
+        assert np.array_equal(row.P > 0, want), (v, k)
+        kept = row.soft.p[want].astype(np.float64)
+        assert abs(row.P[want].astype(np.float64).sum() - 1.0) < 1e-5
+        assert np.allclose(row.P[want], kept / kept.sum(), rtol=1e-6, atol=0)
+    x = rng.normal(size=512).astype(np.float32)
+    top = np.argsort(-x)
+    x[top[5]] = x[top[4]]  # the 5th and 6th largest tie
+    row = os_.filter_row(x, 1.0, 5)
+    assert (row.P > 0).sum() == 6 and row.P[top[4]] == row.P[top[5]] > 0
+
+
 def test_categorical_pick_matches_torch_reference():
     g = torch.Generator().manual_seed(5)
     probs = torch.softmax(torch.randn(64, 5000, generator=g) * 2, -1)
