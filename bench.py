@@ -330,7 +330,8 @@ def bench_spec(cfg, steps: int, warmup: int, device: torch.device, nsets: int) -
                    "temperature": cfg.temperature, "top_p": cfg.top_p, "penalty": cfg.penalty,
                    "input_sets": nsets, "input_set_bytes": nbytes,
                    "kernels": ("ls::bitmap_kernel + ls::stream_kernel<DT>" if cfg.penalty != 1.0
-                               else "ls::stream_reg_kernel<DT>") + " + ls::fin_kernel<DT>",
+                               else "ls::stream_reg_kernel<DT>")
+                   + (" + ls::fin2_kernel<DT>" if cfg.batch * (cfg.k + 1) > 256 else " + ls::fin_kernel<DT>"),
                    "submission": "hipGraph of one ls_spec_verify call (%d launches) per step"
                    % (3 if cfg.penalty != 1.0 else 2)},
         "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
@@ -429,7 +430,7 @@ def bench_c5(steps: int, warmup: int, device: torch.device, nsets: int) -> dict:
                    "vocab": cfg.vocab, "temperature": cfg.temperature, "top_p": cfg.top_p,
                    "kv_planes": kvc.planes, "kv_token_bytes": kvc.token_bytes, "page_size": kvc.page_size,
                    "input_sets": nsets, "logit_bytes": logit_bytes, "kv_commit_bytes": kv_bytes,
-                   "kernels": "ls::stream_reg_kernel<DT> + ls::fin_kernel<DT> + kv_plan_kernel + kv_copy_kernel",
+                   "kernels": "ls::stream_reg_kernel<DT> + ls::fin2_kernel<DT> + kv_plan_kernel + kv_copy_kernel",
                    "submission": "hipGraph of four launches per step"},
         "tokens_per_s": (accepted + cfg.batch) / (ms_per_step * 1e-3),
         "acceptance_rate": accepted / (cfg.batch * cfg.k),
